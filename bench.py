@@ -1,0 +1,233 @@
+"""Benchmark of the MoE SwiGLU layer on one MI355X (the metric and configs of BASELINE.json).
+
+A step is one pass of the layer over one batch of seeded synthetic tokens, inputs resident in HBM:
+  c5 (default)  training step at the C3 shape: forward + backward (16384 tokens, d=1536, 16 experts, top-2, h=4096)
+  c3            forward only at the same shape
+  c4            forward only, Zipf(1.2)-biased router logits, 2 experts never routed
+  c2            forward only, 2048 tokens, d=1024, 8 experts, top-2, h=2048
+value = algorithmic grouped-GEMM TFLOP/s of the layer step (routed rows only: 6*M*d*h forward, 18*M*d*h forward +
+backward) / measured step time; ms_per_step is the layer time.  One JSON line is printed.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/clk/CU
+PEAK_HBM_GBS = 8000.0
+METRIC = "MoE layer µs + grouped-GEMM TFLOP/s (% bf16 MFMA peak) at 16k tokens, 1 GPU"
+
+WORKLOADS = {
+    "c2": dict(T=2048, d=1024, E=8, k=2, h=2048, backward=False, zipf=False,
+               desc="C2: MoE layer forward, 8 images x 256 tokens = 2048 tokens, d_model=1024, 8 experts, top-2, "
+                    "SwiGLU hidden=2048"),
+    "c3": dict(T=16384, d=1536, E=16, k=2, h=4096, backward=False, zipf=False,
+               desc="C3: MoE layer forward, 4 images x 4096 tokens = 16384 tokens, d_model=1536, 16 experts, top-2, "
+                    "SwiGLU hidden=4096"),
+    "c4": dict(T=16384, d=1536, E=16, k=2, h=4096, backward=False, zipf=True,
+               desc="C4: MoE layer forward, 16384 packed tokens, d_model=1536, 16 experts, top-2, SwiGLU hidden=4096, "
+                    "Zipf(1.2) expert bias with 2 experts never routed"),
+    "c5": dict(T=16384, d=1536, E=16, k=2, h=4096, backward=True, zipf=False,
+               desc="C5: MoE layer training step (forward + backward) at the C3 shape: 16384 tokens, d_model=1536, "
+                    "16 experts, top-2, SwiGLU hidden=4096"),
+}
+
+
+def gemm_flops(w):
+    M = w["T"] * w["k"]
+    return (18 if w["backward"] else 6) * M * w["d"] * w["h"]
+
+
+def zipf_bias(E, seed=0, s=1.2, n_empty=2):
+    """Per-expert logit bias: a seeded permutation of the experts; rank r (1-based) gets -s*ln(r), the last n_empty
+    get -inf (never routed)."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    perm = rng.permutation(E)
+    b = np.empty(E, np.float32)
+    for r, e in enumerate(perm):
+        b[e] = -np.inf if r >= E - n_empty else np.float32(-s * np.log(r + 1.0))
+    return b
+
+
+def run_gpu(w, steps, warmup, probe_kernel="gate_up_swiglu"):
+    import torch
+
+    from trenowanie_generatora_obrazkow_amd import moe_swiglu, ops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    g = torch.Generator().manual_seed(0)
+    T, d, E, h, k = w["T"], w["d"], w["E"], w["h"], w["k"]
+    x = torch.randn(T, d, generator=g).bfloat16().to(dev)
+    wr = (torch.randn(E, d, generator=g) * 0.02).bfloat16().to(dev)
+    wgu = (torch.randn(E, d, 2 * h, generator=g) * 0.02).bfloat16().to(dev)
+    wd = (torch.randn(E, h, d, generator=g) * 0.02).bfloat16().to(dev)
+    dout = torch.randn(T, d, generator=g).bfloat16().to(dev)
+    bias = torch.zeros(E, dtype=torch.float32)
+    if w["zipf"]:
+        bias = torch.from_numpy(zipf_bias(E, seed=0))
+    bias = bias.to(dev)
+    if w["backward"]:
+        for t in (x, wr, wgu, wd):
+            t.requires_grad_(True)
+
+    def step():
+        if w["backward"]:
+            for t in (x, wr, wgu, wd):
+                t.grad = None
+            out, _, _ = moe_swiglu(x, wr, wgu, wd, k, logit_bias=bias)
+            out.backward(dout)
+        else:
+            with torch.no_grad():
+                moe_swiglu(x, wr, wgu, wd, k, logit_bias=bias)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    # timed region: exactly `steps` steps, events around the dominant kernel on its launch stream
+    ops.probe = {probe_kernel: []}
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    dom = [a.elapsed_time(b) for a, b in ops.probe[probe_kernel]]
+    ops.probe = None
+    ms = (t1 - t0) * 1e3 / steps
+
+    # per-kernel breakdown: a second pass with events around every op (reported, not the headline)
+    names = ["route_topk", "dispatch", "gate_up_swiglu", "down_scatter", "combine", "combine_bwd",
+             "down_dgrad_swiglu", "grouped_wgrad", "gate_up_dgrad", "router_bwd", "unpermute_bwd"]
+    ops.probe = {n: [] for n in names}
+    nb = max(3, min(steps, 10))
+    for _ in range(nb):
+        step()
+    torch.cuda.synchronize()
+    kern = {}
+    for n in names:
+        ts = [a.elapsed_time(b) * 1e3 for a, b in ops.probe[n]]
+        if not ts:
+            continue
+        if n == "grouped_wgrad":  # two calls per step: down (first) then gate/up
+            kern["wgrad_down"] = statistics.median(ts[0::2])
+            kern["wgrad_gate_up"] = statistics.median(ts[1::2])
+        else:
+            kern[n] = statistics.median(ts)
+    ops.probe = None
+    return ms, statistics.mean(dom), kern
+
+
+def cpu_baseline(w, budget_s=15.0):
+    """The reference's PyTorch CPU path (oracle/cpu_path.py: router + _fused_moe_infer's `grouped` branch, autograd
+    for the backward) on a bounded sample of the same workload: the full d, E, k, h with fewer tokens."""
+    import torch
+
+    from oracle import cpu_path
+
+    threads = torch.get_num_threads()
+    T = 512
+    d, E, h, k = w["d"], w["E"], w["h"], w["k"]
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(T, d, generator=g).bfloat16()
+    wr = (torch.randn(E, d, generator=g) * 0.02).bfloat16()
+    wgu = (torch.randn(E, d, 2 * h, generator=g) * 0.02).bfloat16()
+    wd = (torch.randn(E, h, d, generator=g) * 0.02).bfloat16()
+    dout = torch.randn(T, d, generator=g).bfloat16()
+    bias = torch.from_numpy(zipf_bias(E, seed=0)) if w["zipf"] else None
+
+    def step():
+        if w["backward"]:
+            ts = [t.clone().requires_grad_(True) for t in (x, wr, wgu, wd)]
+            cpu_path.training_step(*ts, k, dout, bias=bias)
+        else:
+            with torch.no_grad():
+                cpu_path.layer_forward(x, wr, wgu, wd, k, bias=bias)
+
+    t0 = time.perf_counter()
+    step()
+    one = time.perf_counter() - t0
+    reps = int(max(3, min(10, budget_s / max(one, 1e-3))))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    flops = (18 if w["backward"] else 6) * T * k * d * h
+    return {"value": flops / med / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{T} tokens of the same layer shape (d={d}, E={E}, top-{k}, h={h}), bf16, torch CPU "
+                      f"{'forward+backward' if w['backward'] else 'forward'}; median of {reps} runs after 1 warm-up; "
+                      f"{med * 1e3:.1f} ms per sample step"}
+
+
+def load_traffic(workload):
+    p = os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
+    if os.path.exists(p):
+        with open(p) as f:
+            return json.load(f)
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="c5", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); the MoE layer has no "
+              f"multi-GPU path here", file=sys.stderr)
+        sys.exit(2)
+    w = WORKLOADS[args.workload]
+    ms, dom_ms, kern = run_gpu(w, args.steps, args.warmup)
+    flops = gemm_flops(w)
+    tflops = flops / (ms * 1e-3) / 1e12
+    M = w["T"] * w["k"]
+    dom_flops = 4 * M * w["d"] * w["h"]  # gate/up: 2 * M * d * (2h)
+    dom_tflops = dom_flops / (dom_ms * 1e-3) / 1e12
+    traffic = load_traffic(args.workload)
+    res = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) tokens and upstream gradient, N(0,0.02) router and expert weights "
+                "(torch CPU generator, seed 0, fp32 then bf16)",
+        "config": {"workload": w["desc"], "tokens": w["T"], "d_model": w["d"], "experts": w["E"], "top_k": w["k"],
+                   "hidden": w["h"], "pass": "forward+backward" if w["backward"] else "forward"},
+        "layer_us": round(ms * 1e3, 1),
+        "pct_bf16_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2),
+        "gemm_flops_per_step": flops,
+        "roofline": {"bound": "mfma", "kernel": "hmoe gate/up grouped GEMM + fused SwiGLU (grouped_gemm_kernel, "
+                                                "EPI_SWIGLU)",
+                     "achieved": round(dom_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(dom_tflops / PEAK_BF16_TFLOPS, 4),
+                     "flops_per_launch": dom_flops, "avg_launch_us": round(dom_ms * 1e3, 2),
+                     "traffic": traffic.get("bytes_per_launch") if traffic else None},
+        "kernels_us": {k_: round(v, 1) for k_, v in kern.items()},
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(w)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

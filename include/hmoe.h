@@ -1,0 +1,171 @@
+/*
+ * hmoe: C ABI of the MI355X-native (gfx950) mixture-of-experts SwiGLU layer.
+ *
+ * Every entry point takes device pointers, sizes and a HIP stream (as void*), is asynchronous on that stream,
+ * never synchronises the device, never reads data back to the host and never allocates: the caller allocates
+ * outputs and any workspace (sized by the matching *_workspace_size query).  Return value 0 = success, negative =
+ * an HMOE_ERR_* code (hmoe_error_string gives the text).  Element types are passed as HMOE_DT_* codes.
+ *
+ * Conventions shared with the reference (adamo1139/trenowanie_generatora_obrazkow):
+ *   - flat routed row f = token * k + slot (topk_ids.reshape(-1), aurora/hf_compat.py:70);
+ *   - sorted row r: rows grouped by expert in expert order, stable in f (argsort(stable=True), :71);
+ *     order[r] = f, a_idx[r] = f / k, y_idx[r] = f (:78), inv_pos[f] = r;
+ *   - stacked expert weights wgu (E, d, 2h) = [gate | up] and wd (E, h, d), N contiguous (:154-155);
+ *   - bf16 storage, fp32 accumulation, one rounding on store; the routing weight is rounded to bf16 before use
+ *     (:80) and applied to the fp32 accumulator (aurora/moe_triton.py:52-56).
+ * Row offsets are 64-bit.  Index arrays (a_idx, y_idx, ...) are trusted to be in range.
+ */
+#ifndef HMOE_H_
+#define HMOE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HMOE_ABI_VERSION 1
+
+#define HMOE_OK 0
+#define HMOE_ERR_ARG (-1)       /* null pointer, negative size, misaligned pointer or leading dimension */
+#define HMOE_ERR_SHAPE (-2)     /* shape the kernels do not support (e.g. K or N not a multiple of 8) */
+#define HMOE_ERR_DTYPE (-3)     /* element type not supported for this argument */
+#define HMOE_ERR_LAUNCH (-4)    /* hipGetLastError reported a launch failure */
+#define HMOE_ERR_WORKSPACE (-5) /* workspace missing or smaller than the *_workspace_size query */
+#define HMOE_ERR_DEVICE (-6)    /* device query failed */
+
+#define HMOE_DT_BF16 0
+#define HMOE_DT_F16 1
+#define HMOE_DT_F32 2
+#define HMOE_DT_I32 3
+#define HMOE_DT_I64 4
+#define HMOE_DT_I8 5
+
+typedef void* hmoe_stream_t; /* a hipStream_t (0 = the null stream) */
+
+int hmoe_abi_version(void);
+const char* hmoe_error_string(int code);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Routing
+ * ------------------------------------------------------------------------------------------------------------- */
+
+/* Softmax top-k router.  No counterpart in the reference's own code: its production gate is remote HF code
+ * (aurora/hf_compat.py:49-51); conventions follow aurora/hf_pipeline.py:352-359 (fp32 logits of
+ * F.linear(x.float(), W.float()), top-k, w / (sum + 1e-20) * scaling).
+ * x (T, d) bf16 with row stride ldx, wr (E, d) bf16, bias (E,) fp32 or NULL.  Outputs topk_ids (T, k) int32 and
+ * topk_w (T, k) fp32 (slots in descending order, ties to the lower expert), logits (T, E) fp32 (NULL to skip).
+ * The dot products use a fixed, documented reduction order (64 lane partials over 8-element groups, xor
+ * butterfly), so ids, weights and logits are bit-reproducible by a host restatement.  d % 8 == 0, E <= 256,
+ * k <= 16. */
+int hmoe_route_topk(const void* x, int64_t ldx, const void* wr, const float* bias, int64_t T, int64_t d, int E,
+                    int k, int renorm, float scaling, float* logits, int32_t* topk_ids, float* topk_w,
+                    hmoe_stream_t stream);
+
+/* Workspace bytes for hmoe_dispatch. */
+size_t hmoe_dispatch_workspace_size(int64_t T, int k, int E);
+
+/* Token dispatch: replaces aurora/hf_compat.py:69-72 (flat ids, stable argsort, bincount), :78 (a_idx, y_idx),
+ * :80 (routing weight in sorted order, rounded to bf16) and the row gather x[order // k] of :83.
+ * topk_ids (T, k) int32 or int64 (ids_dtype), topk_w (T, k) fp32 or bf16 (w_dtype; NULL to skip w_sorted).
+ * Outputs (NULL skips an optional one): counts (E,) int32 [required], counts64 (E,) int64, starts (E+1,) int32
+ * [required; starts[e] = first sorted row of expert e], order (M,) int32 (= y_idx), a_idx (M,) int32,
+ * inv_pos (M,) int32, w_sorted (M,) bf16, xs (M, d) bf16 = x[a_idx] (needs x (T, d) bf16 with row stride ldx).
+ * Expert ids outside [0, E) are counted nowhere and make the rows they own undefined; the caller validates ids.
+ * E <= 1024. */
+int hmoe_dispatch(const void* topk_ids, int ids_dtype, const void* topk_w, int w_dtype, int64_t T, int k, int E,
+                  const void* x, int64_t ldx, int64_t d, void* xs, int32_t* counts, int64_t* counts64,
+                  int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos, uint16_t* w_sorted,
+                  void* workspace, size_t workspace_bytes, hmoe_stream_t stream);
+
+/* make_schedule: replaces aurora/moe_triton.py:93-107.  For each of the ceil(M / block_m) + E blocks: the expert
+ * (or -1), the first sorted row and the end row of that expert, int32, computed on the device from counts
+ * (int32 or int64).  E <= 1024. */
+int hmoe_make_schedule(const void* counts, int counts_dtype, int E, int64_t M, int block_m, int32_t* block_e,
+                       int32_t* block_row, int32_t* row_end, hmoe_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Grouped GEMMs (bf16 MFMA, fp32 accumulation, persistent tile scheduler over ragged expert groups)
+ * ------------------------------------------------------------------------------------------------------------- */
+
+/* grouped_mm: replaces aurora/moe_triton.py:65-90 (_grouped_kernel :22-56).
+ * y[y_idx[r] or r, :] = bf16((a[a_idx[r] or r, :] @ w[e(r)]) * w_scale[e, :] * scale[r]) for the M sorted rows r,
+ * e(r) the expert owning row r under counts.  a bf16 (rows of lda elements), w (E, K, N) bf16 with element
+ * strides (stride_we, stride_wk, 1), scale (M,) bf16 or fp32 or NULL, w_scale: must be NULL (int8 weights are not
+ * supported yet: HMOE_ERR_DTYPE), y bf16 with row stride ldy.  K % 8 == 0, N % 8 == 0, lda/ldy/stride_wk % 8 == 0.
+ * Rows of y not named by the schedule are not written. */
+int hmoe_grouped_mm(const void* a, int64_t lda, int a_dtype, const void* w, int w_dtype, int64_t E, int64_t K,
+                    int64_t N, int64_t stride_we, int64_t stride_wk, const void* counts, int counts_dtype, int64_t M,
+                    const int32_t* a_idx, const int32_t* y_idx, const void* scale, int scale_dtype,
+                    const void* w_scale, int w_scale_dtype, void* y, int64_t ldy, hmoe_stream_t stream);
+
+/* Gate/up projection with the SwiGLU fused into the epilogue: replaces aurora/hf_compat.py:79 (grouped_mm(x,
+ * _wgu, counts, sched, a_idx=a_idx).chunk(2)) and the self._act(g) * u of :81.
+ * A rows: xs (M, d) in sorted order (a_idx NULL) or x (T, d) gathered through a_idx.  wgu (E, d, 2h) bf16.
+ * act (M, h) bf16 = bf16(bf16(silu(g)) * u) with g, u the bf16-rounded gate / up outputs; gu (M, 2h) bf16 =
+ * [g | u] when not NULL (kept for the backward).  d % 8 == 0, h % 8 == 0. */
+int hmoe_gate_up_swiglu(const void* x, int64_t ldx, const int32_t* a_idx, const void* wgu, int64_t E, int64_t d,
+                        int64_t h, const void* counts, int counts_dtype, int64_t M, void* act, void* gu,
+                        hmoe_stream_t stream);
+
+/* Down projection with routing weight and scatter: replaces aurora/hf_compat.py:80-81 (grouped_mm(act, _wd,
+ * counts, sched, y_idx=y_idx, scale=w)).  y[y_idx[r]] = bf16(fp32(act[r] @ wd[e]) * w_sorted[r]); yhat (M, d) bf16
+ * = bf16(act[r] @ wd[e]) in sorted order when not NULL (kept for the backward). */
+int hmoe_down_scatter(const void* act, const void* wd, int64_t E, int64_t h, int64_t d, const void* counts,
+                      int counts_dtype, int64_t M, const uint16_t* w_sorted, const int32_t* y_idx, void* y,
+                      void* yhat, hmoe_stream_t stream);
+
+/* Combine: replaces aurora/hf_compat.py:82 (y.view(n, k, -1).sum(1)): out[t] = bf16(sum_j fp32(y[t*k + j])). */
+int hmoe_combine(const void* y, int64_t T, int k, int64_t d, void* out, hmoe_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Backward.  The reference has no backward for this path (aurora/hf_compat.py:62 is @torch.no_grad); each entry
+ * point below differentiates the forward line it names.
+ * ------------------------------------------------------------------------------------------------------------- */
+
+/* Backward of :80-82 (weight multiply + combine).  For each sorted row r (token t = a_idx[r], flat f = order[r]):
+ * dys[r] = bf16(w_sorted[r] * dout[t]) (M, d) and dtopk_w[f] = <dout[t], yhat[r]> (fp32, fixed order). */
+int hmoe_combine_bwd(const void* dout, const void* yhat, const int32_t* order, const int32_t* a_idx,
+                     const uint16_t* w_sorted, int64_t M, int k, int64_t d, void* dys, float* dtopk_w,
+                     hmoe_stream_t stream);
+
+/* Backward of :81 through the down projection and the SwiGLU: dact[r] = w_sorted[r] * (dy[a_idx[r]] @ wd[e]^T)
+ * (fp32; a_idx NULL: dy holds the sorted rows (M, d); w_sorted NULL: no scale), then
+ * dgu[r] = [bf16(dact * u * silu'(g)) | bf16(dact * silu(g))] with [g | u] = gu[r].  dy is the upstream gradient of
+ * the combined output (T, d) bf16: the routing weight enters in fp32, not through a rounded copy. */
+int hmoe_down_dgrad_swiglu(const void* dy, const int32_t* a_idx, const uint16_t* w_sorted, const void* wd,
+                           int64_t E, int64_t h, int64_t d, const void* counts, int counts_dtype, int64_t M,
+                           const void* gu, void* dgu, hmoe_stream_t stream);
+
+/* Backward of :79 to the sorted input rows: dxs[r] = dgu[r] @ wgu[e]^T, stored bf16 or fp32 (dxs_dtype). */
+int hmoe_gate_up_dgrad(const void* dgu, const void* wgu, int64_t E, int64_t d, int64_t h, const void* counts,
+                       int counts_dtype, int64_t M, void* dxs, int dxs_dtype, hmoe_stream_t stream);
+
+/* Weight gradients of :79 and :81: dw[e] = a[rows of e]^T @ b[rows of e] (fp32 accumulation over the expert's
+ * ragged row range, no split, deterministic); a (M, P) row stride lda, b (M, N) row stride ldb, both bf16 in
+ * sorted order; dw (E, P, N) fp32 or bf16 (dw_dtype).  Experts with no rows get zeros.  P, N % 8 == 0. */
+int hmoe_grouped_wgrad(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t E, int64_t P, int64_t N,
+                       const void* counts, int counts_dtype, int64_t M, void* dw, int dw_dtype,
+                       hmoe_stream_t stream);
+
+/* Workspace bytes for hmoe_router_bwd. */
+size_t hmoe_router_bwd_workspace_size(int64_t T, int E, int64_t d);
+
+/* Router backward (softmax -> top-k gather -> renormalise, as in hmoe_route_topk): dlogits (T, E) fp32 from
+ * dtopk_w (T, k) fp32, and dwr (E, d) = dlogits^T @ x (fp32 or bf16 per dwr_dtype; fixed-order reduction). */
+int hmoe_router_bwd(const float* logits, const int32_t* topk_ids, const float* dtopk_w, int64_t T, int E, int k,
+                    int renorm, float scaling, const void* x, int64_t ldx, int64_t d, float* dlogits, void* dwr,
+                    int dwr_dtype, void* workspace, size_t workspace_bytes, hmoe_stream_t stream);
+
+/* Input gradient: backward of the gather x[order // k] (:83 / a_idx of :78) plus the router's x.float() @ wr^T:
+ * dx[t] = bf16(sum_j dxs[inv_pos[t*k + j]] + sum_e dlogits[t, e] * wr[e]) in fp32 (dlogits NULL: expert part
+ * only); dxs (M, d) bf16 or fp32 (dxs_dtype). */
+int hmoe_unpermute_bwd(const void* dxs, int dxs_dtype, const int32_t* inv_pos, const float* dlogits, const void* wr,
+                       int64_t T, int k, int64_t d, int E, void* dx, hmoe_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HMOE_H_ */

@@ -1,0 +1,364 @@
+"""TEST INFRASTRUCTURE ONLY -- CPU oracle for the MoE SwiGLU layer.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and only as the checker:
+the product package (trenowanie_generatora_obrazkow_amd) never imports it and has no CPU fallback.
+
+A numpy restatement (float64 arithmetic, with the reference's bf16 rounding points) of the path served by
+aurora/moe_triton.py and aurora/hf_compat.py in the reference.  The router and the exact counting sort live in the C
+half of the oracle (oracle/router.c), loaded here through ctypes.
+
+Pinning (what each function is checked against, in tests/test_oracle.py):
+  route / topk_from_logits   C restatement; ids vs torch.softmax + torch.topk on the same logits, logits vs
+                             float64 matmul, hexp vs math.exp (ulp bound), brute force on tiny inputs, ties, -inf bias
+  dispatch                   numpy stable argsort vs the C counting sort vs torch.argsort(stable=True)/bincount, plus
+                             invariants (permutation, sortedness, stability)
+  make_schedule              numpy restatement vs the C block-by-block restatement vs brute-force coverage
+  grouped_mm                 per-expert float64 matmul of the reference's _self_test construction
+                             (aurora/hf_compat.py:112-121) and torch._grouped_mm on CPU; bf16 rounding bracket
+  moe_forward                per-token loop (pure Python) on tiny shapes; rounding points of the Triton path
+  moe_backward               torch float64 autograd of the forward and central finite differences on tiny shapes
+  router_backward            torch float64 autograd of softmax -> gather -> renormalise
+  quant_int8                 closed form: |q| <= 127, dequantised error <= scale / 2
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "liborouter.so")
+_lib = None
+
+
+# ----------------------------------------------------------------------------------------------------------------
+# bf16 helpers (round to nearest even, NaN -> 0x7fc0: c10::BFloat16's rule)
+# ----------------------------------------------------------------------------------------------------------------
+def f32_to_bf16_bits(a) -> np.ndarray:
+    u = np.ascontiguousarray(np.asarray(a, dtype=np.float32)).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = 0x7FC0
+    return r
+
+
+def bf16_bits_to_f32(b) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def round_bf16(a) -> np.ndarray:
+    """Round (float32 or float64) values to the nearest bf16 value, returned as float32.  float64 input is rounded to
+    bf16 directly from float64 (no intermediate float32 rounding) by rounding on the float64 bit pattern."""
+    a = np.asarray(a)
+    if a.dtype == np.float64:
+        u = np.ascontiguousarray(a).view(np.uint64)
+        nan = np.isnan(a)
+        # bf16 keeps the top 16 bits of a float32: 7 mantissa bits -> 45 dropped bits of the float64 mantissa
+        drop = np.uint64(45)
+        half = np.uint64(1) << (drop - np.uint64(1))
+        lsb = (u >> drop) & np.uint64(1)
+        r = ((u + (half - np.uint64(1)) + lsb) >> drop) << drop
+        out = r.view(np.float64)
+        # magnitudes beyond bf16's range go to inf; below float32's normal range the float32 path is exact enough
+        out = out.astype(np.float32)
+        small = np.abs(a) < 2.0 ** -126
+        if small.any():
+            out[small] = bf16_bits_to_f32(f32_to_bf16_bits(a[small].astype(np.float32)))
+        out[nan] = np.nan
+        return out
+    return bf16_bits_to_f32(f32_to_bf16_bits(a.astype(np.float32)))
+
+
+# ----------------------------------------------------------------------------------------------------------------
+# C half (router.c)
+# ----------------------------------------------------------------------------------------------------------------
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(f"oracle C library not built: {_LIB_PATH} (run oracle/build.py)")
+        L = ctypes.CDLL(_LIB_PATH)
+        P, I64, I32, F32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
+        L.orc_hexp.argtypes, L.orc_hexp.restype = [F32], F32
+        L.orc_f32_to_bf16.argtypes, L.orc_f32_to_bf16.restype = [F32], ctypes.c_uint16
+        L.orc_router_logits.argtypes = [P, I64, P, P, I64, I64, I32, P]
+        L.orc_topk_from_logits.argtypes = [P, I64, I32, I32, I32, F32, P, P, P]
+        L.orc_route.argtypes = [P, I64, P, P, I64, I64, I32, I32, I32, F32, P, P, P]
+        L.orc_dispatch.argtypes = [P, I64, I32, I32, P, P, P, P]
+        L.orc_dispatch.restype = I32
+        L.orc_make_schedule.argtypes = [P, I32, I64, I32, P, P, P]
+        _lib = L
+    return _lib
+
+
+def _ptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p) if a is not None else None
+
+
+def hexp(x) -> np.ndarray:
+    x = np.asarray(x, dtype=np.float32)
+    L = lib()
+    return np.array([L.orc_hexp(float(v)) for v in x.ravel()], dtype=np.float32).reshape(x.shape)
+
+
+def router_logits(x_bits: np.ndarray, wr_bits: np.ndarray, bias=None) -> np.ndarray:
+    """fp32 router logits in the fixed reduction order of router.c.  x_bits (T, d), wr_bits (E, d): bf16 bit patterns
+    (uint16).  Convention source: aurora/hf_pipeline.py:352 (F.linear(x.float(), W.float()))."""
+    x_bits = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    wr_bits = np.ascontiguousarray(wr_bits, dtype=np.uint16)
+    T, d = x_bits.shape
+    E = wr_bits.shape[0]
+    out = np.empty((T, E), dtype=np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    lib().orc_router_logits(_ptr(x_bits), d, _ptr(wr_bits), _ptr(b), T, d, E, _ptr(out))
+    return out
+
+
+def topk_from_logits(logits: np.ndarray, k: int, renorm: bool = True, scaling: float = 1.0, with_probs=False):
+    """softmax + top-k + renormalisation (aurora/hf_pipeline.py:359 conventions) on given fp32 logits.
+    Returns ids (T, k) int32 and weights (T, k) fp32 (and probs (T, E) when asked)."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    T, E = logits.shape
+    ids = np.empty((T, k), dtype=np.int32)
+    w = np.empty((T, k), dtype=np.float32)
+    probs = np.empty((T, E), dtype=np.float32) if with_probs else None
+    lib().orc_topk_from_logits(_ptr(logits), T, E, k, int(renorm), float(scaling), _ptr(ids), _ptr(w), _ptr(probs))
+    return (ids, w, probs) if with_probs else (ids, w)
+
+
+def route(x_bits, wr_bits, k, bias=None, renorm=True, scaling=1.0):
+    logits = router_logits(x_bits, wr_bits, bias)
+    ids, w = topk_from_logits(logits, k, renorm, scaling)
+    return logits, ids, w
+
+
+# ----------------------------------------------------------------------------------------------------------------
+# dispatch: aurora/hf_compat.py:69-72 (flat, stable argsort, bincount), :78 (a_idx = order // k, y_idx = order),
+# :80 (routing weight gathered in sorted order and rounded to x.dtype)
+# ----------------------------------------------------------------------------------------------------------------
+def dispatch(ids: np.ndarray, E: int):
+    """ids (T, k) -> dict(counts (E,) int64, order (M,) int64, a_idx (M,) int32, y_idx (M,) int32,
+    inv_pos (M,) int32 with inv_pos[order[r]] = r)."""
+    T, k = ids.shape
+    flat = ids.reshape(-1).astype(np.int64)
+    order = np.argsort(flat, kind="stable")
+    counts = np.bincount(flat, minlength=E).astype(np.int64)
+    inv = np.empty_like(order)
+    inv[order] = np.arange(order.size)
+    return dict(counts=counts, order=order, a_idx=(order // k).astype(np.int32), y_idx=order.astype(np.int32),
+                inv_pos=inv.astype(np.int32))
+
+
+def dispatch_c(ids: np.ndarray, E: int):
+    """The same as dispatch() by an explicit counting sort in C."""
+    T, k = ids.shape
+    flat = np.ascontiguousarray(ids.reshape(-1), dtype=np.int64)
+    M = flat.size
+    counts = np.empty(E, np.int64)
+    order = np.empty(M, np.int64)
+    a_idx = np.empty(M, np.int32)
+    inv = np.empty(M, np.int32)
+    rc = lib().orc_dispatch(_ptr(flat), M, k, E, _ptr(counts), _ptr(order), _ptr(a_idx), _ptr(inv))
+    if rc != 0:
+        raise ValueError("expert id out of range")
+    return dict(counts=counts, order=order, a_idx=a_idx, y_idx=order.astype(np.int32), inv_pos=inv)
+
+
+BLOCK_M = 64  # aurora/moe_triton.py:13
+
+
+def make_schedule(counts: np.ndarray, M: int, block_m: int = BLOCK_M):
+    """aurora/moe_triton.py:93-107, restated in numpy: per block b < ceil(M/block_m) + E, the expert (or -1), its
+    first row and the end row of that expert."""
+    counts = np.asarray(counts, dtype=np.int64)
+    E = counts.size
+    starts = np.cumsum(counts) - counts
+    nblk = (counts + block_m - 1) // block_m
+    cum = np.cumsum(nblk)
+    nb = -(-M // block_m) + E
+    b = np.arange(nb)
+    e = np.searchsorted(cum, b, side="right")
+    valid = e < E
+    ec = np.minimum(e, E - 1)
+    block_row = starts[ec] + (b - (cum[ec] - nblk[ec])) * block_m
+    row_end = starts[ec] + counts[ec]
+    return (np.where(valid, ec, -1).astype(np.int32), block_row.astype(np.int32), row_end.astype(np.int32))
+
+
+def make_schedule_c(counts, M, block_m=BLOCK_M):
+    counts = np.ascontiguousarray(counts, dtype=np.int64)
+    E = counts.size
+    nb = -(-M // block_m) + E
+    be, br, re_ = (np.empty(nb, np.int32) for _ in range(3))
+    lib().orc_make_schedule(_ptr(counts), E, M, block_m, _ptr(be), _ptr(br), _ptr(re_))
+    return be, br, re_
+
+
+# ----------------------------------------------------------------------------------------------------------------
+# grouped GEMM: aurora/moe_triton.py:22-56 (fused gather / int8 weight / scale / scatter, fp32 accumulation, one
+# rounding on store) -- restated with float64 accumulation; the fp32-vs-fp64 accumulation gap is what the tests'
+# tolerance covers.
+# ----------------------------------------------------------------------------------------------------------------
+def grouped_mm(a, w, counts, a_idx=None, y_idx=None, scale=None, w_scale=None, round_out=True):
+    """a (T|M, K), w (E, K, N) (float values, int8 allowed with w_scale (E, N)), counts (E,) -> y (M, N).
+    Row r of the sorted problem reads a[a_idx[r]] (or a[r]) and is written to y[y_idx[r]] (or y[r]).  Epilogue order
+    as the reference: acc * w_scale[e, n] then * scale[r], one bf16 rounding."""
+    counts = np.asarray(counts, dtype=np.int64)
+    M = int(counts.sum()) if a_idx is None else len(a_idx)
+    N = w.shape[2]
+    y = np.zeros((M, N), dtype=np.float32 if round_out else np.float64)
+    start = 0
+    for e, c in enumerate(counts.tolist()):
+        if c == 0:
+            continue
+        rows = np.arange(start, start + c)
+        src = a[a_idx[rows]] if a_idx is not None else a[rows]
+        acc = src.astype(np.float64) @ w[e].astype(np.float64)
+        if w_scale is not None:
+            acc = acc * w_scale[e].astype(np.float64)[None, :]
+        if scale is not None:
+            acc = acc * np.asarray(scale, dtype=np.float64)[rows, None]
+        dst = y_idx[rows] if y_idx is not None else rows
+        y[dst] = round_bf16(acc) if round_out else acc
+        start += c
+    return y
+
+
+def silu64(g):
+    g = np.asarray(g, dtype=np.float64)
+    return g / (1.0 + np.exp(-g))
+
+
+def swiglu_fwd(gb, ub):
+    """act = self._act(g) * u on bf16 tensors (aurora/hf_compat.py:81): silu rounded to bf16, then the product
+    rounded to bf16 (gb, ub already bf16 values)."""
+    s = round_bf16(silu64(gb))
+    return round_bf16(s.astype(np.float64) * ub.astype(np.float64))
+
+
+def quant_int8(w):
+    """aurora/hf_compat.py:106-110: per-(expert, output column) absmax / 127 scale (stored bf16), int8 weights."""
+    w = np.asarray(w, dtype=np.float32)
+    scale = np.maximum(np.abs(w).max(axis=1), 1e-8) / np.float32(127)
+    q = np.clip(np.round(w / scale[:, None, :]), -127, 127).astype(np.int8)
+    return q, round_bf16(scale)
+
+
+# ----------------------------------------------------------------------------------------------------------------
+# layer forward: the Triton path of aurora/hf_compat.py:75-82
+# ----------------------------------------------------------------------------------------------------------------
+def moe_forward(x, ids, topk_w, wgu, wd, tokens=None):
+    """x (T, d) bf16 values (float32 array), ids (T, k), topk_w (T, k) fp32, wgu (E, d, 2h), wd (E, h, d).
+    Returns dict with out (T, d) and the per-flat-row intermediates (gb, ub, act, yhat, y) in flat order
+    f = t*k + j.  tokens: optional subset of token indices (then only those tokens' rows are computed; arrays are
+    indexed by position in `tokens`)."""
+    T, k = ids.shape
+    E = wgu.shape[0]
+    h = wgu.shape[2] // 2
+    tok = np.arange(T) if tokens is None else np.asarray(tokens)
+    n = tok.size
+    d = x.shape[1]
+    gb = np.zeros((n * k, h), np.float32)
+    ub = np.zeros((n * k, h), np.float32)
+    act = np.zeros((n * k, h), np.float32)
+    yhat = np.zeros((n * k, d), np.float64)
+    y = np.zeros((n * k, d), np.float32)
+    wb = round_bf16(topk_w[tok].reshape(-1))
+    flat_e = ids[tok].reshape(-1)
+    rows_t = np.repeat(tok, k)
+    for e in range(E):
+        sel = np.nonzero(flat_e == e)[0]
+        if sel.size == 0:
+            continue
+        gu = x[rows_t[sel]].astype(np.float64) @ wgu[e].astype(np.float64)
+        gb[sel] = round_bf16(gu[:, :h])
+        ub[sel] = round_bf16(gu[:, h:])
+        act[sel] = swiglu_fwd(gb[sel], ub[sel])
+        yh = act[sel].astype(np.float64) @ wd[e].astype(np.float64)
+        yhat[sel] = yh
+        y[sel] = round_bf16(yh * wb[sel].astype(np.float64)[:, None])
+    out = round_bf16(y.reshape(n, k, d).astype(np.float64).sum(1))
+    return dict(out=out, gb=gb, ub=ub, act=act, yhat=yhat, y=y, wb=wb)
+
+
+def moe_backward(x, ids, topk_w, wgu, wd, dout, fwd=None):
+    """Closed-form backward of moe_forward (float64; the bf16 roundings of the forward are treated as identity and
+    the derivatives are taken at the stored bf16 values, as autograd does).  Returns dict(dx_experts (T, d),
+    dwgu, dwd, dtopk_w (T, k))."""
+    T, k = ids.shape
+    E = wgu.shape[0]
+    h = wgu.shape[2] // 2
+    d = x.shape[1]
+    f = fwd if fwd is not None else moe_forward(x, ids, topk_w, wgu, wd)
+    dout64 = np.asarray(dout, dtype=np.float64)
+    rows_t = np.repeat(np.arange(T), k)
+    flat_e = ids.reshape(-1)
+    wb = f["wb"].astype(np.float64)
+    dtw = np.einsum("fd,fd->f", dout64[rows_t], f["yhat"]).reshape(T, k)
+    dyhat = dout64[rows_t] * wb[:, None]
+    dx = np.zeros((T, d), np.float64)
+    dwgu = np.zeros(wgu.shape, np.float64)
+    dwd = np.zeros(wd.shape, np.float64)
+    for e in range(E):
+        sel = np.nonzero(flat_e == e)[0]
+        if sel.size == 0:
+            continue
+        g = f["gb"][sel].astype(np.float64)
+        u = f["ub"][sel].astype(np.float64)
+        a = f["act"][sel].astype(np.float64)
+        dact = dyhat[sel] @ wd[e].astype(np.float64).T
+        dwd[e] = a.T @ dyhat[sel]
+        sig = 1.0 / (1.0 + np.exp(-g))
+        s = g * sig
+        dg = dact * u * sig * (1.0 + g * (1.0 - sig))
+        du = dact * s
+        dgu = np.concatenate([dg, du], axis=1)
+        dxs = dgu @ wgu[e].astype(np.float64).T
+        np.add.at(dx, rows_t[sel], dxs)
+        dwgu[e] = x[rows_t[sel]].astype(np.float64).T @ dgu
+    return dict(dx_experts=dx, dwgu=dwgu, dwd=dwd, dtopk_w=dtw)
+
+
+def router_backward(logits, ids, dtopk_w, renorm=True, scaling=1.0):
+    """d loss / d logits (T, E) for w = topk(softmax(logits)) [renormalised] * scaling, float64."""
+    lg = np.asarray(logits, dtype=np.float64)
+    T, E = lg.shape
+    k = ids.shape[1]
+    m = lg.max(axis=1, keepdims=True)
+    ex = np.exp(lg - m)
+    p = ex / ex.sum(axis=1, keepdims=True)
+    sel = np.take_along_axis(p, ids.astype(np.int64), axis=1)
+    dw = np.asarray(dtopk_w, dtype=np.float64) * scaling
+    if renorm:
+        s = sel.sum(axis=1, keepdims=True) + 1e-20
+        dsel = dw / s - (dw * sel).sum(axis=1, keepdims=True) / s ** 2
+    else:
+        dsel = dw
+    dp = np.zeros((T, E), np.float64)
+    np.add.at(dp, (np.repeat(np.arange(T), k), ids.reshape(-1).astype(np.int64)), dsel.reshape(-1))
+    return p * (dp - (p * dp).sum(axis=1, keepdims=True))
+
+
+def layer_backward(x, wr, ids, topk_w, logits, wgu, wd, dout, renorm=True, scaling=1.0, fwd=None):
+    """Full layer backward: expert path + router path.  Returns dict(dx, dwr, dwgu, dwd, dlogits, dtopk_w)."""
+    b = moe_backward(x, ids, topk_w, wgu, wd, dout, fwd)
+    dl = router_backward(logits, ids, b["dtopk_w"], renorm, scaling)
+    x64 = np.asarray(x, dtype=np.float64)
+    dx = b["dx_experts"] + dl @ np.asarray(wr, dtype=np.float64)
+    dwr = dl.T @ x64
+    return dict(dx=dx, dwr=dwr, dwgu=b["dwgu"], dwd=b["dwd"], dlogits=dl, dtopk_w=b["dtopk_w"])
+
+
+# ----------------------------------------------------------------------------------------------------------------
+# seeded synthetic inputs (same generator as the benchmark: torch CPU generator, fp32, then cast)
+# ----------------------------------------------------------------------------------------------------------------
+def zipf_bias(E: int, seed: int, s: float = 1.2, n_empty: int = 2) -> np.ndarray:
+    """Per-expert router-logit bias: a seeded permutation of the experts; the first E - n_empty get
+    -s * ln(rank) (rank 1-based), the last n_empty get -inf (never routed)."""
+    rng = np.random.default_rng(seed)
+    perm = rng.permutation(E)
+    b = np.empty(E, np.float32)
+    for r, e in enumerate(perm):
+        b[e] = -np.inf if r >= E - n_empty else np.float32(-s * np.log(r + 1.0))
+    return b

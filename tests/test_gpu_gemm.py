@@ -1,0 +1,90 @@
+"""Grouped GEMM parity on the GPU against the float64 oracle: the reference's own known-answer construction
+(aurora/hf_compat.py:112-121), ragged / skewed / empty experts, gather, scatter and row scale, both tile sizes,
+and the weight-gradient (ragged-K) GEMM."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from tests.util import assert_close_bf16, f32
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(params=["L", "S"])
+def tile(request, monkeypatch):
+    monkeypatch.setenv("HMOE_GEMM_TILE", request.param)
+    return request.param
+
+
+def test_self_test_shape(oracle, tile):
+    """48x64 @ (3, 64, 32), counts [16, 0, 32]: the reference's _self_test, plus the tighter bf16 bound."""
+    from trenowanie_generatora_obrazkow_amd import moe_triton
+    from trenowanie_generatora_obrazkow_amd.hf_compat import _self_test
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(48, 64, generator=g).bfloat16()
+    w = torch.randn(3, 64, 32, generator=g).bfloat16()
+    counts = torch.tensor([16, 0, 32])
+    y = moe_triton.grouped_mm(a.cuda(), w.cuda(), counts.cuda())
+    ref = oracle.grouped_mm(f32(a), f32(w), counts.numpy())
+    assert_close_bf16(f32(y), ref, "self-test shape")
+    assert _self_test(lambda a_, w_, c_: moe_triton.grouped_mm(a_, w_, c_), torch.device("cuda"), torch.bfloat16)
+
+
+@pytest.mark.parametrize("T,K,N,E,k,skew", [(1024, 256, 512, 8, 2, 0), (700, 520, 264, 5, 2, 1),
+                                            (2048, 1024, 1536, 16, 1, 1), (64, 2048, 640, 128, 8, 0)])
+def test_grouped_mm_fused(oracle, tile, T, K, N, E, k, skew):
+    """gather (a_idx), scale, scatter (y_idx) as _fused_moe_infer's second call uses them."""
+    from trenowanie_generatora_obrazkow_amd import moe_triton
+    print(f"grouped_mm T={T} K={K} N={N} E={E} k={k} skew={skew} tile={tile}", flush=True)
+    g = torch.Generator().manual_seed(K + N)
+    if skew:
+        p = torch.tensor([0.0 if e == 1 else 2.0 ** (-e) for e in range(E)])
+        ids = torch.multinomial(p / p.sum(), T * k, replacement=True, generator=g).view(T, k)
+    else:
+        ids = torch.randint(0, E, (T, k), generator=g)
+    x = torch.randn(T, K, generator=g).bfloat16()
+    w = (torch.randn(E, K, N, generator=g) * 0.05).bfloat16()
+    sc = torch.rand(T * k, generator=g).bfloat16()
+    flat = ids.reshape(-1)
+    order = flat.argsort(stable=True)
+    counts = torch.bincount(flat, minlength=E)
+    a_idx = (order // k).int()
+    y_idx = order.int()
+    dev = torch.device("cuda")
+    y = moe_triton.grouped_mm(x.to(dev), w.to(dev), counts.to(dev), a_idx=a_idx.to(dev), y_idx=y_idx.to(dev),
+                              scale=sc.to(dev))
+    ref = oracle.grouped_mm(f32(x), f32(w), counts.numpy(), a_idx=a_idx.numpy(), y_idx=y_idx.numpy(), scale=f32(sc))
+    assert_close_bf16(f32(y), ref, "grouped_mm fused")
+    # plain sorted rows
+    xs = x[order // k]
+    y2 = moe_triton.grouped_mm(xs.to(dev), w.to(dev), counts.to(dev))
+    ref2 = oracle.grouped_mm(f32(xs), f32(w), counts.numpy())
+    assert_close_bf16(f32(y2), ref2, "grouped_mm sorted")
+
+
+@pytest.mark.parametrize("M,P,N,E,skew", [(4096, 256, 512, 8, 0), (3000, 520, 264, 5, 1), (777, 128, 1024, 16, 1)])
+def test_grouped_wgrad(oracle, tile, M, P, N, E, skew):
+    from trenowanie_generatora_obrazkow_amd import ops
+    print(f"wgrad M={M} P={P} N={N} E={E} tile={tile}", flush=True)
+    g = torch.Generator().manual_seed(M)
+    if skew:
+        p = torch.tensor([0.0 if e == 2 else 3.0 ** (-e) for e in range(E)])
+        ids = torch.multinomial(p / p.sum(), M, replacement=True, generator=g)
+    else:
+        ids = torch.randint(0, E, (M,), generator=g)
+    counts = torch.bincount(ids, minlength=E)
+    a = torch.randn(M, P, generator=g).bfloat16()
+    b = torch.randn(M, N, generator=g).bfloat16()
+    dev = torch.device("cuda")
+    for dt in (torch.float32, torch.bfloat16):
+        dw = ops.grouped_wgrad(a.to(dev), b.to(dev), counts.int().to(dev), E, dtype=dt)
+        ref = np.zeros((E, P, N))  # float64; compared after one rounding to the output dtype
+        st = 0
+        a64, b64 = f32(a).astype(np.float64), f32(b).astype(np.float64)
+        for e, c in enumerate(counts.tolist()):
+            ref[e] = a64[st:st + c].T @ b64[st:st + c]
+            st += c
+        assert_close_bf16(f32(dw), oracle.round_bf16(ref) if dt == torch.bfloat16 else ref, f"wgrad {dt}")
+        assert (f32(dw)[counts.numpy() == 0] == 0).all()

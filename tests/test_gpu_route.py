@@ -1,0 +1,51 @@
+"""Router parity on the GPU: ids, weights and logits bit-exact with the oracle's C restatement (same reduction
+order, same exp), over the configs' router shapes plus edge cases (ties, -inf bias, many experts, large k)."""
+import numpy as np
+import pytest
+import torch
+
+from tests.util import bits, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(oracle, x, wr, k, bias=None, renorm=True, scaling=1.0):
+    from trenowanie_generatora_obrazkow_amd import ops
+    dev = torch.device("cuda")
+    b_t = None if bias is None else torch.as_tensor(bias, dtype=torch.float32).to(dev)
+    lg, ids, w = ops.route_topk(x.to(dev), wr.to(dev), k, bias=b_t, renorm=renorm, scaling=scaling)
+    rl, rids, rw = oracle.route(bits(x), bits(wr), k, bias=bias, renorm=renorm, scaling=scaling)
+    np.testing.assert_array_equal(lg.cpu().numpy().view(np.uint32), rl.view(np.uint32))
+    np.testing.assert_array_equal(ids.cpu().numpy(), rids)
+    np.testing.assert_array_equal(w.cpu().numpy().view(np.uint32), rw.view(np.uint32))
+    return rids
+
+
+@pytest.mark.parametrize("T,d,E,k", [(512, 256, 8, 2), (2048, 1024, 8, 2), (4096, 1536, 16, 2), (300, 2048, 128, 8),
+                                     (77, 520, 5, 3), (64, 4096, 256, 16)])
+def test_route_bitexact(oracle, T, d, E, k):
+    print(f"route T={T} d={d} E={E} k={k}", flush=True)
+    x, wr, _, _ = make_inputs(T, d, E, 8, seed=T + d)
+    _check(oracle, x, wr, k)
+
+
+def test_route_no_renorm_and_scaling(oracle):
+    x, wr, _, _ = make_inputs(1000, 1024, 16, 8, seed=3)
+    _check(oracle, x, wr, 4, renorm=False, scaling=2.5)
+    _check(oracle, x, wr, 4, renorm=True, scaling=2.5)
+
+
+def test_route_zipf_bias_empty_experts(oracle):
+    x, wr, _, _ = make_inputs(16384, 1536, 16, 8, seed=0)
+    bias = oracle.zipf_bias(16, seed=0)
+    rids = _check(oracle, x, wr, 2, bias=bias)
+    counts = np.bincount(rids.reshape(-1), minlength=16)
+    assert (counts[np.isinf(bias)] == 0).all()
+
+
+def test_route_ties(oracle):
+    # all-zero router weights -> every logit 0: ties resolve to the lowest expert ids, equal weights
+    x, wr, _, _ = make_inputs(128, 256, 8, 8, seed=1)
+    wr = torch.zeros_like(wr)
+    rids = _check(oracle, x, wr, 3)
+    assert (rids == np.array([0, 1, 2])).all()

@@ -1,0 +1,785 @@
+// Routing, dispatch (stable counting sort + row permutation), schedule and combine kernels, with their C entry
+// points.  HBM-bound integer/byte work: vectorised 16-byte row copies, wave ballots for the stable ranks.
+#include "hmoe_common.h"
+
+namespace hmoe {
+
+// ---------------------------------------------------------------------------------------------------------------
+// Router: logits in the documented order, softmax, top-k, renormalisation.  One wave per token.
+// ---------------------------------------------------------------------------------------------------------------
+constexpr int kRouteMaxE = 256;  // experts per lane: 4
+constexpr int kRouteEPL = kRouteMaxE / 64;
+constexpr int kMaxK = 16;
+
+template <int NCH>
+__global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                         const uint16_t* __restrict__ wr,
+                                                         const float* __restrict__ bias, int T, int d, int E, int k,
+                                                         int renorm, float scaling, float* __restrict__ logits,
+                                                         int32_t* __restrict__ ids, float* __restrict__ wout) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int nwaves = blockDim.x >> 6;
+  const int wave = threadIdx.x >> 6;
+  for (int t = blockIdx.x * nwaves + wave; t < T; t += gridDim.x * nwaves) {
+    uint4 xr[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      int idx = c * 512 + lane * 8;
+      if (idx < d)
+        xr[c] = *reinterpret_cast<const uint4*>(x + (int64_t)t * ldx + idx);
+      else
+        xr[c] = make_uint4(0, 0, 0, 0);
+    }
+    float lg[kRouteEPL];
+#pragma unroll
+    for (int i = 0; i < kRouteEPL; ++i) lg[i] = -__builtin_inff();
+    for (int e = 0; e < E; ++e) {
+      float acc = 0.0f;
+      const uint16_t* wrow = wr + (int64_t)e * d;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        int idx = c * 512 + lane * 8;
+        if (idx < d) {
+          uint4 wv = *reinterpret_cast<const uint4*>(wrow + idx);
+          uint32_t xw[4] = {xr[c].x, xr[c].y, xr[c].z, xr[c].w};
+          uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            acc = __fadd_rn(acc, __fmul_rn(bf_lo(xw[j]), bf_lo(ww[j])));
+            acc = __fadd_rn(acc, __fmul_rn(bf_hi(xw[j]), bf_hi(ww[j])));
+          }
+        }
+      }
+      float v = wave_sum_butterfly(acc);
+      if (bias) v = __fadd_rn(v, bias[e]);
+#pragma unroll
+      for (int i = 0; i < kRouteEPL; ++i)
+        if (e == i * 64 + lane) lg[i] = v;
+    }
+    // softmax over the E logits held lane-wise (lane l: experts l, l+64, ...)
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < kRouteEPL; ++i)
+      if (i * 64 + lane < E) m = fmaxf(m, lg[i]);
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
+    float ex[kRouteEPL];
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kRouteEPL; ++i) {
+      ex[i] = 0.0f;
+      if (i * 64 + lane < E) {
+        ex[i] = hexp(__fsub_rn(lg[i], m));
+        a = __fadd_rn(a, ex[i]);
+      }
+    }
+    const float S = wave_sum_butterfly(a);
+    if (logits) {
+#pragma unroll
+      for (int i = 0; i < kRouteEPL; ++i)
+        if (i * 64 + lane < E) logits[(int64_t)t * E + i * 64 + lane] = lg[i];
+    }
+    bool taken[kRouteEPL];
+#pragma unroll
+    for (int i = 0; i < kRouteEPL; ++i) taken[i] = false;
+    float selp[kMaxK];
+    int sele[kMaxK];
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) {
+      selp[j] = 0.0f;
+      sele[j] = 0;
+      if (j < k) {
+        float bv = 0.0f;
+        int be = 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < kRouteEPL; ++i) {
+          int e = i * 64 + lane;
+          if (e < E && !taken[i] && (be == 0x7fffffff || lg[i] > bv)) {
+            bv = lg[i];
+            be = e;
+          }
+        }
+#pragma unroll
+        for (int s = 32; s >= 1; s >>= 1) {
+          float ov = __shfl_xor(bv, s, 64);
+          int oe = __shfl_xor(be, s, 64);
+          bool take = oe != 0x7fffffff && (be == 0x7fffffff || ov > bv || (ov == bv && oe < be));
+          if (take) {
+            bv = ov;
+            be = oe;
+          }
+        }
+        float myex = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kRouteEPL; ++i)
+          if (be == i * 64 + lane) {
+            taken[i] = true;
+            myex = ex[i];
+          }
+        float pex = __shfl(myex, be & 63, 64);
+        selp[j] = __fdiv_rn(pex, S);
+        sele[j] = be;
+      }
+    }
+    if (lane == 0) {
+      float den = 0.0f;
+      if (renorm) {
+        float s = selp[0];
+#pragma unroll
+        for (int j = 1; j < kMaxK; ++j)
+          if (j < k) s = __fadd_rn(s, selp[j]);
+        den = __fadd_rn(s, 1e-20f);
+      }
+#pragma unroll
+      for (int j = 0; j < kMaxK; ++j)
+        if (j < k) {
+          float wj = renorm ? __fmul_rn(__fdiv_rn(selp[j], den), scaling) : __fmul_rn(selp[j], scaling);
+          ids[(int64_t)t * k + j] = sele[j];
+          wout[(int64_t)t * k + j] = wj;
+        }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Dispatch: stable counting sort of flat ids.  Pass 1 (one wave per block of kFPB flat rows): per-block expert
+// histogram and the stable rank of each flat row among earlier rows of the same expert inside its block (wave
+// ballots: a lane's peers are the lanes whose id agrees on every bit).  Pass 2 (one workgroup): per-expert totals,
+// expert starts, and per-(block, expert) first sorted row.  Pass 3: positions, index arrays and the row copy.
+// ---------------------------------------------------------------------------------------------------------------
+constexpr int kFPB = 1024;       // flat rows per histogram block
+constexpr int kMaxEDispatch = 1024;
+
+__device__ __forceinline__ int load_id(const void* ids, int is64, int64_t f) {
+  return is64 ? (int)reinterpret_cast<const int64_t*>(ids)[f] : reinterpret_cast<const int32_t*>(ids)[f];
+}
+
+__global__ __launch_bounds__(64) void dispatch_hist_kernel(const void* __restrict__ ids, int ids64, int64_t M, int E,
+                                                           int nbits, int32_t* __restrict__ hist,
+                                                           int32_t* __restrict__ rank) {
+  __shared__ int run[kMaxEDispatch];
+  const int lane = threadIdx.x;
+  for (int e = lane; e < E; e += 64) run[e] = 0;
+  __syncthreads();
+  const int64_t start = (int64_t)blockIdx.x * kFPB;
+  const int64_t end = min(M, start + kFPB);
+  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int64_t base = start; base < end; base += 64) {
+    const int64_t f = base + lane;
+    int e = -1;
+    if (f < end) e = load_id(ids, ids64, f);
+    const bool valid = e >= 0 && e < E;
+    uint64_t peers = __ballot(valid);
+    for (int b = 0; b < nbits; ++b) {
+      const bool bit = valid && ((e >> b) & 1);
+      const uint64_t m1 = __ballot(bit);
+      peers &= ((e >> b) & 1) ? m1 : ~m1;
+    }
+    const int r = __popcll(peers & lt);
+    const int cnt = __popcll(peers);
+    int basecnt = 0;
+    if (valid) basecnt = run[e];
+    __syncthreads();
+    if (valid) {
+      rank[f] = basecnt + r;
+      if (r == 0) run[e] = basecnt + cnt;
+    }
+    __syncthreads();
+  }
+  for (int e = lane; e < E; e += 64) hist[(int64_t)blockIdx.x * E + e] = run[e];
+}
+
+__global__ __launch_bounds__(256) void dispatch_scan_kernel(int32_t* __restrict__ hist, int nblk, int E,
+                                                            int32_t* __restrict__ counts,
+                                                            int64_t* __restrict__ counts64,
+                                                            int32_t* __restrict__ starts) {
+  __shared__ int cnt[kMaxEDispatch + 1];
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    int s = 0;
+    for (int b = 0; b < nblk; ++b) s += hist[(int64_t)b * E + e];
+    cnt[e] = s;
+    counts[e] = s;
+    if (counts64) counts64[e] = s;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int e = 0; e < E; ++e) {
+      int c = cnt[e];
+      cnt[e] = run;
+      starts[e] = run;
+      run += c;
+    }
+    starts[E] = run;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    int run = cnt[e];
+    for (int b = 0; b < nblk; ++b) {
+      int c = hist[(int64_t)b * E + e];
+      hist[(int64_t)b * E + e] = run;
+      run += c;
+    }
+  }
+}
+
+// one wave per token: sorted positions of its k rows, index arrays, then the row copy x[t] -> xs[pos_j]
+__global__ __launch_bounds__(256) void dispatch_scatter_kernel(
+    const void* __restrict__ ids, int ids64, const void* __restrict__ tw, int tw_dtype, int64_t T, int k, int E,
+    const int32_t* __restrict__ blkoff, const int32_t* __restrict__ rank, const uint16_t* __restrict__ x,
+    int64_t ldx, int64_t d, uint16_t* __restrict__ xs, int32_t* __restrict__ order, int32_t* __restrict__ a_idx,
+    int32_t* __restrict__ inv_pos, uint16_t* __restrict__ w_sorted) {
+  const int lane = threadIdx.x & 63;
+  const int nwaves = blockDim.x >> 6;
+  const int64_t nvec = d / 8;
+  for (int64_t t = (int64_t)blockIdx.x * nwaves + (threadIdx.x >> 6); t < T; t += (int64_t)gridDim.x * nwaves) {
+    int64_t pos[kMaxK];
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) {
+      pos[j] = -1;
+      if (j < k) {
+        const int64_t f = t * k + j;
+        const int e = load_id(ids, ids64, f);
+        if (e >= 0 && e < E) pos[j] = (int64_t)blkoff[(f / kFPB) * E + e] + rank[f];
+        if (lane == j && pos[j] >= 0) {
+          order[pos[j]] = (int32_t)f;
+          if (a_idx) a_idx[pos[j]] = (int32_t)t;
+          if (w_sorted) {
+            uint32_t wb;
+            if (tw_dtype == HMOE_DT_F32)
+              wb = f2bf(reinterpret_cast<const float*>(tw)[f]);
+            else
+              wb = reinterpret_cast<const uint16_t*>(tw)[f];
+            w_sorted[pos[j]] = (uint16_t)wb;
+          }
+        }
+        if (lane == j && inv_pos) inv_pos[f] = (int32_t)pos[j];
+      }
+    }
+    if (xs) {
+      const uint4* src = reinterpret_cast<const uint4*>(x + t * ldx);
+      for (int64_t c = lane; c < nvec; c += 64) {
+        const uint4 v = src[c];
+#pragma unroll
+        for (int j = 0; j < kMaxK; ++j)
+          if (j < k && pos[j] >= 0) reinterpret_cast<uint4*>(xs + pos[j] * d)[c] = v;
+      }
+    }
+  }
+}
+
+// make_schedule (aurora/moe_triton.py:93-107): one thread per block b; expert found by a scan over the counts.
+__global__ __launch_bounds__(256) void make_schedule_kernel(const void* __restrict__ counts, int is64, int E,
+                                                            int64_t nb, int block_m, int32_t* __restrict__ block_e,
+                                                            int32_t* __restrict__ block_row,
+                                                            int32_t* __restrict__ row_end) {
+  __shared__ int64_t s_start[kMaxEDispatch + 1];
+  __shared__ int64_t s_cum[kMaxEDispatch + 1];
+  if (threadIdx.x == 0) {
+    int64_t st = 0, cu = 0;
+    for (int e = 0; e < E; ++e) {
+      const int64_t c = read_count(counts, is64, e);
+      s_start[e] = st;
+      st += c;
+      cu += (c + block_m - 1) / block_m;
+      s_cum[e] = cu;
+    }
+  }
+  __syncthreads();
+  for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nb; b += (int64_t)gridDim.x * blockDim.x) {
+    // e = searchsorted(cum, b, right=True): number of cum entries <= b
+    int lo = 0, hi = E;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (s_cum[mid] <= b)
+        lo = mid + 1;
+      else
+        hi = mid;
+    }
+    const int e = lo;
+    const int ec = e < E ? e : E - 1;
+    const int64_t c = read_count(counts, is64, ec);
+    const int64_t nblk = (c + block_m - 1) / block_m;
+    block_e[b] = e < E ? ec : -1;
+    block_row[b] = (int32_t)(s_start[ec] + (b - (s_cum[ec] - nblk)) * block_m);
+    row_end[b] = (int32_t)(s_start[ec] + c);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Combine (forward) and its backward.
+// ---------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ y, int64_t T, int k, int64_t d,
+                                                      uint16_t* __restrict__ out) {
+  const int64_t nvec = d / 8;
+  const int64_t total = T * nvec;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / nvec, c = i - t * nvec;
+    const uint4* src = reinterpret_cast<const uint4*>(y + t * k * d) + c;
+    float s[8];
+    {
+      const uint4 v = src[0];
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        s[2 * q] = bf_lo(w[q]);
+        s[2 * q + 1] = bf_hi(w[q]);
+      }
+    }
+    for (int j = 1; j < k; ++j) {
+      const uint4 v = src[j * nvec];
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        s[2 * q] += bf_lo(w[q]);
+        s[2 * q + 1] += bf_hi(w[q]);
+      }
+    }
+    uint4 o;
+    o.x = pack_bf2(s[0], s[1]);
+    o.y = pack_bf2(s[2], s[3]);
+    o.z = pack_bf2(s[4], s[5]);
+    o.w = pack_bf2(s[6], s[7]);
+    reinterpret_cast<uint4*>(out + t * d)[c] = o;
+  }
+}
+
+// one wave per sorted row: dys[r] = bf16(w_r * dout[t]); dtopk_w[f] = <dout[t], yhat[r]>
+__global__ __launch_bounds__(256) void combine_bwd_kernel(const uint16_t* __restrict__ dout,
+                                                          const uint16_t* __restrict__ yhat,
+                                                          const int32_t* __restrict__ order,
+                                                          const int32_t* __restrict__ a_idx,
+                                                          const uint16_t* __restrict__ w_sorted, int64_t M, int k,
+                                                          int64_t d, uint16_t* __restrict__ dys,
+                                                          float* __restrict__ dtopk_w) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int nwaves = blockDim.x >> 6;
+  const int64_t nvec = d / 8;
+  for (int64_t r = (int64_t)blockIdx.x * nwaves + (threadIdx.x >> 6); r < M; r += (int64_t)gridDim.x * nwaves) {
+    const int64_t t = a_idx[r];
+    const float wr = bf2f(w_sorted[r]);
+    const uint4* go = reinterpret_cast<const uint4*>(dout + t * d);
+    const uint4* yh = reinterpret_cast<const uint4*>(yhat + r * d);
+    uint4* dy = reinterpret_cast<uint4*>(dys + r * d);
+    float acc = 0.0f;
+    for (int64_t c = lane; c < nvec; c += 64) {
+      const uint4 g = go[c], yv = yh[c];
+      const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, yw[4] = {yv.x, yv.y, yv.z, yv.w};
+      uint32_t ow[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float g0 = bf_lo(gw[q]), g1 = bf_hi(gw[q]);
+        acc = __fadd_rn(acc, __fmul_rn(g0, bf_lo(yw[q])));
+        acc = __fadd_rn(acc, __fmul_rn(g1, bf_hi(yw[q])));
+        ow[q] = pack_bf2(__fmul_rn(wr, g0), __fmul_rn(wr, g1));
+      }
+      dy[c] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+    }
+    acc = wave_sum_butterfly(acc);
+    if (lane == 0) dtopk_w[order[r]] = acc;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Router backward: dlogits per token (lanes over experts), then dwr = dlogits^T x by token chunks + fixed-order
+// reduction of the chunk partials.
+// ---------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void router_dlogits_kernel(const float* __restrict__ logits,
+                                                             const int32_t* __restrict__ ids,
+                                                             const float* __restrict__ dtw, int64_t T, int E, int k,
+                                                             int renorm, float scaling,
+                                                             float* __restrict__ dlogits) {
+  const int lane = threadIdx.x & 63;
+  const int nwaves = blockDim.x >> 6;
+  for (int64_t t = (int64_t)blockIdx.x * nwaves + (threadIdx.x >> 6); t < T; t += (int64_t)gridDim.x * nwaves) {
+    float lg[kRouteEPL];
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < kRouteEPL; ++i) {
+      lg[i] = -__builtin_inff();
+      if (i * 64 + lane < E) {
+        lg[i] = logits[t * E + i * 64 + lane];
+        m = fmaxf(m, lg[i]);
+      }
+    }
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
+    float ex[kRouteEPL];
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kRouteEPL; ++i) {
+      ex[i] = 0.0f;
+      if (i * 64 + lane < E) {
+        ex[i] = hexp(__fsub_rn(lg[i], m));
+        a = __fadd_rn(a, ex[i]);
+      }
+    }
+    const float S = wave_sum_butterfly(a);
+    float p[kRouteEPL];
+#pragma unroll
+    for (int i = 0; i < kRouteEPL; ++i) p[i] = __fdiv_rn(ex[i], S);
+    // selected probabilities and their upstream grads
+    float sp[kMaxK], dw[kMaxK];
+    int se[kMaxK];
+    float ssum = 0.0f, sdot = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) {
+      sp[j] = 0.0f;
+      dw[j] = 0.0f;
+      se[j] = -1;
+      if (j < k) {
+        se[j] = ids[t * k + j];
+        float mine = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kRouteEPL; ++i)
+          if (se[j] == i * 64 + lane) mine = p[i];
+        sp[j] = __shfl(mine, se[j] & 63, 64);
+        dw[j] = dtw[t * k + j] * scaling;
+        ssum += sp[j];
+        sdot += dw[j] * sp[j];
+      }
+    }
+    const float den = ssum + 1e-20f;
+    float dsel[kMaxK];
+    float pdp = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) {
+      dsel[j] = 0.0f;
+      if (j < k) {
+        dsel[j] = renorm ? dw[j] / den - sdot / (den * den) : dw[j];
+        pdp += sp[j] * dsel[j];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kRouteEPL; ++i) {
+      const int e = i * 64 + lane;
+      if (e < E) {
+        float dp = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kMaxK; ++j)
+          if (j < k && se[j] == e) dp += dsel[j];
+        dlogits[t * E + e] = p[i] * (dp - pdp);
+      }
+    }
+  }
+}
+
+constexpr int kRouterTC = 256;  // tokens per dwr partial chunk
+constexpr int kRouterEG = 8;    // experts per workgroup
+
+// grid (chunks, ceil(E / kRouterEG)); thread owns 8 consecutive columns (column blocks of 2048 in a loop)
+__global__ __launch_bounds__(256) void router_dwr_partial_kernel(const float* __restrict__ dlogits,
+                                                                 const uint16_t* __restrict__ x, int64_t ldx,
+                                                                 int64_t T, int E, int64_t d,
+                                                                 float* __restrict__ part) {
+  __shared__ float s_dl[kRouterTC][kRouterEG];
+  const int chunk = blockIdx.x, e0 = blockIdx.y * kRouterEG;
+  const int64_t t0 = (int64_t)chunk * kRouterTC;
+  const int64_t t1 = min(T, t0 + kRouterTC);
+  for (int i = threadIdx.x; i < kRouterTC * kRouterEG; i += blockDim.x) {
+    const int tt = i / kRouterEG, eg = i % kRouterEG;
+    s_dl[tt][eg] = (t0 + tt < t1 && e0 + eg < E) ? dlogits[(t0 + tt) * E + e0 + eg] : 0.0f;
+  }
+  __syncthreads();
+  for (int64_t col = (int64_t)threadIdx.x * 8; col < d; col += (int64_t)blockDim.x * 8) {
+    float acc[kRouterEG][8];
+#pragma unroll
+    for (int eg = 0; eg < kRouterEG; ++eg)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) acc[eg][q] = 0.0f;
+    for (int64_t t = t0; t < t1; ++t) {
+      const uint4 v = *reinterpret_cast<const uint4*>(x + t * ldx + col);
+      const float xv[8] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y),
+                           bf_lo(v.z), bf_hi(v.z), bf_lo(v.w), bf_hi(v.w)};
+#pragma unroll
+      for (int eg = 0; eg < kRouterEG; ++eg) {
+        const float g = s_dl[t - t0][eg];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc[eg][q] = __builtin_fmaf(g, xv[q], acc[eg][q]);
+      }
+    }
+#pragma unroll
+    for (int eg = 0; eg < kRouterEG; ++eg) {
+      if (e0 + eg >= E) break;
+      float4* dst = reinterpret_cast<float4*>(part + ((int64_t)chunk * E + e0 + eg) * d + col);
+      dst[0] = make_float4(acc[eg][0], acc[eg][1], acc[eg][2], acc[eg][3]);
+      dst[1] = make_float4(acc[eg][4], acc[eg][5], acc[eg][6], acc[eg][7]);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void router_dwr_reduce_kernel(const float* __restrict__ part, int nchunk, int E,
+                                                                int64_t d, void* __restrict__ dwr, int dwr_bf16) {
+  const int64_t total = (int64_t)E * d;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    float s = 0.0f;
+    for (int c = 0; c < nchunk; ++c) s += part[(int64_t)c * total + i];
+    if (dwr_bf16)
+      reinterpret_cast<uint16_t*>(dwr)[i] = (uint16_t)f2bf(s);
+    else
+      reinterpret_cast<float*>(dwr)[i] = s;
+  }
+}
+
+// dx[t] = bf16(sum_j dxs[inv_pos[t*k+j]] + sum_e dlogits[t,e] * wr[e]); one thread per 8 columns of a token
+template <bool F32>
+__global__ __launch_bounds__(256) void unpermute_bwd_kernel(const void* __restrict__ dxs,
+                                                            const int32_t* __restrict__ inv_pos,
+                                                            const float* __restrict__ dlogits,
+                                                            const uint16_t* __restrict__ wr, int64_t T, int k,
+                                                            int64_t d, int E, uint16_t* __restrict__ dx) {
+  const int64_t nvec = d / 8;
+  const int64_t total = T * nvec;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / nvec, c = i - t * nvec;
+    float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int j = 0; j < k; ++j) {
+      const int64_t r = inv_pos[t * k + j];
+      if constexpr (F32) {
+        const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(dxs) + r * d) + 2 * c;
+        const float4 v0 = src[0], v1 = src[1];
+        s[0] += v0.x;
+        s[1] += v0.y;
+        s[2] += v0.z;
+        s[3] += v0.w;
+        s[4] += v1.x;
+        s[5] += v1.y;
+        s[6] += v1.z;
+        s[7] += v1.w;
+      } else {
+        const uint4 v = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(dxs) + r * d)[c];
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          s[2 * q] += bf_lo(w[q]);
+          s[2 * q + 1] += bf_hi(w[q]);
+        }
+      }
+    }
+    if (dlogits) {
+      for (int e = 0; e < E; ++e) {
+        const float g = dlogits[t * E + e];
+        const uint4 v = reinterpret_cast<const uint4*>(wr + (int64_t)e * d)[c];
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          s[2 * q] = __builtin_fmaf(g, bf_lo(w[q]), s[2 * q]);
+          s[2 * q + 1] = __builtin_fmaf(g, bf_hi(w[q]), s[2 * q + 1]);
+        }
+      }
+    }
+    uint4 o;
+    o.x = pack_bf2(s[0], s[1]);
+    o.y = pack_bf2(s[2], s[3]);
+    o.z = pack_bf2(s[4], s[5]);
+    o.w = pack_bf2(s[6], s[7]);
+    reinterpret_cast<uint4*>(dx + t * d)[c] = o;
+  }
+}
+
+static inline int grid_for(int64_t work, int per_block, int cap = 8192) {
+  int64_t g = (work + per_block - 1) / per_block;
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return (int)g;
+}
+
+static inline bool al16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace hmoe
+
+using namespace hmoe;
+
+extern "C" {
+
+int hmoe_abi_version(void) { return HMOE_ABI_VERSION; }
+
+const char* hmoe_error_string(int code) {
+  switch (code) {
+    case HMOE_OK: return "ok";
+    case HMOE_ERR_ARG: return "invalid argument (null pointer, negative size or misaligned pointer / stride)";
+    case HMOE_ERR_SHAPE: return "unsupported shape";
+    case HMOE_ERR_DTYPE: return "unsupported element type";
+    case HMOE_ERR_LAUNCH: return "kernel launch failed";
+    case HMOE_ERR_WORKSPACE: return "workspace missing or too small";
+    case HMOE_ERR_DEVICE: return "device query failed";
+    default: return "unknown error";
+  }
+}
+
+int hmoe_route_topk(const void* x, int64_t ldx, const void* wr, const float* bias, int64_t T, int64_t d, int E,
+                    int k, int renorm, float scaling, float* logits, int32_t* topk_ids, float* topk_w,
+                    hmoe_stream_t stream) {
+  if (T < 0 || d <= 0 || E <= 0 || k <= 0) return HMOE_ERR_ARG;
+  if (T == 0) return HMOE_OK;
+  if (!x || !wr || !topk_ids || !topk_w) return HMOE_ERR_ARG;
+  if (E > kRouteMaxE || k > kMaxK || k > E || T > INT32_MAX) return HMOE_ERR_SHAPE;
+  if (d % 8 || ldx % 8 || ldx < d || !al16(x) || !al16(wr)) return HMOE_ERR_ARG;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int grid = grid_for(T, 4, 4096);
+  const int nch = (int)((d + 511) / 512);
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  const uint16_t* wp = static_cast<const uint16_t*>(wr);
+#define HMOE_ROUTE(NC)                                                                                          \
+  hipLaunchKernelGGL(route_topk_kernel<NC>, dim3(grid), dim3(256), 0, s, xp, ldx, wp, bias, (int)T, (int)d, E, k, \
+                     renorm, scaling, logits, topk_ids, topk_w)
+  if (nch <= 2)
+    HMOE_ROUTE(2);
+  else if (nch <= 4)
+    HMOE_ROUTE(4);
+  else if (nch <= 8)
+    HMOE_ROUTE(8);
+  else if (nch <= 16)
+    HMOE_ROUTE(16);
+  else
+    return HMOE_ERR_SHAPE;
+#undef HMOE_ROUTE
+  HMOE_CHECK_LAUNCH();
+  return HMOE_OK;
+}
+
+size_t hmoe_dispatch_workspace_size(int64_t T, int k, int E) {
+  const int64_t M = T * k;
+  const int64_t nblk = (M + kFPB - 1) / kFPB;
+  const size_t hist = (size_t)(nblk > 0 ? nblk : 1) * (size_t)E * 4;
+  const size_t rank = (size_t)(M > 0 ? M : 1) * 4;
+  return ((hist + 255) / 256) * 256 + ((rank + 255) / 256) * 256;
+}
+
+int hmoe_dispatch(const void* topk_ids, int ids_dtype, const void* topk_w, int w_dtype, int64_t T, int k, int E,
+                  const void* x, int64_t ldx, int64_t d, void* xs, int32_t* counts, int64_t* counts64,
+                  int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos, uint16_t* w_sorted,
+                  void* workspace, size_t workspace_bytes, hmoe_stream_t stream) {
+  if (T < 0 || k <= 0 || E <= 0) return HMOE_ERR_ARG;
+  if (E > kMaxEDispatch || k > kMaxK) return HMOE_ERR_SHAPE;
+  if (!counts || !starts) return HMOE_ERR_ARG;
+  if (ids_dtype != HMOE_DT_I32 && ids_dtype != HMOE_DT_I64) return HMOE_ERR_DTYPE;
+  if (topk_w && w_dtype != HMOE_DT_F32 && w_dtype != HMOE_DT_BF16) return HMOE_ERR_DTYPE;
+  if (w_sorted && !topk_w) return HMOE_ERR_ARG;
+  const int64_t M = T * k;
+  if (M > INT32_MAX) return HMOE_ERR_SHAPE;
+  if (xs && (!x || d <= 0 || d % 8 || ldx % 8 || ldx < d || !al16(x) || !al16(xs))) return HMOE_ERR_ARG;
+  if (workspace_bytes < hmoe_dispatch_workspace_size(T, k, E) || !workspace) return HMOE_ERR_WORKSPACE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t nblk = (M + kFPB - 1) / kFPB;
+  int32_t* hist = static_cast<int32_t*>(workspace);
+  const size_t hist_bytes = (((size_t)(nblk > 0 ? nblk : 1) * (size_t)E * 4 + 255) / 256) * 256;
+  int32_t* rank = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + hist_bytes);
+  int nbits = 0;
+  while ((1 << nbits) < E) ++nbits;
+  const int ids64 = ids_dtype == HMOE_DT_I64;
+  if (M > 0) {
+    hipLaunchKernelGGL(dispatch_hist_kernel, dim3((unsigned)nblk), dim3(64), 0, s, topk_ids, ids64, M, E, nbits,
+                       hist, rank);
+    HMOE_CHECK_LAUNCH();
+  }
+  hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(256), 0, s, hist, (int)nblk, E, counts, counts64, starts);
+  HMOE_CHECK_LAUNCH();
+  if (M > 0) {
+    if (!order) return HMOE_ERR_ARG;
+    const int grid = grid_for(T, 4, 8192);
+    hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(grid), dim3(256), 0, s, topk_ids, ids64, topk_w, w_dtype, T, k,
+                       E, hist, rank, static_cast<const uint16_t*>(x), ldx, d, static_cast<uint16_t*>(xs), order,
+                       a_idx, inv_pos, w_sorted);
+    HMOE_CHECK_LAUNCH();
+  }
+  return HMOE_OK;
+}
+
+int hmoe_make_schedule(const void* counts, int counts_dtype, int E, int64_t M, int block_m, int32_t* block_e,
+                       int32_t* block_row, int32_t* row_end, hmoe_stream_t stream) {
+  if (!counts || !block_e || !block_row || !row_end || E <= 0 || M < 0 || block_m <= 0) return HMOE_ERR_ARG;
+  if (E > kMaxEDispatch) return HMOE_ERR_SHAPE;
+  if (counts_dtype != HMOE_DT_I32 && counts_dtype != HMOE_DT_I64) return HMOE_ERR_DTYPE;
+  const int64_t nb = (M + block_m - 1) / block_m + E;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(make_schedule_kernel, dim3(grid_for(nb, 256, 1024)), dim3(256), 0, s, counts,
+                     counts_dtype == HMOE_DT_I64, E, nb, block_m, block_e, block_row, row_end);
+  HMOE_CHECK_LAUNCH();
+  return HMOE_OK;
+}
+
+int hmoe_combine(const void* y, int64_t T, int k, int64_t d, void* out, hmoe_stream_t stream) {
+  if (T < 0 || k <= 0 || d <= 0) return HMOE_ERR_ARG;
+  if (T == 0) return HMOE_OK;
+  if (!y || !out || d % 8 || !al16(y) || !al16(out)) return HMOE_ERR_ARG;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t work = T * (d / 8);
+  hipLaunchKernelGGL(combine_kernel, dim3(grid_for(work, 256, 65536)), dim3(256), 0, s,
+                     static_cast<const uint16_t*>(y), T, k, d, static_cast<uint16_t*>(out));
+  HMOE_CHECK_LAUNCH();
+  return HMOE_OK;
+}
+
+int hmoe_combine_bwd(const void* dout, const void* yhat, const int32_t* order, const int32_t* a_idx,
+                     const uint16_t* w_sorted, int64_t M, int k, int64_t d, void* dys, float* dtopk_w,
+                     hmoe_stream_t stream) {
+  if (M < 0 || k <= 0 || d <= 0) return HMOE_ERR_ARG;
+  if (M == 0) return HMOE_OK;
+  if (!dout || !yhat || !order || !a_idx || !w_sorted || !dys || !dtopk_w) return HMOE_ERR_ARG;
+  if (d % 8 || !al16(dout) || !al16(yhat) || !al16(dys)) return HMOE_ERR_ARG;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(combine_bwd_kernel, dim3(grid_for(M, 4, 16384)), dim3(256), 0, s,
+                     static_cast<const uint16_t*>(dout), static_cast<const uint16_t*>(yhat), order, a_idx, w_sorted,
+                     M, k, d, static_cast<uint16_t*>(dys), dtopk_w);
+  HMOE_CHECK_LAUNCH();
+  return HMOE_OK;
+}
+
+size_t hmoe_router_bwd_workspace_size(int64_t T, int E, int64_t d) {
+  const int64_t nchunk = (T + kRouterTC - 1) / kRouterTC;
+  return (size_t)(nchunk > 0 ? nchunk : 1) * (size_t)E * (size_t)d * 4;
+}
+
+int hmoe_router_bwd(const float* logits, const int32_t* topk_ids, const float* dtopk_w, int64_t T, int E, int k,
+                    int renorm, float scaling, const void* x, int64_t ldx, int64_t d, float* dlogits, void* dwr,
+                    int dwr_dtype, void* workspace, size_t workspace_bytes, hmoe_stream_t stream) {
+  if (T < 0 || E <= 0 || k <= 0 || d <= 0) return HMOE_ERR_ARG;
+  if (E > kRouteMaxE || k > kMaxK) return HMOE_ERR_SHAPE;
+  if (!logits || !topk_ids || !dtopk_w || !dlogits) return HMOE_ERR_ARG;
+  if (dwr && dwr_dtype != HMOE_DT_F32 && dwr_dtype != HMOE_DT_BF16) return HMOE_ERR_DTYPE;
+  if (dwr && (!x || d % 8 || ldx % 8 || !al16(x))) return HMOE_ERR_ARG;
+  if (dwr && (!workspace || workspace_bytes < hmoe_router_bwd_workspace_size(T, E, d))) return HMOE_ERR_WORKSPACE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (T > 0) {
+    hipLaunchKernelGGL(router_dlogits_kernel, dim3(grid_for(T, 4, 8192)), dim3(256), 0, s, logits, topk_ids,
+                       dtopk_w, T, E, k, renorm, scaling, dlogits);
+    HMOE_CHECK_LAUNCH();
+  }
+  if (dwr) {
+    const int nchunk = (int)((T + kRouterTC - 1) / kRouterTC);
+    float* part = static_cast<float*>(workspace);
+    if (nchunk > 0) {
+      hipLaunchKernelGGL(router_dwr_partial_kernel, dim3(nchunk, (E + kRouterEG - 1) / kRouterEG), dim3(256), 0, s,
+                         dlogits, static_cast<const uint16_t*>(x), ldx, T, E, d, part);
+      HMOE_CHECK_LAUNCH();
+    }
+    hipLaunchKernelGGL(router_dwr_reduce_kernel, dim3(grid_for((int64_t)E * d, 256, 4096)), dim3(256), 0, s, part,
+                       nchunk, E, d, dwr, dwr_dtype == HMOE_DT_BF16);
+    HMOE_CHECK_LAUNCH();
+  }
+  return HMOE_OK;
+}
+
+int hmoe_unpermute_bwd(const void* dxs, int dxs_dtype, const int32_t* inv_pos, const float* dlogits, const void* wr,
+                       int64_t T, int k, int64_t d, int E, void* dx, hmoe_stream_t stream) {
+  if (T < 0 || k <= 0 || d <= 0) return HMOE_ERR_ARG;
+  if (T == 0) return HMOE_OK;
+  if (dxs_dtype != HMOE_DT_BF16 && dxs_dtype != HMOE_DT_F32) return HMOE_ERR_DTYPE;
+  if (!dxs || !inv_pos || !dx || d % 8 || !al16(dxs) || !al16(dx)) return HMOE_ERR_ARG;
+  if (dlogits && (!wr || E <= 0 || !al16(wr))) return HMOE_ERR_ARG;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t work = T * (d / 8);
+  if (dxs_dtype == HMOE_DT_F32)
+    hipLaunchKernelGGL(unpermute_bwd_kernel<true>, dim3(grid_for(work, 256, 65536)), dim3(256), 0, s, dxs, inv_pos,
+                       dlogits, static_cast<const uint16_t*>(wr), T, k, d, E, static_cast<uint16_t*>(dx));
+  else
+    hipLaunchKernelGGL(unpermute_bwd_kernel<false>, dim3(grid_for(work, 256, 65536)), dim3(256), 0, s, dxs, inv_pos,
+                       dlogits, static_cast<const uint16_t*>(wr), T, k, d, E, static_cast<uint16_t*>(dx));
+  HMOE_CHECK_LAUNCH();
+  return HMOE_OK;
+}
+
+}  // extern "C"

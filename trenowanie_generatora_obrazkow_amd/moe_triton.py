@@ -1,0 +1,51 @@
+"""Drop-in for the reference's aurora/moe_triton.py: the same names and call signatures (BLOCK_M, m_bucket,
+make_schedule, grouped_mm), served by hand-written gfx950 HIP kernels through the hmoe C ABI (no Triton).
+
+    y[rows of e] = a[rows of e] @ w[e]   (grouped over experts in one persistent launch)
+
+with the reference's fused extras: gather of A rows (a_idx), per-row scale (routing weight), scatter of Y rows
+(y_idx); fp32 accumulation and one rounding to a.dtype on store (aurora/moe_triton.py:22-56).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import ops
+
+BLOCK_M = 64  # aurora/moe_triton.py:13 -- the row granularity of make_schedule's blocks
+
+
+def m_bucket(M: int, E: int) -> int:
+    """aurora/moe_triton.py:59-62: rows per expert rounded up to a power of two, clamped to [16, 1024].  The HIP
+    kernels do not autotune per call; the value is kept for callers that key caches on it."""
+    v = max(1, M // E)
+    p = 1 << (v - 1).bit_length()
+    return min(1024, max(16, p))
+
+
+def make_schedule(counts: torch.Tensor, M: int):
+    """aurora/moe_triton.py:93-107: per BLOCK_M-row block of the ceil(M/BLOCK_M)+E upper-bound grid, (expert or -1,
+    first row, end row of that expert) as int32 tensors on counts.device, computed on the device (no host sync)."""
+    return ops.make_schedule(counts, M, BLOCK_M)
+
+
+def grouped_mm(a: torch.Tensor, w: torch.Tensor, counts: torch.Tensor, sched=None, a_idx=None, y_idx=None,
+               scale=None, w_scale=None) -> torch.Tensor:
+    """aurora/moe_triton.py:65-90.  a (M, K) sorted by expert -- or the unsorted token matrix when a_idx (M,) int32
+    names the row to read --, w (E, K, N) with contiguous rows, counts (E,) rows per expert (sum = M) -> (M, N) of
+    a.dtype.  scale[r] multiplies output row r; y_idx[r] is where row r is written.  `sched` (make_schedule's
+    output) is accepted for call compatibility; the kernel derives its own tile map from `counts` on the device.
+    w may not be int8 (w_scale): that variant is not implemented in this build."""
+    M = a_idx.numel() if a_idx is not None else a.shape[0]
+    assert w.stride(2) == 1, "w must be (E, K, N) with contiguous rows"
+    if w_scale is not None:
+        raise NotImplementedError("int8 expert weights (w_scale) are not supported by the hmoe kernels yet")
+    if a.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise TypeError(f"hmoe grouped_mm supports bf16 a and w (got {a.dtype}, {w.dtype})")
+    a = a.contiguous()
+    if a_idx is not None and a_idx.dtype != torch.int32:
+        a_idx = a_idx.to(torch.int32)
+    if y_idx is not None and y_idx.dtype != torch.int32:
+        y_idx = y_idx.to(torch.int32)
+    return ops.grouped_mm(a, w, counts, M, a_idx=a_idx.contiguous() if a_idx is not None else None,
+                          y_idx=y_idx.contiguous() if y_idx is not None else None, scale=scale)

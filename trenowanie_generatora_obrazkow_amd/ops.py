@@ -1,0 +1,257 @@
+"""Tensor-level wrappers of the hmoe C entry points.  Each allocates its outputs with torch (caching allocator),
+validates layouts, and launches on the current stream of the tensors' device.  GPU tensors only."""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib as L
+
+
+def _dev_stream(t):
+    L.require_gpu(t, "input")
+    return L.stream(t.device)
+
+
+# Optional event probe: when `probe` is set to {op name: list}, each listed op records a (start, end) pair of
+# torch.cuda.Events on the stream its kernels are launched on (the current stream) around its C call.
+probe = None
+
+
+class _Probe:
+    def __init__(self, name):
+        self.name = name
+        self.ev = None
+
+    def __enter__(self):
+        if probe is not None and self.name in probe:
+            self.ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            self.ev[0].record()
+        return self
+
+    def __exit__(self, *exc):
+        if self.ev is not None:
+            self.ev[1].record()
+            probe[self.name].append(self.ev)
+        return False
+
+
+def _contig(t, name):
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t
+
+
+def route_topk(x: torch.Tensor, wr: torch.Tensor, k: int, bias=None, renorm=True, scaling=1.0, want_logits=True):
+    """Softmax top-k router -> (logits (T, E) fp32 or None, topk_ids (T, k) int32, topk_w (T, k) fp32)."""
+    T, d = x.shape
+    E = wr.shape[0]
+    if x.dtype != torch.bfloat16 or wr.dtype != torch.bfloat16:
+        raise TypeError("router expects bf16 x and weight")
+    if x.stride(1) != 1:
+        raise ValueError("x rows must be contiguous")
+    wr = _contig(wr, "router weight")
+    if bias is not None:
+        bias = _contig(bias.to(torch.float32), "bias")
+    s = _dev_stream(x)
+    logits = torch.empty(T, E, device=x.device, dtype=torch.float32) if want_logits else None
+    ids = torch.empty(T, k, device=x.device, dtype=torch.int32)
+    w = torch.empty(T, k, device=x.device, dtype=torch.float32)
+    with _Probe("route_topk"):
+        L.call("hmoe_route_topk", L.ptr(x), x.stride(0), L.ptr(wr), L.ptr(bias), T, d, E, k, int(bool(renorm)),
+               float(scaling), L.ptr(logits), L.ptr(ids), L.ptr(w), s)
+    return logits, ids, w
+
+
+@dataclass
+class Dispatch:
+    counts: torch.Tensor  # (E,) int32
+    counts64: torch.Tensor  # (E,) int64 or None
+    starts: torch.Tensor  # (E+1,) int32
+    order: torch.Tensor  # (M,) int32  (= y_idx)
+    a_idx: torch.Tensor  # (M,) int32
+    inv_pos: torch.Tensor  # (M,) int32
+    w_sorted: torch.Tensor  # (M,) bf16 or None
+    xs: torch.Tensor  # (M, d) bf16 or None
+
+
+def dispatch(topk_ids: torch.Tensor, E: int, topk_w=None, x=None, want_counts64=False, want_inv=True) -> Dispatch:
+    """Stable counting sort of the flat routed rows (aurora/hf_compat.py:69-72, 78, 80) and optionally the row
+    permutation xs = x[a_idx]."""
+    T, k = topk_ids.shape
+    M = T * k
+    dev = topk_ids.device
+    s = _dev_stream(topk_ids)
+    ids = _contig(topk_ids, "topk_ids")
+    if topk_w is not None:
+        topk_w = _contig(topk_w, "topk_weight")
+        if topk_w.dtype not in (torch.float32, torch.bfloat16):
+            topk_w = topk_w.float()
+    counts = torch.empty(E, device=dev, dtype=torch.int32)
+    counts64 = torch.empty(E, device=dev, dtype=torch.int64) if want_counts64 else None
+    starts = torch.empty(E + 1, device=dev, dtype=torch.int32)
+    order = torch.empty(M, device=dev, dtype=torch.int32)
+    a_idx = torch.empty(M, device=dev, dtype=torch.int32)
+    inv = torch.empty(M, device=dev, dtype=torch.int32) if want_inv else None
+    w_sorted = torch.empty(M, device=dev, dtype=torch.bfloat16) if topk_w is not None else None
+    xs = None
+    d = 0
+    ldx = 0
+    if x is not None:
+        if x.dtype != torch.bfloat16 or x.stride(1) != 1:
+            raise ValueError("x must be bf16 with contiguous rows")
+        d = x.shape[1]
+        ldx = x.stride(0)
+        xs = torch.empty(M, d, device=dev, dtype=torch.bfloat16)
+    ws_bytes = L.lib().hmoe_dispatch_workspace_size(T, k, E)
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+    with _Probe("dispatch"):
+        L.call("hmoe_dispatch", L.ptr(ids), L.dt(ids), L.ptr(topk_w), L.dt(topk_w) if topk_w is not None else 0, T, k, E,
+               L.ptr(x), ldx, d, L.ptr(xs), L.ptr(counts), L.ptr(counts64), L.ptr(starts), L.ptr(order), L.ptr(a_idx),
+               L.ptr(inv), L.ptr(w_sorted), L.ptr(ws), ws_bytes, s)
+    return Dispatch(counts, counts64, starts, order, a_idx, inv, w_sorted, xs)
+
+
+def make_schedule(counts: torch.Tensor, M: int, block_m: int = 64):
+    E = counts.numel()
+    nb = -(-M // block_m) + E
+    s = _dev_stream(counts)
+    counts = _contig(counts, "counts")
+    if counts.dtype not in (torch.int32, torch.int64):
+        counts = counts.to(torch.int64)
+    out = [torch.empty(nb, device=counts.device, dtype=torch.int32) for _ in range(3)]
+    with _Probe("make_schedule"):
+        L.call("hmoe_make_schedule", L.ptr(counts), L.dt(counts), E, M, block_m, *(L.ptr(o) for o in out), s)
+    return tuple(out)
+
+
+def _counts(counts):
+    counts = _contig(counts, "counts")
+    if counts.dtype not in (torch.int32, torch.int64):
+        counts = counts.to(torch.int64)
+    return counts
+
+
+def grouped_mm(a, w, counts, M, a_idx=None, y_idx=None, scale=None, w_scale=None, out=None):
+    E, K, N = w.shape
+    s = _dev_stream(a)
+    counts = _counts(counts)
+    if a.stride(1) != 1:
+        a = a.contiguous()
+    y = out if out is not None else torch.empty(M, N, device=a.device, dtype=a.dtype)
+    if scale is not None:
+        scale = _contig(scale, "scale")
+        if scale.dtype not in (torch.bfloat16, torch.float32):
+            scale = scale.float()
+    for t, n in ((a_idx, "a_idx"), (y_idx, "y_idx")):
+        if t is not None and (t.dtype != torch.int32 or not t.is_contiguous()):
+            raise ValueError(f"{n} must be contiguous int32")
+    with _Probe("grouped_mm"):
+        L.call("hmoe_grouped_mm", L.ptr(a), a.stride(0), L.dt(a), L.ptr(w), L.dt(w), E, K, N, w.stride(0), w.stride(1),
+               L.ptr(counts), L.dt(counts), M, L.ptr(a_idx), L.ptr(y_idx), L.ptr(scale),
+               L.dt(scale) if scale is not None else 0, L.ptr(w_scale), L.dt(w_scale) if w_scale is not None else 0,
+               L.ptr(y), y.stride(0), s)
+    return y
+
+
+def gate_up_swiglu(x, wgu, counts, M, a_idx=None, keep_gu=False):
+    E, d, h2 = wgu.shape
+    h = h2 // 2
+    s = _dev_stream(x)
+    wgu = _contig(wgu, "wgu")
+    counts = _counts(counts)
+    act = torch.empty(M, h, device=x.device, dtype=torch.bfloat16)
+    gu = torch.empty(M, h2, device=x.device, dtype=torch.bfloat16) if keep_gu else None
+    with _Probe("gate_up_swiglu"):
+        L.call("hmoe_gate_up_swiglu", L.ptr(x), x.stride(0), L.ptr(a_idx), L.ptr(wgu), E, d, h, L.ptr(counts),
+               L.dt(counts), M, L.ptr(act), L.ptr(gu), s)
+    return act, gu
+
+
+def down_scatter(act, wd, counts, M, w_sorted, y_idx, keep_yhat=False):
+    E, h, d = wd.shape
+    s = _dev_stream(act)
+    wd = _contig(wd, "wd")
+    counts = _counts(counts)
+    y = torch.empty(M, d, device=act.device, dtype=torch.bfloat16)
+    yhat = torch.empty(M, d, device=act.device, dtype=torch.bfloat16) if keep_yhat else None
+    with _Probe("down_scatter"):
+        L.call("hmoe_down_scatter", L.ptr(act), L.ptr(wd), E, h, d, L.ptr(counts), L.dt(counts), M, L.ptr(w_sorted),
+               L.ptr(y_idx), L.ptr(y), L.ptr(yhat), s)
+    return y, yhat
+
+
+def combine(y, T, k):
+    d = y.shape[1]
+    out = torch.empty(T, d, device=y.device, dtype=y.dtype)
+    with _Probe("combine"):
+        L.call("hmoe_combine", L.ptr(_contig(y, "y")), T, k, d, L.ptr(out), _dev_stream(y))
+    return out
+
+
+def combine_bwd(dout, yhat, disp: Dispatch, k):
+    M, d = yhat.shape
+    T = M // k
+    dout = dout.contiguous()
+    dys = torch.empty(M, d, device=dout.device, dtype=torch.bfloat16)
+    dtw = torch.empty(T, k, device=dout.device, dtype=torch.float32)
+    with _Probe("combine_bwd"):
+        L.call("hmoe_combine_bwd", L.ptr(dout), L.ptr(yhat), L.ptr(disp.order), L.ptr(disp.a_idx), L.ptr(disp.w_sorted),
+               M, k, d, L.ptr(dys), L.ptr(dtw), _dev_stream(dout))
+    return dys, dtw
+
+
+def down_dgrad_swiglu(dy, wd, counts, M, gu, a_idx=None, w_sorted=None):
+    """dgu (M, 2h) from the upstream gradient dy (T, d) gathered through a_idx (or sorted rows (M, d) when a_idx is
+    None) and scaled by w_sorted in fp32."""
+    E, h, d = wd.shape
+    dgu = torch.empty(M, 2 * h, device=dy.device, dtype=torch.bfloat16)
+    with _Probe("down_dgrad_swiglu"):
+        L.call("hmoe_down_dgrad_swiglu", L.ptr(dy), L.ptr(a_idx), L.ptr(w_sorted), L.ptr(wd), E, h, d, L.ptr(counts),
+               L.dt(counts), M, L.ptr(gu), L.ptr(dgu), _dev_stream(dy))
+    return dgu
+
+
+def gate_up_dgrad(dgu, wgu, counts, M, dtype=torch.float32):
+    E, d, h2 = wgu.shape
+    dxs = torch.empty(M, d, device=dgu.device, dtype=dtype)
+    with _Probe("gate_up_dgrad"):
+        L.call("hmoe_gate_up_dgrad", L.ptr(dgu), L.ptr(wgu), E, d, h2 // 2, L.ptr(counts), L.dt(counts), M, L.ptr(dxs),
+               L.dt(dxs), _dev_stream(dgu))
+    return dxs
+
+
+def grouped_wgrad(a, b, counts, E, dtype=torch.bfloat16):
+    M, P = a.shape
+    N = b.shape[1]
+    dw = torch.empty(E, P, N, device=a.device, dtype=dtype)
+    with _Probe("grouped_wgrad"):
+        L.call("hmoe_grouped_wgrad", L.ptr(a), a.stride(0), L.ptr(b), b.stride(0), E, P, N, L.ptr(counts), L.dt(counts), M,
+               L.ptr(dw), L.dt(dw), _dev_stream(a))
+    return dw
+
+
+def router_bwd(logits, ids, dtw, x, renorm=True, scaling=1.0, dwr_dtype=torch.float32, want_dwr=True):
+    T, E = logits.shape
+    k = ids.shape[1]
+    d = x.shape[1]
+    dl = torch.empty(T, E, device=logits.device, dtype=torch.float32)
+    dwr = torch.empty(E, d, device=logits.device, dtype=dwr_dtype) if want_dwr else None
+    ws_bytes = L.lib().hmoe_router_bwd_workspace_size(T, E, d) if want_dwr else 0
+    ws = torch.empty(max(ws_bytes, 1), device=logits.device, dtype=torch.uint8)
+    with _Probe("router_bwd"):
+        L.call("hmoe_router_bwd", L.ptr(logits), L.ptr(ids), L.ptr(dtw), T, E, k, int(bool(renorm)), float(scaling),
+               L.ptr(x), x.stride(0), d, L.ptr(dl), L.ptr(dwr), L.dt(dwr_dtype), L.ptr(ws) if want_dwr else None, ws_bytes,
+               _dev_stream(logits))
+    return dl, dwr
+
+
+def unpermute_bwd(dxs, inv_pos, T, k, dlogits=None, wr=None):
+    d = dxs.shape[1]
+    E = wr.shape[0] if wr is not None else 0
+    dx = torch.empty(T, d, device=dxs.device, dtype=torch.bfloat16)
+    with _Probe("unpermute_bwd"):
+        L.call("hmoe_unpermute_bwd", L.ptr(dxs), L.dt(dxs), L.ptr(inv_pos), L.ptr(dlogits), L.ptr(wr), T, k, d, E,
+               L.ptr(dx), _dev_stream(dxs))
+    return dx
