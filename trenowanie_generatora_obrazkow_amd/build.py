@@ -15,7 +15,7 @@ ARCH = os.environ.get("HMOE_ARCH", "gfx950")
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in generated code.
 HIPCC_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
-               "-packed-fp32-ops", "-Wall", "-Wno-unused-result", "-Wno-unused-variable", "-Wno-unused-but-set-variable"]
+               "-packed-fp32-ops", "-Wall", "-Wno-inline-asm", "-Wno-unused-result", "-Wno-unused-variable", "-Wno-unused-but-set-variable"]
 
 
 def _hipcc():

@@ -8,12 +8,14 @@
 // Both use a persistent grid: each workgroup walks tile ids blockIdx.x, +gridDim.x, ... up to a total computed on
 // the device from `counts`, so no host readback and no per-expert launch; empty experts own no m-tiles (MGROUP) or
 // produce zero tiles (KGROUP).  The block -> tile order is XCD-aware (the 8 XCDs get contiguous tile ranges) and
-// groups GROUP_M m-tiles per band so A rows and B columns are reused from the XCD's L2.
+// groups GM m-tiles per band so A rows and B columns are reused from the XCD's L2.
 //
-// Tiles are staged through LDS as [rows][64] bf16 (k contiguous, 16-byte chunks XOR-swizzled per row) in two
-// buffers: the next k-tile's global loads are in flight while MFMAs run on the current one, one barrier per k-tile.
-// Operands whose k index is strided in memory (weights stored (K, N) with N contiguous; the row-major activations
-// of a weight gradient) are loaded as 8x8 bf16 blocks and transposed in registers before the LDS store.
+// Data path: global memory -> LDS with global_load_lds_dwordx4 (no register staging) into an NSTAGE-deep ring of
+// BK = 32 k-slices, one barrier per slice; fragments come out of LDS with ds_read_b128 for tiles stored k-contiguous
+// and with ds_read_b64_tr_b16 (the gfx950 LDS transpose read) for tiles stored m/n-contiguous -- weights kept
+// (K, N) with N contiguous, and both operands of a weight gradient -- so no operand is ever transposed in
+// registers or in global memory.  Lanes whose source lies outside the operand (ragged expert ends, K / N tails)
+// read a zero page instead, so every LDS slot is written each slice.
 //
 // MFMA roles: the N-side tile feeds the MFMA "A" operand and the M-side tile the "B" operand, so each lane's
 // accumulator holds one output row and 4 consecutive output columns per group -> 8-byte bf16 / 16-byte fp32 stores.
@@ -21,127 +23,151 @@
 
 namespace hmoe {
 
-constexpr int kBK = 64;
-constexpr int kKCH = kBK / 8;  // 16-byte chunks per LDS row
+constexpr int kBK = 32;      // k per LDS slice
+constexpr int kNStage = 4;   // slices in flight
 constexpr int kMaxEGemm = 1024;
 
-__device__ __forceinline__ int lds_swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
-__device__ __forceinline__ int lds_idx(int row, int kc) { return row * kKCH + (kc ^ lds_swz(row)); }
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// Source of masked lanes' direct loads: 64 zero bytes.
+__device__ __attribute__((aligned(64))) uint16_t g_zero_page[32];
 
 template <int BM_, int BN_, int WM_, int WN_, int GM_>
 struct Cfg {
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, GM = GM_;
-  static constexpr int NT = WM * WN * 64;
+  static constexpr int NWAVES = WM * WN, NT = NWAVES * 64;
   static constexpr int TM = BM / WM, TN = BN / WN;
   static constexpr int FM = TM / 32, FN = TN / 32;
-  static constexpr int LDS_A = BM * kKCH, LDS_B = BN * kKCH;  // uint4 per stage
-  static constexpr int LDS_BYTES = 2 * (LDS_A + LDS_B) * 16;
+  // a wave's fragments are interleaved with the other waves' along each dimension: fragment f of wave w covers
+  // 32 rows / columns from f * FS + 32 w (FS = 32 * waves along that dimension)
+  static constexpr int FSM = 32 * WM, FSN = 32 * WN;
+  static constexpr int A_BYTES = BM * kBK * 2, B_BYTES = BN * kBK * 2;  // per slice
+  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  static constexpr int LDS_BYTES = kNStage * STAGE_BYTES;
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be a multiple of 32");
 };
 
 // ----------------------------------------------------------------------------------------------------------------
-// Operand loaders.  A loader owns a tile of ROWS rows (the M or N side) x 64 k; it is initialised per tile with
-// row / column pointers and masks, then load(k0) issues the global reads into registers and store() writes LDS.
+// LDS tile layouts (one k-slice of BK = 32)
+//   K-major  [ROWS][32]: 64-byte rows, four 16-byte chunks; chunk c of row r stored at c ^ ((r >> 2) & 3).
+//   MN-major [32][ROWS]: k-rows of 2*ROWS bytes, ROWS/8 chunks; the low 3 bits of chunk c in k-row k are XORed
+//            with ((2 * (k & 3)) | ((k >> 3) & 1)).
+// Both swizzles make the fragment reads below conflict-free (K-major) or close to it (transpose reads).
 // ----------------------------------------------------------------------------------------------------------------
+__device__ __forceinline__ int swz_k(int row) { return (row >> 2) & 3; }
+__device__ __forceinline__ int swz_mn(int k) { return ((2 * (k & 3)) | ((k >> 3) & 1)) & 7; }
+__device__ __forceinline__ int mn_chunk(int k, int c) { return (c & ~7) | ((c ^ swz_mn(k)) & 7); }
 
-// K-contiguous source: row p at base_p, elements k contiguous.
-template <int ROWS, int NT>
-struct LoadK {
-  static constexpr int PER = ROWS * kKCH / NT;
-  static_assert(ROWS * kKCH % NT == 0, "K loader: rows*8 must be a multiple of the thread count");
-  static constexpr int RSTEP = NT / kKCH;
-  const uint16_t* base[PER];
-  uint4 r[PER];
-  int kc, row0;
-  __device__ __forceinline__ void set_thread(int tid) {
-    kc = tid % kKCH;
-    row0 = tid / kKCH;
-  }
-  __device__ __forceinline__ int row(int i) const { return row0 + i * RSTEP; }
-  __device__ __forceinline__ void load(int k0, int K) {
-    const int kk = k0 + kc * 8;
+// Direct global -> LDS copy of 16 bytes per lane: lane l's bytes land at lds + 16 l (lds is wave-uniform; it goes
+// to M0).  Issued as inline asm so the compiler does not guard every later LDS read with a vmcnt(0) wait for it:
+// completion of these copies is tracked explicitly (wait_vm + barrier before a slice is read).
+__device__ __forceinline__ void g2lds(const uint16_t* src, char* lds) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(lds);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src) : "memory", "m0");
+}
+
+// K-major operand: ROWS rows x 32 k per slice; ROWS/16 copy instructions per slice (each 16 rows x 64 bytes),
+// spread over the workgroup's waves.
+template <int ROWS, int NWAVES>
+struct KTile {
+  static constexpr int INSTR = ROWS / 16;
+  static constexpr int PER_WAVE = INSTR / NWAVES;
+  static_assert(INSTR % NWAVES == 0, "K tile copy instructions must divide over the waves");
+  const uint16_t* rowp[PER_WAVE];  // row base (k = 0) of the row this lane copies, or the zero page
+  int chunk[PER_WAVE];             // logical k-chunk this lane copies
+  int K;
+  // lane l of instruction (wave w, i) fills LDS row 16*(w*PER_WAVE + i) + l/4, physical chunk l%4
+  __device__ __forceinline__ int row_of(int wave, int lane, int i) const { return 16 * (wave * PER_WAVE + i) + lane / 4; }
+  __device__ __forceinline__ void issue(char* lds_tile, int wave, int lane, int k0) const {
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      if (base[i] != nullptr && kk < K)
-        r[i] = *reinterpret_cast<const uint4*>(base[i] + kk);
-      else
-        r[i] = make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < PER_WAVE; ++i) {
+      const int kk = k0 + chunk[i] * 8;
+      const uint16_t* src = (rowp[i] != g_zero_page && kk < K) ? rowp[i] + kk : g_zero_page;
+      g2lds(src, lds_tile + (wave * PER_WAVE + i) * 1024);
     }
   }
-  __device__ __forceinline__ void store(uint4* lds) const {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) lds[lds_idx(row(i), kc)] = r[i];
+  // Lane part of a fragment read address: row w32*32 + lane%32, k-chunk lane/32 (ks = 0), swizzled.  The
+  // swizzle of row grp64 + w32*32 + lane%32 is that of lane%32, and chunk 2 + c stored at (2 + c) ^ s = (c ^ s) ^ 2,
+  // so the 64-row group and ks parts are compile-time offsets.
+  __device__ __forceinline__ static int lane_off(int w32, int lane) {
+    const int row = w32 * 32 + (lane & 31);
+    return row * 64 + (((lane >> 5) ^ swz_k(row)) * 16);
+  }
+  // MFMA operand fragment: 32 rows (grp64 + 32 w32 + lane%32) x 16 k (ks*16 + (lane/32)*8 + 0..7)
+  __device__ __forceinline__ static bf16x8 frag(const char* lds_tile, int grp64, int loff, int ks) {
+    return *reinterpret_cast<const bf16x8*>(lds_tile + grp64 * 64 + (loff ^ (ks * 32)));
   }
 };
 
-// MN-contiguous source: element (k, p) at col_p + k * ld (8 consecutive p per 16-byte load).  Each thread loads an
-// 8 (k) x 8 (p) block and transposes it in registers.
-template <int ROWS, int NT>
-struct LoadMN {
-  static constexpr int BLOCKS = (ROWS / 8) * kKCH;
-  static constexpr int PER = (BLOCKS + NT - 1) / NT;
-  const uint16_t* col[PER];  // pointer to (k = 0, p = first of the 8 columns); nullptr -> zeros
-  uint4 r[PER][8];
-  int kc[PER], ng[PER];
-  bool act[PER];
+// MN-major operand: 32 k-rows x ROWS columns per slice; ROWS/16 copy instructions (each 1 KB = 512/ROWS k-rows).
+template <int ROWS, int NWAVES>
+struct MNTile {
+  static constexpr int INSTR = ROWS / 16;
+  static constexpr int PER_WAVE = INSTR / NWAVES;
+  static constexpr int CPR = ROWS / 8;      // 16-byte chunks per k-row
+  static constexpr int KPI = 64 / CPR;      // k-rows per copy instruction
+  static_assert(INSTR % NWAVES == 0, "MN tile copy instructions must divide over the waves");
+  const uint16_t* colp[PER_WAVE];  // (k = 0, first of the 8 columns) of the chunk this lane copies, or zero page
+  int krow[PER_WAVE];              // k-row within the slice
   int64_t ld;
-  __device__ __forceinline__ void set_thread(int tid) {
+  int Kvalid;
+  __device__ __forceinline__ void issue(char* lds_tile, int wave, int lane, int k0) const {
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int q = tid + i * NT;
-      act[i] = q < BLOCKS;
-      kc[i] = q % kKCH;
-      ng[i] = q / kKCH;
+    for (int i = 0; i < PER_WAVE; ++i) {
+      const int k = k0 + krow[i];
+      const uint16_t* src = (colp[i] != g_zero_page && k < Kvalid) ? colp[i] + (int64_t)k * ld : g_zero_page;
+      g2lds(src, lds_tile + (wave * PER_WAVE + i) * 1024);
     }
   }
-  __device__ __forceinline__ void load(int k0, int Kvalid) {
+  // lane l of instruction (wave w, i): k-row (w*PER_WAVE + i)*KPI + l / CPR, physical chunk l % CPR
+  __device__ __forceinline__ static void slot(int wave, int lane, int i, int& k, int& col) {
+    k = (wave * PER_WAVE + i) * KPI + lane / CPR;
+    col = mn_chunk(k, lane % CPR) * 8;  // the logical column this physical slot holds
+  }
+  // Lane part of a fragment read address (see frag): k-row (g/2)*8 + j, columns w32*32 + (g%2)*16 + 4a of the
+  // 64-column group, swizzled.  k & 3 = j and (k >> 3) & 1 = g / 2 for every (ks, hh), so the swizzle is a lane
+  // constant and the (ks, hh, 64-column group) parts of the address are compile-time offsets.
+  __device__ __forceinline__ static int lane_off(int w32, int lane) {
+    const int g = lane >> 4, j = (lane >> 2) & 3, a = lane & 3;
+    const int k = (g >> 1) * 8 + j;
+    const int c = w32 * 4 + (g & 1) * 2 + (a >> 1);  // chunk within the 64-column group, 0..7
+    const int s = (2 * j) | (g >> 1);                 // swz_mn(k) for every k this lane reads
+    return k * (ROWS * 2) + ((c ^ s) & 7) * 16 + (a & 1) * 8;
+  }
+  // MFMA operand fragment via two transpose reads: 32 columns (grp64 + 32 w32 + lane%32) x 16 k
+  // (ks*16 + (lane/32)*8 + 0..7); `loff` = lane_off(w32, lane).
+  __device__ __forceinline__ static bf16x8 frag(const char* lds_tile, int grp64, int loff, int ks) {
+    s16x4 h[2];
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        const int krow = k0 + kc[i] * 8 + kk;
-        if (act[i] && col[i] != nullptr && krow < Kvalid)
-          r[i][kk] = *reinterpret_cast<const uint4*>(col[i] + (int64_t)krow * ld);
-        else
-          r[i][kk] = make_uint4(0, 0, 0, 0);
-      }
+    for (int hh = 0; hh < 2; ++hh) {
+      const char* p = lds_tile + loff + (ks * 16 + 4 * hh) * (ROWS * 2) + grp64 * 2;
+      h[hh] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
     }
-  }
-  __device__ __forceinline__ static uint32_t w(const uint4& v, int j) {
-    return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w;
-  }
-  __device__ __forceinline__ static uint32_t pk(uint32_t lo_src, uint32_t hi_src, bool odd) {
-    return odd ? ((lo_src >> 16) | (hi_src & 0xffff0000u)) : ((lo_src & 0xffffu) | (hi_src << 16));
-  }
-  __device__ __forceinline__ void store(uint4* lds) const {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      if (!act[i]) continue;
-#pragma unroll
-      for (int nn = 0; nn < 8; ++nn) {
-        const int j = nn >> 1;
-        const bool odd = nn & 1;
-        uint4 o;
-        o.x = pk(w(r[i][0], j), w(r[i][1], j), odd);
-        o.y = pk(w(r[i][2], j), w(r[i][3], j), odd);
-        o.z = pk(w(r[i][4], j), w(r[i][5], j), odd);
-        o.w = pk(w(r[i][6], j), w(r[i][7], j), odd);
-        lds[lds_idx(ng[i] * 8 + nn, kc[i])] = o;
-      }
-    }
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    const s16x8 v = __builtin_shufflevector(h[0], h[1], 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(bf16x8, v);
   }
 };
 
-template <bool MN, int ROWS, int NT>
-struct LoaderSel;
-template <int ROWS, int NT>
-struct LoaderSel<false, ROWS, NT> {
-  using type = LoadK<ROWS, NT>;
+template <bool MN, int ROWS, int NWAVES>
+struct TileSel;
+template <int ROWS, int NWAVES>
+struct TileSel<false, ROWS, NWAVES> {
+  using type = KTile<ROWS, NWAVES>;
 };
-template <int ROWS, int NT>
-struct LoaderSel<true, ROWS, NT> {
-  using type = LoadMN<ROWS, NT>;
+template <int ROWS, int NWAVES>
+struct TileSel<true, ROWS, NWAVES> {
+  using type = MNTile<ROWS, NWAVES>;
 };
+
+// wait until at most N vector-memory operations of this thread are outstanding (s_waitcnt vmcnt(N); the
+// expcnt / lgkmcnt fields are left at their maxima so they do not wait)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 
 // ----------------------------------------------------------------------------------------------------------------
 // Kernel parameters
@@ -155,7 +181,7 @@ struct GemmParams {
   const uint16_t* A;
   int64_t lda;
   const int32_t* a_idx;
-  // N side (B).  MGROUP: weights of expert e at B + e*strideBe; b_mn: element (k, n) at k*ldb + n, else n*ldb + k.
+  // N side (B).  MGROUP: weights of expert e at B + e*strideBe; B_MN: element (k, n) at k*ldb + n, else n*ldb + k.
   //              KGROUP: Y (M, N) with N contiguous, row stride ldb.
   const uint16_t* B;
   int64_t ldb, strideBe;
@@ -171,9 +197,9 @@ struct GemmParams {
   // epilogue
   void* C;  // EPI_STORE: y; EPI_SWIGLU: act (M, h); EPI_SWIGLU_BWD: dgu (M, 2h); EPI_WGRAD: dw (E, P, N)
   int64_t ldc, strideCe;
-  int c_f32;                // EPI_WGRAD: fp32 output
+  int c_f32;                // EPI_WGRAD / EPI_STORE: fp32 output
   const int32_t* y_idx;     // EPI_STORE scatter
-  const void* scale;        // EPI_STORE per-row scale
+  const void* scale;        // EPI_STORE / EPI_SWIGLU_BWD per-row scale
   int scale_f32;
   uint16_t* aux;            // EPI_STORE: yhat (unscaled, sorted); EPI_SWIGLU: gu store
   const uint16_t* gu_in;    // EPI_SWIGLU_BWD: [g | u]
@@ -184,15 +210,13 @@ struct GemmParams {
 // ----------------------------------------------------------------------------------------------------------------
 template <class C, int MODE, bool A_MN, bool B_MN, int EPI>
 __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
-  extern __shared__ uint4 smem[];
-  uint4* As = smem;                      // [2][LDS_A]
-  uint4* Bs = smem + 2 * C::LDS_A;       // [2][LDS_B]
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
   __shared__ int64_t s_rstart[kMaxEGemm + 1];
   __shared__ int s_tstart[kMaxEGemm + 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / C::WN, wn = wave % C::WN;
   const int E = p.E;
 
@@ -250,10 +274,11 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
   const int total_m = MODE == MGROUP ? s_tstart[E] : E * nb_i;
   const int total = total_m * nb_n;
 
-  typename LoaderSel<A_MN, C::BM, C::NT>::type la;
-  typename LoaderSel<B_MN, C::BN, C::NT>::type lb;
-  la.set_thread(tid);
-  lb.set_thread(tid);
+  typename TileSel<A_MN, C::BM, C::NWAVES>::type ta;
+  typename TileSel<B_MN, C::BN, C::NWAVES>::type tb;
+  static_assert(C::FSM == 64 && C::FSN == 64, "fragment reads assume two waves along each tile dimension");
+  const int loff_a = decltype(ta)::lane_off(wm, lane);
+  const int loff_b = decltype(tb)::lane_off(wn, lane);
 
   // XCD-aware slot: consecutive workgroup ids are dealt round-robin over the 8 XCDs; give each XCD a contiguous
   // range of tile ids so the tiles it runs share A rows and B columns in its L2.
@@ -288,7 +313,6 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
           hi = mid;
       }
       e = lo;
-      while (e + 1 < E && s_tstart[e + 1] <= mt) ++e;
       row0 = s_rstart[e] + (int64_t)(mt - s_tstart[e]) * C::BM;
       row_end = min(s_rstart[e + 1], p.M);
     } else {
@@ -300,26 +324,27 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
     }
     const int n0 = nb * (EPI == EPI_SWIGLU ? C::BN / 2 : C::BN);
 
-    // ---- operand pointers ----
+    // ---- copy sources for this tile ----
     if constexpr (MODE == MGROUP) {
-      // A: K-contiguous rows (gathered or sorted)
       static_assert(!A_MN, "MGROUP A is K-contiguous");
+      ta.K = p.K;
 #pragma unroll
-      for (int i = 0; i < la.PER; ++i) {
-        const int64_t r = row0 + la.row(i);
-        const uint16_t* ptr = nullptr;
+      for (int i = 0; i < ta.PER_WAVE; ++i) {
+        const int rr = ta.row_of(wave, lane, i);
+        const int64_t r = row0 + rr;
+        const uint16_t* ptr = g_zero_page;
         if (r < row_end) {
           const int64_t src = p.a_idx ? (int64_t)p.a_idx[r] : r;
           ptr = p.A + src * p.lda;
         }
-        la.base[i] = ptr;
+        ta.rowp[i] = ptr;
+        ta.chunk[i] = (lane & 3) ^ swz_k(rr);
       }
       const uint16_t* Be = p.B + (int64_t)e * p.strideBe;
       auto gcol = [&](int nn, int& col) -> bool {  // tile column -> weight column
         if (EPI == EPI_SWIGLU) {
-          const int wnn = nn / C::TN, c = nn % C::TN;
-          const int half = c / (C::TN / 2), j = c % (C::TN / 2);
-          const int ac = n0 + wnn * (C::TN / 2) + j;
+          const int half = nn / (C::BN / 2);  // tile columns [0, BN/2) gate, [BN/2, BN) the matching up
+          const int ac = n0 + nn % (C::BN / 2);
           col = half * p.h + ac;
           return ac < p.N;
         } else {
@@ -328,38 +353,48 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
         }
       };
       if constexpr (B_MN) {
-        lb.ld = p.ldb;
+        tb.ld = p.ldb;
+        tb.Kvalid = p.K;
 #pragma unroll
-        for (int i = 0; i < lb.PER; ++i) {
-          int col;
-          const bool ok = gcol(lb.ng[i] * 8, col);
-          lb.col[i] = ok ? Be + col : nullptr;
+        for (int i = 0; i < tb.PER_WAVE; ++i) {
+          int k, nn, col;
+          tb.slot(wave, lane, i, k, nn);
+          tb.krow[i] = k;
+          tb.colp[i] = gcol(nn, col) ? Be + col : g_zero_page;
         }
       } else {
+        tb.K = p.K;
 #pragma unroll
-        for (int i = 0; i < lb.PER; ++i) {
+        for (int i = 0; i < tb.PER_WAVE; ++i) {
+          const int nn = tb.row_of(wave, lane, i);
           int col;
-          const bool ok = gcol(lb.row(i), col);
-          lb.base[i] = ok ? Be + (int64_t)col * p.ldb : nullptr;
+          tb.rowp[i] = gcol(nn, col) ? Be + (int64_t)col * p.ldb : g_zero_page;
+          tb.chunk[i] = (lane & 3) ^ swz_k(nn);
         }
       }
     } else {
       static_assert(A_MN && B_MN, "KGROUP operands are MN-contiguous");
-      la.ld = p.lda;
-      lb.ld = p.ldb;
+      ta.ld = p.lda;
+      ta.Kvalid = kvalid;
+      tb.ld = p.ldb;
+      tb.Kvalid = kvalid;
 #pragma unroll
-      for (int i = 0; i < la.PER; ++i) {
-        const int ic = i0 + la.ng[i] * 8;
-        la.col[i] = ic < p.P ? p.A + kstart * p.lda + ic : nullptr;
+      for (int i = 0; i < ta.PER_WAVE; ++i) {
+        int k, ic;
+        ta.slot(wave, lane, i, k, ic);
+        ta.krow[i] = k;
+        ta.colp[i] = (i0 + ic < p.P) ? p.A + kstart * p.lda + i0 + ic : g_zero_page;
       }
 #pragma unroll
-      for (int i = 0; i < lb.PER; ++i) {
-        const int nc = n0 + lb.ng[i] * 8;
-        lb.col[i] = nc < p.N ? p.B + kstart * p.ldb + nc : nullptr;
+      for (int i = 0; i < tb.PER_WAVE; ++i) {
+        int k, nc;
+        tb.slot(wave, lane, i, k, nc);
+        tb.krow[i] = k;
+        tb.colp[i] = (n0 + nc < p.N) ? p.B + kstart * p.ldb + n0 + nc : g_zero_page;
       }
     }
 
-    // ---- main loop ----
+    // ---- main loop: NSTAGE-deep ring of k-slices ----
     f32x16 acc[C::FM][C::FN];
 #pragma unroll
     for (int a = 0; a < C::FM; ++a)
@@ -368,169 +403,240 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
 
+    constexpr int LOADS = decltype(ta)::PER_WAVE + decltype(tb)::PER_WAVE;  // direct loads per thread per slice
     const int nk = (kvalid + kBK - 1) / kBK;
-    if (nk > 0) {
-      la.load(0, kvalid);
-      lb.load(0, kvalid);
-      la.store(As);
-      lb.store(Bs);
-      __syncthreads();
-      for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) {
-          la.load((kt + 1) * kBK, kvalid);
-          lb.load((kt + 1) * kBK, kvalid);
-        }
-        const uint4* Ac = As + cur * C::LDS_A;
-        const uint4* Bc = Bs + cur * C::LDS_B;
+    char* const ring_end = smem + C::LDS_BYTES;
+    char* fill = smem;        // next ring slot to fill
+    const char* cons = smem;  // ring slot consumed by the current slice
+    auto issue = [&](int kslice) {
+      ta.issue(fill, wave, lane, kslice * kBK);
+      tb.issue(fill + C::A_BYTES, wave, lane, kslice * kBK);
+      fill += C::STAGE_BYTES;
+      if (fill == ring_end) fill = smem;
+    };
+    // Fragment-level software pipeline over the ring (two k16 steps per slice):
+    //   iteration kt:  read ks1 fragments of slice kt      | MFMAs on ks0 fragments of slice kt
+    //                  wait for slice kt+1, barrier, refill the slot of slice kt with slice kt+4
+    //                  read ks0 fragments of slice kt+1    | MFMAs on ks1 fragments of slice kt
+    // The barrier comes after every wave has read all of slice kt, so its slot can be refilled at once: four
+    // slices are in flight while one is consumed, and LDS read latency hides under the MFMAs.
+    typedef typename TileSel<A_MN, C::BM, C::NWAVES>::type TA;
+    typedef typename TileSel<B_MN, C::BN, C::NWAVES>::type TB;
+    constexpr int RD = C::FM * (A_MN ? 2 : 1) + C::FN * (B_MN ? 2 : 1);  // LDS reads per k16 step
+    constexpr int NMF = C::FM * C::FN;                                     // MFMAs per k16 step
+    constexpr int PAIRS = RD < NMF ? RD : NMF;
+    struct Frags {
+      bf16x8 xa[C::FM], wb[C::FN];
+    };
+    auto read = [&](const char* slot, int ks) {
+      Frags f;
 #pragma unroll
-        for (int ks = 0; ks < kBK / 16; ++ks) {
-          const int kc = ks * 2 + (lane >> 5);
-          bf16x8 xa[C::FM], wb[C::FN];
+      for (int a = 0; a < C::FM; ++a) f.xa[a] = TA::frag(slot, a * C::FSM, loff_a, ks);
 #pragma unroll
-          for (int a = 0; a < C::FM; ++a) {
-            const uint4 v = Ac[lds_idx(wm * C::TM + a * 32 + (lane & 31), kc)];
-            xa[a] = __builtin_bit_cast(bf16x8, v);
-          }
+      for (int b = 0; b < C::FN; ++b) f.wb[b] = TB::frag(slot + C::A_BYTES, b * C::FSN, loff_b, ks);
+      return f;
+    };
+    auto mfmas = [&](const Frags f) {
 #pragma unroll
-          for (int b = 0; b < C::FN; ++b) {
-            const uint4 v = Bc[lds_idx(wn * C::TN + b * 32 + (lane & 31), kc)];
-            wb[b] = __builtin_bit_cast(bf16x8, v);
-          }
+      for (int a = 0; a < C::FM; ++a)
 #pragma unroll
-          for (int a = 0; a < C::FM; ++a)
+        for (int b = 0; b < C::FN; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.wb[b], f.xa[a], acc[a][b], 0, 0, 0);
+    };
+    // one LDS read after each MFMA while both last, then whichever is left
+    auto interleave = [&]() {
 #pragma unroll
-            for (int b = 0; b < C::FN; ++b)
-              acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wb[b], xa[a], acc[a][b], 0, 0, 0);
-        }
-        if (kt + 1 < nk) {
-          la.store(As + (cur ^ 1) * C::LDS_A);
-          lb.store(Bs + (cur ^ 1) * C::LDS_B);
-        }
-        __syncthreads();
+      for (int i = 0; i < PAIRS; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
       }
+      if constexpr (NMF > PAIRS) __builtin_amdgcn_sched_group_barrier(0x008, NMF - PAIRS, 0);
+      if constexpr (RD > PAIRS) __builtin_amdgcn_sched_group_barrier(0x100, RD - PAIRS, 0);
+    };
+    static_assert(kNStage == 4 && kBK == 32, "pipeline written for a 4-deep ring of two-step slices");
+#pragma unroll
+    for (int s = 0; s < kNStage; ++s)
+      if (s < nk) issue(s);
+    Frags f0 = {}, f1 = {};
+    if (nk > 0) {
+      const int ahead = min(nk - 1, kNStage - 1);  // slices issued after slice 0
+      if (ahead >= 3)
+        wait_vm<3 * LOADS>();
+      else if (ahead == 2)
+        wait_vm<2 * LOADS>();
+      else if (ahead == 1)
+        wait_vm<LOADS>();
+      else
+        wait_vm<0>();
+      __syncthreads();
+      f0 = read(cons, 0);
     }
+    // The two MFMA blocks are unconditional (a conditional copy would split the accumulators' live ranges); on the
+    // last slice the ks0 read of the "next" slot reads stale LDS that is never used.
+    for (int kt = 0; kt < nk; ++kt) {
+      f1 = read(cons, 1);
+      mfmas(f0);
+      interleave();
+      const int ahead = min(nk - 1, kt + kNStage - 1) - (kt + 1);  // slices issued after slice kt+1
+      if (ahead >= 2)
+        wait_vm<2 * LOADS>();
+      else if (ahead == 1)
+        wait_vm<LOADS>();
+      else
+        wait_vm<0>();
+      __syncthreads();
+      if (kt + kNStage < nk) issue(kt + kNStage);  // into the slot of slice kt (fill == cons here)
+      cons += C::STAGE_BYTES;
+      if (cons == ring_end) cons = smem;
+      f0 = read(cons, 0);
+      mfmas(f1);
+      interleave();
+    }
+    __syncthreads();  // every wave is done with the ring before the epilogue reuses it
 
-    // ---- epilogue ----
-    // lane holds, for fragment (a, b) and group g: row m = wm*TM + a*32 + (lane&31), columns
-    // n = wn*TN + b*32 + 8g + 4*(lane>>5) + {0..3}
+    // ---- epilogue, through LDS in bands of 64 rows ----
+    // Pass a: every wave parks its fragment row a (rows a*64 + wm*32 + 0..31 of the tile, all its columns) in LDS
+    // as fp32 [64][BN + 4] (the padding makes both phases' 16-byte accesses bank-conflict free), then the workgroup
+    // walks the band row-contiguously: thread t owns band row t/4 and the 8-column groups (t%4)*8 + 32m, so each
+    // global store is a 16- or 32-byte vector and four neighbouring threads cover 64 contiguous bytes of a row.
+    constexpr int EP = C::BN + 4;  // band row pitch, floats
+    static_assert(64 * EP * 4 <= C::LDS_BYTES, "epilogue band must fit in the ring");
+    float* band = reinterpret_cast<float*>(smem);
     const int lrow = lane & 31;
     const int lcol = 4 * (lane >> 5);
-    if constexpr (EPI == EPI_WGRAD) {
+    const int q = tid >> 2, s = tid & 3;
 #pragma unroll
-      for (int a = 0; a < C::FM; ++a) {
-        const int i = i0 + wm * C::TM + a * 32 + lrow;
-        if (i >= p.P) continue;
-        char* crow = reinterpret_cast<char*>(p.C) +
-                     ((int64_t)e * p.strideCe + (int64_t)i * p.ldc) * (p.c_f32 ? 4 : 2);
+    for (int a = 0; a < C::FM; ++a) {
+      // phase 1: park fragment row a
 #pragma unroll
-        for (int b = 0; b < C::FN; ++b)
+      for (int b = 0; b < C::FN; ++b)
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int n = n0 + wn * C::TN + b * 32 + 8 * g + lcol;
+        for (int g = 0; g < 4; ++g) {
+          float* dst = band + (wm * 32 + lrow) * EP + b * C::FSN + wn * 32 + 8 * g + lcol;
+          *reinterpret_cast<float4*>(dst) =
+              make_float4(acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2], acc[a][b][4 * g + 3]);
+        }
+      __syncthreads();
+      // phase 2: band row q, columns 32m + 8s + 0..7
+      const float* brow = band + q * EP + 8 * s;
+      auto ld8 = [&](int col, float* v) {
+        const float4 x0 = *reinterpret_cast<const float4*>(brow + col);
+        const float4 x1 = *reinterpret_cast<const float4*>(brow + col + 4);
+        v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+        v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+      };
+      auto pack8 = [](const float* v) {
+        return make_uint4(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]), pack_bf2(v[4], v[5]), pack_bf2(v[6], v[7]));
+      };
+      if constexpr (EPI == EPI_WGRAD) {
+        const int i = i0 + a * 64 + q;
+        if (i < p.P) {
+          char* crow = reinterpret_cast<char*>(p.C) + ((int64_t)e * p.strideCe + (int64_t)i * p.ldc) * (p.c_f32 ? 4 : 2);
+#pragma unroll
+          for (int m = 0; m < C::BN / 32; ++m) {
+            const int n = n0 + 32 * m + 8 * s;
             if (n >= p.N) continue;
-            const float v0 = acc[a][b][4 * g], v1 = acc[a][b][4 * g + 1], v2 = acc[a][b][4 * g + 2],
-                        v3 = acc[a][b][4 * g + 3];
-            if (p.c_f32)
-              *reinterpret_cast<float4*>(crow + (int64_t)n * 4) = make_float4(v0, v1, v2, v3);
-            else
-              *reinterpret_cast<uint2*>(crow + (int64_t)n * 2) = make_uint2(pack_bf2(v0, v1), pack_bf2(v2, v3));
+            float v[8];
+            ld8(32 * m, v);
+            if (p.c_f32) {
+              float4* d = reinterpret_cast<float4*>(crow + (int64_t)n * 4);
+              d[0] = make_float4(v[0], v[1], v[2], v[3]);
+              d[1] = make_float4(v[4], v[5], v[6], v[7]);
+            } else {
+              *reinterpret_cast<uint4*>(crow + (int64_t)n * 2) = pack8(v);
+            }
           }
-      }
-    } else if constexpr (EPI == EPI_STORE) {
+        }
+      } else if constexpr (EPI == EPI_STORE) {
+        const int64_t r = row0 + a * 64 + q;
+        if (r < row_end) {
+          float sc = 1.0f;
+          if (p.scale) sc = p.scale_f32 ? reinterpret_cast<const float*>(p.scale)[r]
+                                        : bf2f(reinterpret_cast<const uint16_t*>(p.scale)[r]);
+          const int64_t yr = p.y_idx ? (int64_t)p.y_idx[r] : r;
+          char* yrow = reinterpret_cast<char*>(p.C) + yr * p.ldc * (p.c_f32 ? 4 : 2);
 #pragma unroll
-      for (int a = 0; a < C::FM; ++a) {
-        const int64_t r = row0 + wm * C::TM + a * 32 + lrow;
-        if (r >= row_end) continue;
-        float sc = 1.0f;
-        if (p.scale) sc = p.scale_f32 ? reinterpret_cast<const float*>(p.scale)[r]
-                                      : bf2f(reinterpret_cast<const uint16_t*>(p.scale)[r]);
-        const int64_t yr = p.y_idx ? (int64_t)p.y_idx[r] : r;
-        uint16_t* yrow = reinterpret_cast<uint16_t*>(p.C) + yr * p.ldc;
-        float* yrow32 = reinterpret_cast<float*>(p.C) + yr * p.ldc;
-        uint16_t* hrow = p.aux ? p.aux + r * p.ldc : nullptr;
-#pragma unroll
-        for (int b = 0; b < C::FN; ++b)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int n = n0 + wn * C::TN + b * 32 + 8 * g + lcol;
+          for (int m = 0; m < C::BN / 32; ++m) {
+            const int n = n0 + 32 * m + 8 * s;
             if (n >= p.N) continue;
-            float v[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) v[q] = acc[a][b][4 * g + q];
-            if (hrow) *reinterpret_cast<uint2*>(hrow + n) = make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
+            float v[8];
+            ld8(32 * m, v);
+            if (p.aux) *reinterpret_cast<uint4*>(p.aux + r * p.ldc + n) = pack8(v);
             if (p.scale) {
 #pragma unroll
-              for (int q = 0; q < 4; ++q) v[q] = v[q] * sc;
+              for (int t = 0; t < 8; ++t) v[t] = v[t] * sc;
             }
-            if (p.c_f32)
-              *reinterpret_cast<float4*>(yrow32 + n) = make_float4(v[0], v[1], v[2], v[3]);
-            else
-              *reinterpret_cast<uint2*>(yrow + n) = make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
+            if (p.c_f32) {
+              float4* d = reinterpret_cast<float4*>(yrow + (int64_t)n * 4);
+              d[0] = make_float4(v[0], v[1], v[2], v[3]);
+              d[1] = make_float4(v[4], v[5], v[6], v[7]);
+            } else {
+              *reinterpret_cast<uint4*>(yrow + (int64_t)n * 2) = pack8(v);
+            }
           }
-      }
-    } else if constexpr (EPI == EPI_SWIGLU) {
-      // fragments b < FN/2 hold gate columns, b + FN/2 the matching up columns
+        }
+      } else if constexpr (EPI == EPI_SWIGLU) {
+        // tile columns [0, BN/2) are gate, [BN/2, BN) the matching up columns
+        const int64_t r = row0 + a * 64 + q;
+        if (r < row_end) {
+          uint16_t* arow = reinterpret_cast<uint16_t*>(p.C) + r * p.ldc;
+          uint16_t* grow = p.aux ? p.aux + r * (int64_t)(2 * p.h) : nullptr;
 #pragma unroll
-      for (int a = 0; a < C::FM; ++a) {
-        const int64_t r = row0 + wm * C::TM + a * 32 + lrow;
-        if (r >= row_end) continue;
-        uint16_t* arow = reinterpret_cast<uint16_t*>(p.C) + r * p.ldc;
-        uint16_t* grow = p.aux ? p.aux + r * (int64_t)(2 * p.h) : nullptr;
-#pragma unroll
-        for (int b = 0; b < C::FN / 2; ++b)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int j = n0 + wn * (C::TN / 2) + b * 32 + 8 * g + lcol;
+          for (int m = 0; m < C::BN / 64; ++m) {
+            const int j = n0 + 32 * m + 8 * s;
             if (j >= p.N) continue;
-            uint32_t gb[4], ub[4];
-            float o[4];
+            float gv[8], uv[8], o[8];
+            ld8(32 * m, gv);
+            ld8(C::BN / 2 + 32 * m, uv);
+            uint32_t gb[8], ub[8];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              gb[q] = f2bf(acc[a][b][4 * g + q]);
-              ub[q] = f2bf(acc[a][b + C::FN / 2][4 * g + q]);
-              const float s = bf2f(f2bf(silu_f(bf2f(gb[q]))));
-              o[q] = s * bf2f(ub[q]);
+            for (int t = 0; t < 8; ++t) {
+              gb[t] = f2bf(gv[t]);
+              ub[t] = f2bf(uv[t]);
+              const float sl = bf2f(f2bf(silu_f(bf2f(gb[t]))));
+              o[t] = sl * bf2f(ub[t]);
             }
-            *reinterpret_cast<uint2*>(arow + j) = make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
+            *reinterpret_cast<uint4*>(arow + j) = pack8(o);
             if (grow) {
-              *reinterpret_cast<uint2*>(grow + j) = make_uint2(gb[0] | (gb[1] << 16), gb[2] | (gb[3] << 16));
-              *reinterpret_cast<uint2*>(grow + p.h + j) = make_uint2(ub[0] | (ub[1] << 16), ub[2] | (ub[3] << 16));
+              *reinterpret_cast<uint4*>(grow + j) = make_uint4(gb[0] | (gb[1] << 16), gb[2] | (gb[3] << 16),
+                                                               gb[4] | (gb[5] << 16), gb[6] | (gb[7] << 16));
+              *reinterpret_cast<uint4*>(grow + p.h + j) = make_uint4(ub[0] | (ub[1] << 16), ub[2] | (ub[3] << 16),
+                                                                     ub[4] | (ub[5] << 16), ub[6] | (ub[7] << 16));
             }
           }
-      }
-    } else if constexpr (EPI == EPI_SWIGLU_BWD) {
+        }
+      } else if constexpr (EPI == EPI_SWIGLU_BWD) {
+        const int64_t r = row0 + a * 64 + q;
+        if (r < row_end) {
+          float sc = 1.0f;
+          if (p.scale) sc = bf2f(reinterpret_cast<const uint16_t*>(p.scale)[r]);
+          const uint16_t* gurow = p.gu_in + r * (int64_t)(2 * p.h);
+          uint16_t* drow = reinterpret_cast<uint16_t*>(p.C) + r * (int64_t)(2 * p.h);
 #pragma unroll
-      for (int a = 0; a < C::FM; ++a) {
-        const int64_t r = row0 + wm * C::TM + a * 32 + lrow;
-        if (r >= row_end) continue;
-        float sc = 1.0f;
-        if (p.scale) sc = bf2f(reinterpret_cast<const uint16_t*>(p.scale)[r]);
-        const uint16_t* gurow = p.gu_in + r * (int64_t)(2 * p.h);
-        uint16_t* drow = reinterpret_cast<uint16_t*>(p.C) + r * (int64_t)(2 * p.h);
-#pragma unroll
-        for (int b = 0; b < C::FN; ++b)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int j = n0 + wn * C::TN + b * 32 + 8 * g + lcol;
+          for (int m = 0; m < C::BN / 32; ++m) {
+            const int j = n0 + 32 * m + 8 * s;
             if (j >= p.N) continue;
-            const uint2 gv = *reinterpret_cast<const uint2*>(gurow + j);
-            const uint2 uv = *reinterpret_cast<const uint2*>(gurow + p.h + j);
-            const float gg[4] = {bf_lo(gv.x), bf_hi(gv.x), bf_lo(gv.y), bf_hi(gv.y)};
-            const float uu[4] = {bf_lo(uv.x), bf_hi(uv.x), bf_lo(uv.y), bf_hi(uv.y)};
-            float dg[4], du[4];
+            float v[8];
+            ld8(32 * m, v);
+            const uint4 gv = *reinterpret_cast<const uint4*>(gurow + j);
+            const uint4 uv = *reinterpret_cast<const uint4*>(gurow + p.h + j);
+            const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+            float dg[8], du[8];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const float da = acc[a][b][4 * g + q] * sc;
-              const float sig = 1.0f / (1.0f + __expf(-gg[q]));
-              const float s = gg[q] * sig;
-              du[q] = da * s;
-              dg[q] = da * uu[q] * sig * (1.0f + gg[q] * (1.0f - sig));
+            for (int t = 0; t < 8; ++t) {
+              const float gg = (t & 1) ? bf_hi(gw[t >> 1]) : bf_lo(gw[t >> 1]);
+              const float uu = (t & 1) ? bf_hi(uw[t >> 1]) : bf_lo(uw[t >> 1]);
+              const float da = v[t] * sc;
+              const float sig = 1.0f / (1.0f + __expf(-gg));
+              du[t] = da * (gg * sig);
+              dg[t] = da * uu * sig * (1.0f + gg * (1.0f - sig));
             }
-            *reinterpret_cast<uint2*>(drow + j) = make_uint2(pack_bf2(dg[0], dg[1]), pack_bf2(dg[2], dg[3]));
-            *reinterpret_cast<uint2*>(drow + p.h + j) = make_uint2(pack_bf2(du[0], du[1]), pack_bf2(du[2], du[3]));
+            *reinterpret_cast<uint4*>(drow + j) = pack8(dg);
+            *reinterpret_cast<uint4*>(drow + p.h + j) = pack8(du);
           }
+        }
       }
+      __syncthreads();  // the band is reused by the next pass / the ring by the next tile
     }
   }
 }
@@ -565,7 +671,8 @@ static int launch(const GemmParams& p, int64_t tiles_upper, hipStream_t s) {
   }
   const int cus = num_cus();
   if (cus <= 0) return HMOE_ERR_DEVICE;
-  int64_t grid = cus;  // one workgroup per CU (LDS-limited)
+  const int per_cu = C::LDS_BYTES <= 72 * 1024 ? 2 : 1;  // LDS-limited residency (160 KB per CU)
+  int64_t grid = (int64_t)cus * per_cu;
   if (tiles_upper < grid) grid = tiles_upper;
   if (grid < 1) grid = 1;
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, s, p);
@@ -573,9 +680,10 @@ static int launch(const GemmParams& p, int64_t tiles_upper, hipStream_t s) {
   return HMOE_OK;
 }
 
-// Tile configurations.  Large: 256 (rows) x 128 (cols) tile, 4 waves of 128x64 (FM = 4, FN = 2: 128 fp32
-// accumulators per lane).  Small: 128x128, 4 waves of 64x64, for problems with few tiles.
-using CfgL = Cfg<256, 128, 2, 2, 4>;
+// Tile configurations.  Large: 256x256 tile, 4 waves of 128x128 (FM = FN = 4: 256 fp32 accumulators per lane,
+// LDS ring 4 x 32 KB).  Small: 128x128, 4 waves of 64x64 (ring 4 x 16 KB, two workgroups per CU), for problems
+// with few tiles.
+using CfgL = Cfg<256, 256, 2, 2, 4>;
 using CfgS = Cfg<128, 128, 2, 2, 4>;
 
 template <class C, int EPI>
