@@ -310,9 +310,10 @@ def moe_backward(x, ids, topk_w, wgu, wd, dout, fwd=None):
         dact = dyhat[sel] @ wd[e].astype(np.float64).T
         dwd[e] = a.T @ dyhat[sel]
         sig = 1.0 / (1.0 + np.exp(-g))
-        s = g * sig
+        # act = R(R(silu(g)) * u): d/du is the stored factor R(silu(g)); d/dg passes the roundings straight through
+        s_r = round_bf16(silu64(g)).astype(np.float64)
         dg = dact * u * sig * (1.0 + g * (1.0 - sig))
-        du = dact * s
+        du = dact * s_r
         dgu = np.concatenate([dg, du], axis=1)
         dxs = dgu @ wgu[e].astype(np.float64).T
         np.add.at(dx, rows_t[sel], dxs)

@@ -1,0 +1,105 @@
+"""The C-ABI library (libhmoe.so) loads without a GPU and exports exactly the entry points include/hmoe.h declares,
+with the argument counts the Python binding uses; argument validation returns the documented error codes before
+any device work (no kernel is launched here).  CPU only."""
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "hmoe.h")
+
+
+def header_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    protos = re.findall(r"^(?:int|size_t|const char\*)\s+(hmoe_\w+)\(([^;]*?)\);", src, flags=re.M | re.S)
+    return {name: (0 if args.strip() == "void" else args.count(",") + 1) for name, args in protos}
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from trenowanie_generatora_obrazkow_amd import _lib
+    return _lib
+
+
+def test_every_declared_symbol_is_exported(lib):
+    decl = header_functions()
+    assert len(decl) >= 17
+    so = ctypes.CDLL(lib.LIB_PATH)
+    for name in decl:
+        assert hasattr(so, name), f"{name} declared in include/hmoe.h but not exported"
+
+
+def test_binding_matches_header(lib):
+    decl = header_functions()
+    assert set(decl) == set(lib.SIGNATURES), set(decl) ^ set(lib.SIGNATURES)
+    for name, nargs in decl.items():
+        assert len(lib.SIGNATURES[name][1]) == nargs, name
+
+
+def test_exports_nothing_undeclared(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", lib.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\sT\s(hmoe_\w+)", out))
+    assert exported == set(header_functions())
+
+
+def test_version_and_errors(lib):
+    L = lib.lib()
+    assert L.hmoe_abi_version() == 1
+    for code, word in ((0, "ok"), (-1, "argument"), (-2, "shape"), (-3, "type"), (-4, "launch"), (-5, "workspace")):
+        assert word in L.hmoe_error_string(code).decode()
+
+
+def test_argument_validation_codes(lib):
+    L = lib.lib()
+    P = 4096  # a non-null stand-in address: never dereferenced, no kernel is launched on these paths
+    # router: negative T, bad alignment, too many experts
+    assert L.hmoe_route_topk(P, 8, P, None, -1, 8, 4, 2, 1, 1.0, None, P, P, None) == -1
+    assert L.hmoe_route_topk(P, 8, P, None, 0, 8, 4, 2, 1, 1.0, None, P, P, None) == 0  # empty input
+    assert L.hmoe_route_topk(P, 8, P, None, 4, 8, 300, 2, 1, 1.0, None, P, P, None) == -2
+    assert L.hmoe_route_topk(P + 2, 8, P, None, 4, 8, 4, 2, 1, 1.0, None, P, P, None) == -1
+    assert L.hmoe_route_topk(P, 8, P, None, 4, 12, 4, 2, 1, 1.0, None, P, P, None) == -1  # d % 8
+    # dispatch: dtype, workspace, E bounds
+    ws = L.hmoe_dispatch_workspace_size(16, 2, 4)
+    assert L.hmoe_dispatch(P, 2, None, 0, 16, 2, 4, None, 0, 0, None, P, None, P, P, P, P, None, P, ws, None) == -3
+    assert L.hmoe_dispatch(P, 4, None, 0, 16, 2, 4, None, 0, 0, None, P, None, P, P, P, P, None, P, ws - 1,
+                           None) == -5
+    assert L.hmoe_dispatch(P, 4, None, 0, 16, 2, 2000, None, 0, 0, None, P, None, P, P, P, P, None, P, ws,
+                           None) == -2
+    # grouped_mm: K % 8, fp32 input, int8 weights
+    assert L.hmoe_grouped_mm(P, 64, 0, P, 0, 3, 60, 32, 60 * 32, 32, P, 4, 48, None, None, None, 0, None, 0, P, 32,
+                             None) == -2
+    assert L.hmoe_grouped_mm(P, 64, 2, P, 0, 3, 64, 32, 64 * 32, 32, P, 4, 48, None, None, None, 0, None, 0, P, 32,
+                             None) == -3
+    assert L.hmoe_grouped_mm(P, 64, 0, P, 0, 3, 64, 32, 64 * 32, 32, P, 4, 48, None, None, None, 0, P, 0, P, 32,
+                             None) == -3
+    assert L.hmoe_grouped_mm(P, 64, 0, P, 0, 3, 64, 32, 64 * 32, 32, P, 4, 0, None, None, None, 0, None, 0, P, 32,
+                             None) == 0  # M == 0: nothing to do
+    assert L.hmoe_grouped_mm(P, 64, 0, P, 0, 3, 64, 32, 64 * 32, 32, None, 4, 48, None, None, None, 0, None, 0, P,
+                             32, None) == -1
+    # wgrad: output dtype, shapes
+    assert L.hmoe_grouped_wgrad(P, 64, P, 64, 3, 64, 64, P, 4, 48, P, 3, None) == -3
+    assert L.hmoe_grouped_wgrad(P, 64, P, 64, 3, 60, 64, P, 4, 48, P, 2, None) == -2
+    # combine / backward elementwise
+    assert L.hmoe_combine(P, 4, 2, 12, P, None) == -1
+    assert L.hmoe_unpermute_bwd(P, 5, P, None, None, 4, 2, 64, 0, P, None) == -3
+    assert L.hmoe_router_bwd(P, P, P, 16, 300, 2, 1, 1.0, P, 64, 64, P, None, 2, None, 0, None) == -2
+    assert L.hmoe_router_bwd(P, P, P, 16, 8, 2, 1, 1.0, P, 64, 64, P, P, 2, None, 0, None) == -5
+
+
+def test_workspace_queries(lib):
+    L = lib.lib()
+    a = L.hmoe_dispatch_workspace_size(16384, 2, 16)
+    b = L.hmoe_dispatch_workspace_size(16384, 2, 128)
+    assert 0 < a < b and a % 256 == 0
+    assert L.hmoe_router_bwd_workspace_size(16384, 16, 1536) == 64 * 16 * 1536 * 4
+
+
+def test_bench_refuses_multi_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 2 and "one GPU" in r.stderr

@@ -1,0 +1,102 @@
+"""Host-side logic of the drop-in surfaces, without a GPU: the moe_triton facade's helpers and argument checks,
+fuse_moe's weight stacking (aurora/hf_compat.py:142-169), mode selection refusing a CPU device, and the MoESwiGLU
+module's parameters.  No kernel is launched."""
+import math
+
+import pytest
+import torch
+import torch.nn as nn
+
+from trenowanie_generatora_obrazkow_amd import MoESwiGLU, moe_triton
+from trenowanie_generatora_obrazkow_amd import hf_compat
+
+
+def ref_m_bucket(M, E):
+    """aurora/moe_triton.py:59-62 with triton.next_power_of_2 (smallest power of two >= n)."""
+    n = max(1, M // E)
+    p = 1
+    while p < n:
+        p *= 2
+    return min(1024, max(16, p))
+
+
+@pytest.mark.parametrize("M,E", [(0, 1), (1, 1), (48, 3), (32768, 16), (8192 * 8, 128), (100, 128), (5000, 7),
+                                 (2 ** 20, 1)])
+def test_m_bucket(M, E):
+    assert moe_triton.m_bucket(M, E) == ref_m_bucket(M, E)
+    assert moe_triton.BLOCK_M == 64
+
+
+def test_facade_rejects_cpu_and_unsupported():
+    a = torch.randn(48, 64).bfloat16()
+    w = torch.randn(3, 64, 32).bfloat16()
+    counts = torch.tensor([16, 0, 32])
+    with pytest.raises(RuntimeError, match="GPU"):
+        moe_triton.grouped_mm(a, w, counts)
+    with pytest.raises(AssertionError):
+        moe_triton.grouped_mm(a, w.transpose(1, 2).contiguous().transpose(1, 2), counts)
+    with pytest.raises(NotImplementedError):
+        moe_triton.grouped_mm(a, w, counts, w_scale=torch.ones(3, 32))
+    with pytest.raises(TypeError):
+        moe_triton.grouped_mm(a.float(), w.float(), counts)
+    with pytest.raises(RuntimeError, match="GPU"):
+        moe_triton.make_schedule(counts, 48)
+
+
+class _Expert(nn.Module):
+    def __init__(self, d, h):
+        super().__init__()
+        self.gate_proj = nn.Linear(d, h, bias=False)
+        self.up_proj = nn.Linear(d, h, bias=False)
+        self.down_proj = nn.Linear(h, d, bias=False)
+        self.act_fn = nn.functional.silu
+
+
+class _Block(nn.Module):
+    def __init__(self, d, h, E):
+        super().__init__()
+        self.experts = nn.ModuleList([_Expert(d, h) for _ in range(E)])
+
+    def moe_infer(self, x, ids, w):
+        raise AssertionError
+
+
+def test_fuse_moe_stacks_reference_layout():
+    torch.manual_seed(0)
+    d, h, E = 32, 24, 5
+    model = nn.Sequential(_Block(d, h, E), _Block(d, h, E))
+    gates = [[e.gate_proj.weight.clone() for e in b.experts] for b in model]
+    ups = [[e.up_proj.weight.clone() for e in b.experts] for b in model]
+    downs = [[e.down_proj.weight.clone() for e in b.experts] for b in model]
+    assert hf_compat.fuse_moe(model) == 2
+    for bi, b in enumerate(model):
+        assert b._wgu.shape == (E, d, 2 * h) and b._wd.shape == (E, h, d)
+        for e in range(E):
+            torch.testing.assert_close(b._wgu[e, :, :h], gates[bi][e].t())  # [gate | up], (in, out)
+            torch.testing.assert_close(b._wgu[e, :, h:], ups[bi][e].t())
+            torch.testing.assert_close(b._wd[e], downs[bi][e].t())
+        assert b._wgu.is_contiguous() and b._wgu_s is None and b._mode is None
+        assert b.experts == list(range(E))
+        with pytest.raises(RuntimeError, match="GPU"):
+            b.moe_infer(torch.randn(4, d), torch.zeros(4, 2, dtype=torch.long), torch.ones(4, 2))
+    with pytest.raises(NotImplementedError):
+        hf_compat.fuse_moe(nn.Sequential(_Block(d, h, E)), quant="int8")
+
+
+def test_quant_int8_matches_reference_rule():
+    w = torch.randn(3, 64, 16)
+    q, s = hf_compat._quant_int8(w)
+    assert q.dtype == torch.int8 and s.dtype == torch.bfloat16
+    deq = hf_compat._dequant(q, s, torch.float32)
+    assert (deq - w).abs().max() <= (w.abs().amax(1).max() / 127) * 0.51 + 1e-2
+
+
+def test_moe_swiglu_module_shapes():
+    torch.manual_seed(0)
+    m = MoESwiGLU(64, 96, 8, top_k=2)
+    assert m.router_weight.shape == (8, 64) and m.w_gu.shape == (8, 64, 192) and m.w_d.shape == (8, 96, 64)
+    assert m.w_gu.dtype == torch.bfloat16
+    assert abs(m.w_gu.float().std().item() - 0.02) < 2e-3
+    assert m.logit_bias.dtype == torch.float32 and (m.logit_bias == 0).all()
+    with pytest.raises(RuntimeError, match="GPU"):
+        m(torch.randn(2, 5, 64))

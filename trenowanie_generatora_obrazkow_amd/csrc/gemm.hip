@@ -628,7 +628,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
               const float uu = (t & 1) ? bf_hi(uw[t >> 1]) : bf_lo(uw[t >> 1]);
               const float da = v[t] * sc;
               const float sig = 1.0f / (1.0f + __expf(-gg));
-              du[t] = da * (gg * sig);
+              du[t] = da * bf2f(f2bf(silu_f(gg)));  // the forward's stored factor bf16(silu(g))
               dg[t] = da * uu * sig * (1.0f + gg * (1.0f - sig));
             }
             *reinterpret_cast<uint4*>(drow + j) = pack8(dg);
