@@ -161,6 +161,15 @@ struct TileSel<true, ROWS, NWAVES> {
   using type = MNTile<ROWS, NWAVES>;
 };
 
+// Workgroup barrier that orders LDS only.  __syncthreads() is a workgroup release/acquire fence over all address
+// spaces, which on gfx9 also drains every outstanding global store (vmcnt(0)) -- the epilogue's stores would then be
+// waited for at each band pass.  Global data staged by the direct loads is ordered by wait_vm() before this barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // wait until at most N vector-memory operations of this thread are outstanding (s_waitcnt vmcnt(N); the
 // expcnt / lgkmcnt fields are left at their maxima so they do not wait)
 template <int N>
@@ -263,7 +272,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
       s_tstart[E] = its;
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   int nb_n;
   if (EPI == EPI_SWIGLU)
@@ -468,7 +477,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
         wait_vm<LOADS>();
       else
         wait_vm<0>();
-      __syncthreads();
+      lds_barrier();
       f0 = read(cons, 0);
     }
     // The two MFMA blocks are unconditional (a conditional copy would split the accumulators' live ranges); on the
@@ -484,7 +493,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
         wait_vm<LOADS>();
       else
         wait_vm<0>();
-      __syncthreads();
+      lds_barrier();
       if (kt + kNStage < nk) issue(kt + kNStage);  // into the slot of slice kt (fill == cons here)
       cons += C::STAGE_BYTES;
       if (cons == ring_end) cons = smem;
@@ -492,7 +501,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
       mfmas(f1);
       interleave();
     }
-    __syncthreads();  // every wave is done with the ring before the epilogue reuses it
+    lds_barrier();  // every wave is done with the ring before the epilogue reuses it
 
     // ---- epilogue, through LDS in bands of 64 rows ----
     // Pass a: every wave parks its fragment row a (rows a*64 + wm*32 + 0..31 of the tile, all its columns) in LDS
@@ -507,6 +516,20 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
     const int q = tid >> 2, s = tid & 3;
 #pragma unroll
     for (int a = 0; a < C::FM; ++a) {
+      // SwiGLU backward: issue this pass's [g | u] loads first, so their latency overlaps phase 1 and the barrier
+      // (rows / columns outside the tile load a valid location and are never used)
+      [[maybe_unused]] uint4 gpre[C::BN / 32], upre[C::BN / 32];
+      if constexpr (EPI == EPI_SWIGLU_BWD) {
+        const int64_t r = row0 + a * 64 + q;
+        const uint16_t* gurow = p.gu_in + (r < row_end ? r : row0) * (int64_t)(2 * p.h);
+#pragma unroll
+        for (int m = 0; m < C::BN / 32; ++m) {
+          const int j = n0 + 32 * m + 8 * s;
+          const int jc = j < p.N ? j : 0;
+          gpre[m] = *reinterpret_cast<const uint4*>(gurow + jc);
+          upre[m] = *reinterpret_cast<const uint4*>(gurow + p.h + jc);
+        }
+      }
       // phase 1: park fragment row a
 #pragma unroll
       for (int b = 0; b < C::FN; ++b)
@@ -516,7 +539,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
           *reinterpret_cast<float4*>(dst) =
               make_float4(acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2], acc[a][b][4 * g + 3]);
         }
-      __syncthreads();
+      lds_barrier();
       // phase 2: band row q, columns 32m + 8s + 0..7
       const float* brow = band + q * EP + 8 * s;
       auto ld8 = [&](int col, float* v) {
@@ -610,7 +633,6 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
         if (r < row_end) {
           float sc = 1.0f;
           if (p.scale) sc = bf2f(reinterpret_cast<const uint16_t*>(p.scale)[r]);
-          const uint16_t* gurow = p.gu_in + r * (int64_t)(2 * p.h);
           uint16_t* drow = reinterpret_cast<uint16_t*>(p.C) + r * (int64_t)(2 * p.h);
 #pragma unroll
           for (int m = 0; m < C::BN / 32; ++m) {
@@ -618,8 +640,8 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
             if (j >= p.N) continue;
             float v[8];
             ld8(32 * m, v);
-            const uint4 gv = *reinterpret_cast<const uint4*>(gurow + j);
-            const uint4 uv = *reinterpret_cast<const uint4*>(gurow + p.h + j);
+            const uint4 gv = gpre[m];
+            const uint4 uv = upre[m];
             const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
             float dg[8], du[8];
 #pragma unroll
@@ -627,8 +649,8 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
               const float gg = (t & 1) ? bf_hi(gw[t >> 1]) : bf_lo(gw[t >> 1]);
               const float uu = (t & 1) ? bf_hi(uw[t >> 1]) : bf_lo(uw[t >> 1]);
               const float da = v[t] * sc;
-              const float sig = 1.0f / (1.0f + __expf(-gg));
-              du[t] = da * bf2f(f2bf(silu_f(gg)));  // the forward's stored factor bf16(silu(g))
+              const float sig = sigmoid_f(gg);
+              du[t] = da * bf2f(f2bf(gg * sig));  // the forward's stored factor bf16(silu(g)), silu_f(g) = g*sig
               dg[t] = da * uu * sig * (1.0f + gg * (1.0f - sig));
             }
             *reinterpret_cast<uint4*>(drow + j) = pack8(dg);
@@ -636,7 +658,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
           }
         }
       }
-      __syncthreads();  // the band is reused by the next pass / the ring by the next tile
+      lds_barrier();  // the band is reused by the next pass / the ring by the next tile
     }
   }
 }

@@ -46,7 +46,11 @@ __device__ __forceinline__ float hexp(float x) {
   return __builtin_ldexpf(p, (int)n);
 }
 
-__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)); }
+// logistic sigmoid and SiLU with the hardware reciprocal (v_rcp_f32, ~1 ulp) instead of an IEEE division; the
+// forward and backward epilogues use these same two functions, so the backward sees exactly the bf16(silu(g)) the
+// forward stored.
+__device__ __forceinline__ float sigmoid_f(float g) { return __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
+__device__ __forceinline__ float silu_f(float g) { return g * sigmoid_f(g); }
 
 // xor-butterfly sum over the 64 lanes; every lane ends with the same value (fp add is commutative).
 __device__ __forceinline__ float wave_sum_butterfly(float v) {
