@@ -96,7 +96,9 @@ def test_workspace_queries(lib):
     a = L.hmoe_dispatch_workspace_size(16384, 2, 16)
     b = L.hmoe_dispatch_workspace_size(16384, 2, 128)
     assert 0 < a < b and a % 256 == 0
-    assert L.hmoe_router_bwd_workspace_size(16384, 16, 1536) == 64 * 16 * 1536 * 4
+    # one fp32 (E, d) partial per 128-token chunk
+    assert L.hmoe_router_bwd_workspace_size(16384, 16, 1536) == 128 * 16 * 1536 * 4
+    assert L.hmoe_router_bwd_workspace_size(129, 16, 1536) == 2 * 16 * 1536 * 4
 
 
 def test_bench_refuses_multi_gpu():

@@ -408,3 +408,19 @@ def test_golden_fixtures_reproduce(oracle):
                               fwd=fwd)
     for key in ("dx", "dwr", "dwgu", "dwd", "dtopk_w", "dlogits"):
         np.testing.assert_allclose(b[key], lz[key], rtol=1e-12, atol=1e-15)
+
+
+def test_bf16_products_exact_in_fp32():
+    # The router's lane partials use fused multiply-adds; that equals the multiply-then-add order because the product
+    # of two bf16 values (8 significant bits each) is exact in fp32.  Check it over the whole normal range.
+    rng = np.random.default_rng(7)
+    a = rng.integers(0, 1 << 16, 200000, dtype=np.uint32).astype(np.uint16)
+    b = rng.integers(0, 1 << 16, 200000, dtype=np.uint32).astype(np.uint16)
+    fa = (a.astype(np.uint32) << 16).view(np.float32)
+    fb = (b.astype(np.uint32) << 16).view(np.float32)
+    exact = fa.astype(np.float64) * fb.astype(np.float64)
+    ok = np.isfinite(exact) & (np.abs(exact) >= 2.0 ** -126) & (np.abs(exact) < 2.0 ** 127)
+    with np.errstate(over="ignore", invalid="ignore"):
+        prod32 = fa[ok] * fb[ok]
+    assert ok.sum() > 50000
+    np.testing.assert_array_equal(prod32.astype(np.float64), exact[ok])

@@ -52,10 +52,86 @@ __device__ __forceinline__ float hexp(float x) {
 __device__ __forceinline__ float sigmoid_f(float g) { return __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 __device__ __forceinline__ float silu_f(float g) { return g * sigmoid_f(g); }
 
-// xor-butterfly sum over the 64 lanes; every lane ends with the same value (fp add is commutative).
+// ---- cross-lane exchange without LDS: the value of lane (l ^ S) ----
+// S = 1, 2: DPP quad permutations; S = 8: DPP rotation of each 16-lane row by 8 (= xor 8); S = 4: row rotations
+// (row_ror:n reads lane (l - n) mod 16 of the row): lanes with bit 2 set read l - 4 (ror 4), the others l + 4
+// (ror 12).  S = 16, 32 are served by the permlane swaps below.
+template <int S>
+__device__ __forceinline__ float lane_xor(float v) {
+  static_assert(S == 1 || S == 2 || S == 4 || S == 8, "lane_xor: S in {1, 2, 4, 8}");
+  const int b = __float_as_int(v);
+  if constexpr (S == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(b, 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
+  if constexpr (S == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(b, 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
+  if constexpr (S == 8) return __int_as_float(__builtin_amdgcn_mov_dpp(b, 0x128, 0xF, 0xF, false)); // row_ror:8
+  if constexpr (S == 4) {
+    const int from_below = __builtin_amdgcn_mov_dpp(b, 0x124, 0xF, 0xF, false);  // row_ror:4:  lane l - 4
+    const int from_above = __builtin_amdgcn_mov_dpp(b, 0x12C, 0xF, 0xF, false);  // row_ror:12: lane l + 4
+    return __int_as_float((__lane_id() & 4) ? from_below : from_above);
+  }
+  return v;
+}
+template <int S>
+__device__ __forceinline__ int lane_xor_i(int v) {
+  return __float_as_int(lane_xor<S>(__int_as_float(v)));
+}
+
+// Pair exchange across 32 / 16 lanes (gfx950 v_permlane32_swap / v_permlane16_swap).  With lo = the value lanes
+// whose bit S is clear keep and hi = the value lanes whose bit S is set keep, returns {own, partner}: lanes with bit S
+// clear get (lo[l], lo[l ^ S]), lanes with it set get (hi[l ^ S], hi[l]).  With lo = hi = v this is (v[l], v[l ^ S])
+// in some order, i.e. one xor-butterfly step.
+template <int S>
+__device__ __forceinline__ void lane_swap(float lo, float hi, float& a, float& b) {
+  static_assert(S == 16 || S == 32, "lane_swap: S in {16, 32}");
+  if constexpr (S == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+  }
+}
+
+// one xor-butterfly step of a sum: v[l] + v[l ^ S] (fp addition is commutative, so every lane pair gets the same sum)
+template <int S>
+__device__ __forceinline__ float bfly_add(float v) {
+  if constexpr (S >= 16) {
+    float a, b;
+    lane_swap<S>(v, v, a, b);
+    return __fadd_rn(a, b);
+  } else {
+    return __fadd_rn(v, lane_xor<S>(v));
+  }
+}
+template <int S>
+__device__ __forceinline__ float bfly_max(float v) {
+  if constexpr (S >= 16) {
+    float a, b;
+    lane_swap<S>(v, v, a, b);
+    return fmaxf(a, b);
+  } else {
+    return fmaxf(v, lane_xor<S>(v));
+  }
+}
+
+// xor-butterfly sum over the 64 lanes (s = 32, 16, ..., 1); every lane ends with the same value.
 __device__ __forceinline__ float wave_sum_butterfly(float v) {
-#pragma unroll
-  for (int s = 32; s >= 1; s >>= 1) v = __fadd_rn(v, __shfl_xor(v, s, 64));
+  v = bfly_add<32>(v);
+  v = bfly_add<16>(v);
+  v = bfly_add<8>(v);
+  v = bfly_add<4>(v);
+  v = bfly_add<2>(v);
+  v = bfly_add<1>(v);
+  return v;
+}
+__device__ __forceinline__ float wave_max_butterfly(float v) {
+  v = bfly_max<32>(v);
+  v = bfly_max<16>(v);
+  v = bfly_max<8>(v);
+  v = bfly_max<4>(v);
+  v = bfly_max<2>(v);
+  v = bfly_max<1>(v);
   return v;
 }
 

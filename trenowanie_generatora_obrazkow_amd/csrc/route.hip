@@ -11,7 +11,84 @@ constexpr int kRouteMaxE = 256;  // experts per lane: 4
 constexpr int kRouteEPL = kRouteMaxE / 64;
 constexpr int kMaxK = 16;
 
-template <int NCH>
+// Transposed butterfly over the G partials of an expert group (see route_topk_kernel): after the call p[0] of lane
+// l holds the partial sum of expert l >> (6 - log2 G), reduced over the lane bits 5, 4, ... that the halvings used.
+template <int G>
+__device__ __forceinline__ void transposed_butterfly(float (&p)[G], int lane) {
+  constexpr int H = G == 8 ? 3 : G == 16 ? 4 : G == 32 ? 5 : 6;
+  static_assert((1 << H) == G, "expert group must be 8, 16, 32 or 64");
+#pragma unroll
+  for (int i = 0; i < G / 2; ++i) {  // s = 32
+    float a, b;
+    lane_swap<32>(p[i], p[i + G / 2], a, b);
+    p[i] = __fadd_rn(a, b);
+  }
+#pragma unroll
+  for (int i = 0; i < G / 4; ++i) {  // s = 16
+    float a, b;
+    lane_swap<16>(p[i], p[i + G / 4], a, b);
+    p[i] = __fadd_rn(a, b);
+  }
+  auto halve = [&](auto sc, int half) {
+    constexpr int S = decltype(sc)::value;
+    const bool upper = (lane & S) != 0;
+#pragma unroll
+    for (int i = 0; i < G / 8; ++i) {
+      if (i < half) {
+        const float keep = upper ? p[i + half] : p[i];
+        const float send = upper ? p[i] : p[i + half];
+        p[i] = __fadd_rn(keep, lane_xor<S>(send));
+      }
+    }
+  };
+  if constexpr (H >= 3) halve(std::integral_constant<int, 8>(), G / 8);
+  if constexpr (H >= 4) halve(std::integral_constant<int, 4>(), G / 16);
+  if constexpr (H >= 5) halve(std::integral_constant<int, 2>(), G / 32);
+  if constexpr (H >= 6) halve(std::integral_constant<int, 1>(), G / 64);
+}
+
+// wave-wide argmax of (value, index): larger value wins, equal values go to the lower index; an index of 0x7fffffff
+// marks an empty candidate.  The winner is unique, so any exchange pattern gives every lane the same result.
+__device__ __forceinline__ void argmax_take(float& bv, int& be, float ov, int oe) {
+  const bool take = oe != 0x7fffffff && (be == 0x7fffffff || ov > bv || (ov == bv && oe < be));
+  if (take) {
+    bv = ov;
+    be = oe;
+  }
+}
+__device__ __forceinline__ void wave_argmax(float& bv, int& be) {
+  {
+    float a0, a1, e0, e1;
+    lane_swap<32>(bv, bv, a0, a1);
+    lane_swap<32>(__int_as_float(be), __int_as_float(be), e0, e1);
+    bv = a0; be = __float_as_int(e0);
+    argmax_take(bv, be, a1, __float_as_int(e1));
+  }
+  {
+    float a0, a1, e0, e1;
+    lane_swap<16>(bv, bv, a0, a1);
+    lane_swap<16>(__int_as_float(be), __int_as_float(be), e0, e1);
+    bv = a0; be = __float_as_int(e0);
+    argmax_take(bv, be, a1, __float_as_int(e1));
+  }
+  argmax_take(bv, be, lane_xor<8>(bv), lane_xor_i<8>(be));
+  argmax_take(bv, be, lane_xor<4>(bv), lane_xor_i<4>(be));
+  argmax_take(bv, be, lane_xor<2>(bv), lane_xor_i<2>(be));
+  argmax_take(bv, be, lane_xor<1>(bv), lane_xor_i<1>(be));
+}
+
+// Logits in the fixed order: lane l's partial is the sequential sum over chunks c and elements i of
+// x[c*512 + 8l + i] * w[c*512 + 8l + i]; the 64 partials are summed by the xor butterfly (s = 32, 16, ..., 1); the
+// bias is added last.  A bf16 x bf16 product has at most 16 significant bits, so it is exact in fp32 and the fused
+// multiply-add rounds exactly once, like a separate multiply and add (barring products below the fp32 normal range,
+// |x w| < 2^-126, which round differently).
+//
+// Experts are processed in groups of G (a power of two <= 64) with a "transposed" butterfly: at step s the lanes
+// with bit s set keep the upper half of the group's partials and send the lower half, so each step halves the values
+// per lane instead of reducing every expert separately; each value still meets exactly the partner the plain
+// butterfly would give it (fp addition is commutative), so the sums are bit-identical.  After log2(G) steps lane l
+// holds expert l >> (6 - log2 G) of the group, and the remaining steps are the plain butterfly.
+template <int NCH, int G>
 __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                          const uint16_t* __restrict__ wr,
                                                          const float* __restrict__ bias, int T, int d, int E, int k,
@@ -34,36 +111,51 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restr
     float lg[kRouteEPL];
 #pragma unroll
     for (int i = 0; i < kRouteEPL; ++i) lg[i] = -__builtin_inff();
-    for (int e = 0; e < E; ++e) {
-      float acc = 0.0f;
-      const uint16_t* wrow = wr + (int64_t)e * d;
+    for (int g0 = 0; g0 < E; g0 += G) {
+      // lane partials of the G experts of this group; rows past E repeat row E-1 and columns past d read column
+      // d-8 against zero x (both only feed lanes / values that are discarded), so the loads carry no branches
+      float p[G];
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-        int idx = c * 512 + lane * 8;
-        if (idx < d) {
-          uint4 wv = *reinterpret_cast<const uint4*>(wrow + idx);
-          uint32_t xw[4] = {xr[c].x, xr[c].y, xr[c].z, xr[c].w};
-          uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+      for (int e = 0; e < G; ++e) {
+        p[e] = 0.0f;
+        const uint16_t* wrow = wr + (int64_t)min(g0 + e, E - 1) * d;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+          const int idx = min(c * 512 + lane * 8, d - 8);
+          const uint4 wv = *reinterpret_cast<const uint4*>(wrow + idx);
+          const uint32_t xw[4] = {xr[c].x, xr[c].y, xr[c].z, xr[c].w};
+          const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            acc = __fadd_rn(acc, __fmul_rn(bf_lo(xw[j]), bf_lo(ww[j])));
-            acc = __fadd_rn(acc, __fmul_rn(bf_hi(xw[j]), bf_hi(ww[j])));
+            p[e] = __builtin_fmaf(bf_lo(xw[j]), bf_lo(ww[j]), p[e]);
+            p[e] = __builtin_fmaf(bf_hi(xw[j]), bf_hi(ww[j]), p[e]);
           }
         }
       }
-      float v = wave_sum_butterfly(acc);
-      if (bias) v = __fadd_rn(v, bias[e]);
+      transposed_butterfly<G>(p, lane);
+      constexpr int H = G == 8 ? 3 : G == 16 ? 4 : G == 32 ? 5 : 6;
+      float v = p[0];
+      if constexpr (H < 4) v = bfly_add<4>(v);  // the plain butterfly finishes in descending s
+      if constexpr (H < 5) v = bfly_add<2>(v);
+      if constexpr (H < 6) v = bfly_add<1>(v);
+      const int my_e = g0 + (lane >> (6 - H));
+      if (bias && my_e < E) v = __fadd_rn(v, bias[my_e]);
+      // lane l collects expert i*64 + l from the lanes of its group slot
 #pragma unroll
-      for (int i = 0; i < kRouteEPL; ++i)
-        if (e == i * 64 + lane) lg[i] = v;
+      for (int i = 0; i < kRouteEPL; ++i) {
+        if (i * 64 < E && i * 64 + 63 >= g0 && i * 64 < g0 + G) {
+          const int e = i * 64 + lane;
+          const float val = __shfl(v, ((e - g0) << (6 - H)) & 63, 64);
+          if (e >= g0 && e < g0 + G && e < E) lg[i] = val;
+        }
+      }
     }
     // softmax over the E logits held lane-wise (lane l: experts l, l+64, ...)
     float m = -__builtin_inff();
 #pragma unroll
     for (int i = 0; i < kRouteEPL; ++i)
       if (i * 64 + lane < E) m = fmaxf(m, lg[i]);
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
+    m = wave_max_butterfly(m);
     float ex[kRouteEPL];
     float a = 0.0f;
 #pragma unroll
@@ -100,16 +192,7 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restr
             be = e;
           }
         }
-#pragma unroll
-        for (int s = 32; s >= 1; s >>= 1) {
-          float ov = __shfl_xor(bv, s, 64);
-          int oe = __shfl_xor(be, s, 64);
-          bool take = oe != 0x7fffffff && (be == 0x7fffffff || ov > bv || (ov == bv && oe < be));
-          if (take) {
-            bv = ov;
-            be = oe;
-          }
-        }
+        wave_argmax(bv, be);
         float myex = 0.0f;
 #pragma unroll
         for (int i = 0; i < kRouteEPL; ++i)
@@ -404,8 +487,7 @@ __global__ __launch_bounds__(256) void router_dlogits_kernel(const float* __rest
         m = fmaxf(m, lg[i]);
       }
     }
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
+    m = wave_max_butterfly(m);
     float ex[kRouteEPL];
     float a = 0.0f;
 #pragma unroll
@@ -466,116 +548,207 @@ __global__ __launch_bounds__(256) void router_dlogits_kernel(const float* __rest
   }
 }
 
-constexpr int kRouterTC = 256;  // tokens per dwr partial chunk
-constexpr int kRouterEG = 8;    // experts per workgroup
+// dwr = dlogits^T x.  A chunk of kDwrWaves * kDwrTok tokens per workgroup; wave w sums its kDwrTok tokens in token
+// order for 8 columns per lane and up to kDwrEG experts per pass (dlogits of a token are wave-uniform scalar loads);
+// the four waves' sums are added in wave order through LDS and stored as the chunk's partial.  The chunk partials
+// are then added in chunk order, so the result does not depend on the launch.
+constexpr int kDwrTok = 32;
+constexpr int kDwrWaves = 4;
+constexpr int kDwrChunk = kDwrTok * kDwrWaves;
+constexpr int kDwrEG = 16;
 
-// grid (chunks, ceil(E / kRouterEG)); thread owns 8 consecutive columns (column blocks of 2048 in a loop)
+// grid (nchunk, ceil(d / 512)), block 256
 __global__ __launch_bounds__(256) void router_dwr_partial_kernel(const float* __restrict__ dlogits,
                                                                  const uint16_t* __restrict__ x, int64_t ldx,
                                                                  int64_t T, int E, int64_t d,
                                                                  float* __restrict__ part) {
-  __shared__ float s_dl[kRouterTC][kRouterEG];
-  const int chunk = blockIdx.x, e0 = blockIdx.y * kRouterEG;
-  const int64_t t0 = (int64_t)chunk * kRouterTC;
-  const int64_t t1 = min(T, t0 + kRouterTC);
-  for (int i = threadIdx.x; i < kRouterTC * kRouterEG; i += blockDim.x) {
-    const int tt = i / kRouterEG, eg = i % kRouterEG;
-    s_dl[tt][eg] = (t0 + tt < t1 && e0 + eg < E) ? dlogits[(t0 + tt) * E + e0 + eg] : 0.0f;
-  }
-  __syncthreads();
-  for (int64_t col = (int64_t)threadIdx.x * 8; col < d; col += (int64_t)blockDim.x * 8) {
-    float acc[kRouterEG][8];
+  constexpr int U = 8;  // tokens whose x loads are in flight together
+  static_assert(kDwrTok % U == 0, "token batch must divide the wave's tokens");
+  __shared__ float s_dl[kDwrChunk][kDwrEG];
+  __shared__ float4 red[kDwrWaves - 1][2][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t chunk = blockIdx.x;
+  const int64_t col = (int64_t)blockIdx.y * 512 + lane * 8;
+  const bool active = col < d;
+  const int64_t t0 = chunk * kDwrChunk;
+  const int64_t tb = t0 + (int64_t)wave * kDwrTok;
+  for (int e0 = 0; e0 < E; e0 += kDwrEG) {
+    // the chunk's dlogits for this expert pass (zero past T and past E)
+    for (int i = threadIdx.x; i < kDwrChunk * kDwrEG; i += blockDim.x) {
+      const int64_t t = t0 + i / kDwrEG;
+      const int e = e0 + i % kDwrEG;
+      s_dl[i / kDwrEG][i % kDwrEG] = (t < T && e < E) ? dlogits[t * E + e] : 0.0f;
+    }
+    __syncthreads();
+    float acc[kDwrEG][8];
 #pragma unroll
-    for (int eg = 0; eg < kRouterEG; ++eg)
+    for (int e = 0; e < kDwrEG; ++e)
 #pragma unroll
-      for (int q = 0; q < 8; ++q) acc[eg][q] = 0.0f;
-    for (int64_t t = t0; t < t1; ++t) {
-      const uint4 v = *reinterpret_cast<const uint4*>(x + t * ldx + col);
-      const float xv[8] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y),
-                           bf_lo(v.z), bf_hi(v.z), bf_lo(v.w), bf_hi(v.w)};
+      for (int q = 0; q < 8; ++q) acc[e][q] = 0.0f;
+    // tokens in order; rows past T load nothing and meet zero dlogits
+    for (int u0 = 0; u0 < kDwrTok; u0 += U) {
+      uint4 v[U];
 #pragma unroll
-      for (int eg = 0; eg < kRouterEG; ++eg) {
-        const float g = s_dl[t - t0][eg];
+      for (int u = 0; u < U; ++u) {
+        const int64_t t = tb + u0 + u;
+        v[u] = make_uint4(0, 0, 0, 0);
+        if (active && t < T) v[u] = *reinterpret_cast<const uint4*>(x + t * ldx + col);
+      }
 #pragma unroll
-        for (int q = 0; q < 8; ++q) acc[eg][q] = __builtin_fmaf(g, xv[q], acc[eg][q]);
+      for (int u = 0; u < U; ++u) {
+        const float xv[8] = {bf_lo(v[u].x), bf_hi(v[u].x), bf_lo(v[u].y), bf_hi(v[u].y),
+                             bf_lo(v[u].z), bf_hi(v[u].z), bf_lo(v[u].w), bf_hi(v[u].w)};
+        const float* g = s_dl[wave * kDwrTok + u0 + u];
+#pragma unroll
+        for (int e = 0; e < kDwrEG; ++e) {
+          const float ge = g[e];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) acc[e][q] = __builtin_fmaf(ge, xv[q], acc[e][q]);
+        }
       }
     }
+    // wave-ordered sum of the four waves, one expert at a time
 #pragma unroll
-    for (int eg = 0; eg < kRouterEG; ++eg) {
-      if (e0 + eg >= E) break;
-      float4* dst = reinterpret_cast<float4*>(part + ((int64_t)chunk * E + e0 + eg) * d + col);
-      dst[0] = make_float4(acc[eg][0], acc[eg][1], acc[eg][2], acc[eg][3]);
-      dst[1] = make_float4(acc[eg][4], acc[eg][5], acc[eg][6], acc[eg][7]);
+    for (int e = 0; e < kDwrEG; ++e) {
+      if (e0 + e >= E) continue;  // uniform: every thread skips the same experts (and their barriers)
+      if (wave > 0) {
+        red[wave - 1][0][lane] = make_float4(acc[e][0], acc[e][1], acc[e][2], acc[e][3]);
+        red[wave - 1][1][lane] = make_float4(acc[e][4], acc[e][5], acc[e][6], acc[e][7]);
+      }
+      __syncthreads();
+      if (wave == 0 && active) {
+        float s[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) s[q] = acc[e][q];
+#pragma unroll
+        for (int w = 0; w < kDwrWaves - 1; ++w) {
+          const float4 a = red[w][0][lane], b = red[w][1][lane];
+          s[0] += a.x; s[1] += a.y; s[2] += a.z; s[3] += a.w;
+          s[4] += b.x; s[5] += b.y; s[6] += b.z; s[7] += b.w;
+        }
+        float4* dst = reinterpret_cast<float4*>(part + (chunk * E + e0 + e) * d + col);
+        dst[0] = make_float4(s[0], s[1], s[2], s[3]);
+        dst[1] = make_float4(s[4], s[5], s[6], s[7]);
+      }
+      __syncthreads();
     }
   }
 }
 
+// out[i] = sum over chunks c (in order) of part[c][i]; block 256 = 64 outputs x 4 chunk quarters, the quarter sums
+// added in quarter order.
 __global__ __launch_bounds__(256) void router_dwr_reduce_kernel(const float* __restrict__ part, int nchunk, int E,
                                                                 int64_t d, void* __restrict__ dwr, int dwr_bf16) {
+  __shared__ float red[3][64];
   const int64_t total = (int64_t)E * d;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+  const int j = threadIdx.x & 63, q = threadIdx.x >> 6;
+  const int per = (nchunk + 3) / 4;
+  const int c0 = q * per, c1 = min(nchunk, c0 + per);
+  for (int64_t base = (int64_t)blockIdx.x * 64; base < total; base += (int64_t)gridDim.x * 64) {
+    const int64_t i = base + j;
     float s = 0.0f;
-    for (int c = 0; c < nchunk; ++c) s += part[(int64_t)c * total + i];
-    if (dwr_bf16)
-      reinterpret_cast<uint16_t*>(dwr)[i] = (uint16_t)f2bf(s);
-    else
-      reinterpret_cast<float*>(dwr)[i] = s;
+    if (i < total)
+      for (int c = c0; c < c1; ++c) s += part[(int64_t)c * total + i];
+    if (q > 0) red[q - 1][j] = s;
+    __syncthreads();
+    if (q == 0 && i < total) {
+      s = ((s + red[0][j]) + red[1][j]) + red[2][j];
+      if (dwr_bf16)
+        reinterpret_cast<uint16_t*>(dwr)[i] = (uint16_t)f2bf(s);
+      else
+        reinterpret_cast<float*>(dwr)[i] = s;
+    }
+    __syncthreads();
   }
 }
 
-// dx[t] = bf16(sum_j dxs[inv_pos[t*k+j]] + sum_e dlogits[t,e] * wr[e]); one thread per 8 columns of a token
-template <bool F32>
+// dx[t] = bf16(sum_j dxs[inv_pos[t*k+j]] + sum_e dlogits[t,e] * wr[e]).  A workgroup walks tokens; each thread owns
+// 8 columns of a column slab (blockIdx.y), so the token's row indices and router gradients are wave-uniform scalar
+// loads.  EMAX > 0: the thread's wr columns for E <= EMAX experts stay in registers for all its tokens.
+template <bool F32, int EMAX>
 __global__ __launch_bounds__(256) void unpermute_bwd_kernel(const void* __restrict__ dxs,
                                                             const int32_t* __restrict__ inv_pos,
                                                             const float* __restrict__ dlogits,
                                                             const uint16_t* __restrict__ wr, int64_t T, int k,
                                                             int64_t d, int E, uint16_t* __restrict__ dx) {
-  const int64_t nvec = d / 8;
-  const int64_t total = T * nvec;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t t = i / nvec, c = i - t * nvec;
-    float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  const int64_t col = ((int64_t)blockIdx.y * blockDim.x + threadIdx.x) * 8;
+  const bool active = col < d;
+  [[maybe_unused]] uint4 wreg[EMAX > 0 ? EMAX : 1];
+  if constexpr (EMAX > 0) {
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e) {
+      wreg[e] = make_uint4(0, 0, 0, 0);
+      if (dlogits && e < E && active) wreg[e] = *reinterpret_cast<const uint4*>(wr + (int64_t)e * d + col);
+    }
+  }
+  // two tokens per pass so that both tokens' row loads are in flight together
+  for (int64_t t0 = (int64_t)blockIdx.x * 2; t0 < T; t0 += (int64_t)gridDim.x * 2) {
+    float s[2][8];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) s[u][q] = 0.0f;
     for (int j = 0; j < k; ++j) {
-      const int64_t r = inv_pos[t * k + j];
-      if constexpr (F32) {
-        const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(dxs) + r * d) + 2 * c;
-        const float4 v0 = src[0], v1 = src[1];
-        s[0] += v0.x;
-        s[1] += v0.y;
-        s[2] += v0.z;
-        s[3] += v0.w;
-        s[4] += v1.x;
-        s[5] += v1.y;
-        s[6] += v1.z;
-        s[7] += v1.w;
-      } else {
-        const uint4 v = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(dxs) + r * d)[c];
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          s[2 * q] += bf_lo(w[q]);
-          s[2 * q + 1] += bf_hi(w[q]);
+      for (int u = 0; u < 2; ++u) {
+        const int64_t t = t0 + u;
+        if (t >= T || !active) continue;
+        const int64_t r = inv_pos[t * k + j];
+        if constexpr (F32) {
+          const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(dxs) + r * d + col);
+          const float4 v0 = src[0], v1 = src[1];
+          s[u][0] += v0.x;
+          s[u][1] += v0.y;
+          s[u][2] += v0.z;
+          s[u][3] += v0.w;
+          s[u][4] += v1.x;
+          s[u][5] += v1.y;
+          s[u][6] += v1.z;
+          s[u][7] += v1.w;
+        } else {
+          const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(dxs) + r * d + col);
+          const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            s[u][2 * q] += bf_lo(w[q]);
+            s[u][2 * q + 1] += bf_hi(w[q]);
+          }
         }
       }
     }
-    if (dlogits) {
-      for (int e = 0; e < E; ++e) {
-        const float g = dlogits[t * E + e];
-        const uint4 v = reinterpret_cast<const uint4*>(wr + (int64_t)e * d)[c];
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          s[2 * q] = __builtin_fmaf(g, bf_lo(w[q]), s[2 * q]);
-          s[2 * q + 1] = __builtin_fmaf(g, bf_hi(w[q]), s[2 * q + 1]);
+    for (int u = 0; u < 2; ++u) {
+      const int64_t t = t0 + u;
+      if (t >= T) break;
+      if (dlogits) {
+        auto fma_row = [&](float g, const uint4 v) {
+          const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            s[u][2 * q] = __builtin_fmaf(g, bf_lo(w[q]), s[u][2 * q]);
+            s[u][2 * q + 1] = __builtin_fmaf(g, bf_hi(w[q]), s[u][2 * q + 1]);
+          }
+        };
+        if constexpr (EMAX > 0) {
+          // experts past E have zero weight columns (wreg), so their (clamped, finite) router gradient adds 0
+#pragma unroll
+          for (int e = 0; e < EMAX; ++e) fma_row(dlogits[t * E + min(e, E - 1)], wreg[e]);
+        } else {
+          for (int e = 0; e < E; ++e)
+            fma_row(dlogits[t * E + e], active ? *reinterpret_cast<const uint4*>(wr + (int64_t)e * d + col)
+                                               : make_uint4(0, 0, 0, 0));
         }
       }
+      if (active) {
+        uint4 o;
+        o.x = pack_bf2(s[u][0], s[u][1]);
+        o.y = pack_bf2(s[u][2], s[u][3]);
+        o.z = pack_bf2(s[u][4], s[u][5]);
+        o.w = pack_bf2(s[u][6], s[u][7]);
+        *reinterpret_cast<uint4*>(dx + t * d + col) = o;
+      }
     }
-    uint4 o;
-    o.x = pack_bf2(s[0], s[1]);
-    o.y = pack_bf2(s[2], s[3]);
-    o.z = pack_bf2(s[4], s[5]);
-    o.w = pack_bf2(s[6], s[7]);
-    reinterpret_cast<uint4*>(dx + t * d)[c] = o;
   }
 }
 
@@ -622,19 +795,43 @@ int hmoe_route_topk(const void* x, int64_t ldx, const void* wr, const float* bia
   const int nch = (int)((d + 511) / 512);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* wp = static_cast<const uint16_t*>(wr);
-#define HMOE_ROUTE(NC)                                                                                          \
-  hipLaunchKernelGGL(route_topk_kernel<NC>, dim3(grid), dim3(256), 0, s, xp, ldx, wp, bias, (int)T, (int)d, E, k, \
-                     renorm, scaling, logits, topk_ids, topk_w)
-  if (nch <= 2)
-    HMOE_ROUTE(2);
-  else if (nch <= 4)
-    HMOE_ROUTE(4);
-  else if (nch <= 8)
-    HMOE_ROUTE(8);
-  else if (nch <= 16)
-    HMOE_ROUTE(16);
-  else
+  // experts per transposed-butterfly group; rows longer than 2048 hold more of x in registers, so smaller groups
+  int group = E <= 8 ? 8 : E <= 16 ? 16 : E <= 32 ? 32 : 64;
+  if (nch > 4 && group > 16) group = 16;
+#define HMOE_ROUTE(NC, GR)                                                                                           \
+  hipLaunchKernelGGL((route_topk_kernel<NC, GR>), dim3(grid), dim3(256), 0, s, xp, ldx, wp, bias, (int)T, (int)d, E, \
+                     k, renorm, scaling, logits, topk_ids, topk_w)
+#define HMOE_ROUTE_G(NC)        \
+  if (group == 8)               \
+    HMOE_ROUTE(NC, 8);          \
+  else if (group == 16)         \
+    HMOE_ROUTE(NC, 16);         \
+  else if (group == 32)         \
+    HMOE_ROUTE(NC, 32);         \
+  else                          \
+    HMOE_ROUTE(NC, 64)
+  if (nch <= 1) {
+    HMOE_ROUTE_G(1);
+  } else if (nch <= 2) {
+    HMOE_ROUTE_G(2);
+  } else if (nch <= 3) {
+    HMOE_ROUTE_G(3);
+  } else if (nch <= 4) {
+    HMOE_ROUTE_G(4);
+  } else if (nch <= 8) {
+    if (group == 8)
+      HMOE_ROUTE(8, 8);
+    else
+      HMOE_ROUTE(8, 16);
+  } else if (nch <= 16) {
+    if (group == 8)
+      HMOE_ROUTE(16, 8);
+    else
+      HMOE_ROUTE(16, 16);
+  } else {
     return HMOE_ERR_SHAPE;
+  }
+#undef HMOE_ROUTE_G
 #undef HMOE_ROUTE
   HMOE_CHECK_LAUNCH();
   return HMOE_OK;
@@ -729,7 +926,7 @@ int hmoe_combine_bwd(const void* dout, const void* yhat, const int32_t* order, c
 }
 
 size_t hmoe_router_bwd_workspace_size(int64_t T, int E, int64_t d) {
-  const int64_t nchunk = (T + kRouterTC - 1) / kRouterTC;
+  const int64_t nchunk = (T + kDwrChunk - 1) / kDwrChunk;
   return (size_t)(nchunk > 0 ? nchunk : 1) * (size_t)E * (size_t)d * 4;
 }
 
@@ -749,14 +946,14 @@ int hmoe_router_bwd(const float* logits, const int32_t* topk_ids, const float* d
     HMOE_CHECK_LAUNCH();
   }
   if (dwr) {
-    const int nchunk = (int)((T + kRouterTC - 1) / kRouterTC);
+    const int nchunk = (int)((T + kDwrChunk - 1) / kDwrChunk);
     float* part = static_cast<float*>(workspace);
     if (nchunk > 0) {
-      hipLaunchKernelGGL(router_dwr_partial_kernel, dim3(nchunk, (E + kRouterEG - 1) / kRouterEG), dim3(256), 0, s,
+      hipLaunchKernelGGL(router_dwr_partial_kernel, dim3(nchunk, (unsigned)((d + 511) / 512)), dim3(256), 0, s,
                          dlogits, static_cast<const uint16_t*>(x), ldx, T, E, d, part);
       HMOE_CHECK_LAUNCH();
     }
-    hipLaunchKernelGGL(router_dwr_reduce_kernel, dim3(grid_for((int64_t)E * d, 256, 4096)), dim3(256), 0, s, part,
+    hipLaunchKernelGGL(router_dwr_reduce_kernel, dim3(grid_for((int64_t)E * d, 64, 4096)), dim3(256), 0, s, part,
                        nchunk, E, d, dwr, dwr_dtype == HMOE_DT_BF16);
     HMOE_CHECK_LAUNCH();
   }
@@ -771,13 +968,29 @@ int hmoe_unpermute_bwd(const void* dxs, int dxs_dtype, const int32_t* inv_pos, c
   if (!dxs || !inv_pos || !dx || d % 8 || !al16(dxs) || !al16(dx)) return HMOE_ERR_ARG;
   if (dlogits && (!wr || E <= 0 || !al16(wr))) return HMOE_ERR_ARG;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int64_t work = T * (d / 8);
-  if (dxs_dtype == HMOE_DT_F32)
-    hipLaunchKernelGGL(unpermute_bwd_kernel<true>, dim3(grid_for(work, 256, 65536)), dim3(256), 0, s, dxs, inv_pos,
-                       dlogits, static_cast<const uint16_t*>(wr), T, k, d, E, static_cast<uint16_t*>(dx));
-  else
-    hipLaunchKernelGGL(unpermute_bwd_kernel<false>, dim3(grid_for(work, 256, 65536)), dim3(256), 0, s, dxs, inv_pos,
-                       dlogits, static_cast<const uint16_t*>(wr), T, k, d, E, static_cast<uint16_t*>(dx));
+  // one thread per 8 columns, up to 256 threads per column slab; workgroups walk the tokens
+  const int64_t vec = d / 8;
+  const int threads = (int)(vec >= 256 ? 256 : ((vec + 63) / 64) * 64);
+  const unsigned slabs = (unsigned)((vec + threads - 1) / threads);
+  const unsigned tgrid = (unsigned)((T + 1) / 2 < 4096 ? (T + 1) / 2 : 4096);
+  const uint16_t* wp = static_cast<const uint16_t*>(wr);
+  uint16_t* dxp = static_cast<uint16_t*>(dx);
+  const bool regs = dlogits == nullptr || E <= 16;
+#define HMOE_UNPERM(F, EM)                                                                                         \
+  hipLaunchKernelGGL((unpermute_bwd_kernel<F, EM>), dim3(tgrid, slabs), dim3(threads), 0, s, dxs, inv_pos, dlogits, \
+                     wp, T, k, d, E, dxp)
+  if (dxs_dtype == HMOE_DT_F32) {
+    if (regs)
+      HMOE_UNPERM(true, 16);
+    else
+      HMOE_UNPERM(true, 0);
+  } else {
+    if (regs)
+      HMOE_UNPERM(false, 16);
+    else
+      HMOE_UNPERM(false, 0);
+  }
+#undef HMOE_UNPERM
   HMOE_CHECK_LAUNCH();
   return HMOE_OK;
 }

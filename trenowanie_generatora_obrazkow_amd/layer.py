@@ -19,17 +19,6 @@ import torch.nn as nn
 from . import ops
 
 
-_SIDE_STREAMS = {}
-
-
-def _side_stream(device):
-    """One default-priority side stream per device for the weight-gradient GEMMs."""
-    key = torch.device(device).index
-    if key not in _SIDE_STREAMS:
-        _SIDE_STREAMS[key] = torch.cuda.Stream(device=device)
-    return _SIDE_STREAMS[key]
-
-
 class _MoEFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, wr, wgu, wd, bias, k, renorm, grad_dtype):
@@ -62,28 +51,20 @@ class _MoEFunction(torch.autograd.Function):
         M = T * k
         disp = ops.Dispatch(counts, None, None, order, a_idx, inv_pos, w_sorted, xs)
         dout = dout.contiguous().to(torch.bfloat16)
-        # The two weight-gradient GEMMs run on a side stream beside the dgrad chain: their tiles fill the CUs the
-        # dgrad GEMMs leave idle in their last round.  The main stream joins the side stream before returning, so
-        # every tensor used on the side stream stays alive and ordered before any later reuse of its memory.
-        main = torch.cuda.current_stream(x.device)
-        side = _side_stream(x.device)
+        # One stream: every GEMM is a persistent launch sized to own all CUs, so two of them side by side only
+        # queue each other's workgroups behind long-running tiles.
         dys, dtw = ops.combine_bwd(dout, yhat, disp, k)
-        side.wait_stream(main)
         dwd = dwgu = None
         if ctx.needs_input_grad[3]:
-            with torch.cuda.stream(side):
-                dwd = ops.grouped_wgrad(act, dys, counts, E, dtype=ctx.grad_dtype)
+            dwd = ops.grouped_wgrad(act, dys, counts, E, dtype=ctx.grad_dtype)
         dgu = ops.down_dgrad_swiglu(dout, wd, counts, M, gu, a_idx=a_idx, w_sorted=w_sorted)
         if ctx.needs_input_grad[2]:
-            side.wait_stream(main)
-            with torch.cuda.stream(side):
-                dwgu = ops.grouped_wgrad(xs, dgu, counts, E, dtype=ctx.grad_dtype)
+            dwgu = ops.grouped_wgrad(xs, dgu, counts, E, dtype=ctx.grad_dtype)
         dxs = ops.gate_up_dgrad(dgu, wgu, counts, M)
         dwr_dtype = wr.dtype if wr.dtype in (torch.bfloat16, torch.float32) else torch.float32
         dl, dwr = ops.router_bwd(logits, ids, dtw, x, renorm=ctx.renorm, dwr_dtype=dwr_dtype,
                                  want_dwr=ctx.needs_input_grad[1])
         dx = ops.unpermute_bwd(dxs, inv_pos, T, k, dlogits=dl, wr=wr) if ctx.needs_input_grad[0] else None
-        main.wait_stream(side)
         if dwr is not None and dwr.dtype != wr.dtype:
             dwr = dwr.to(wr.dtype)
         if dwgu is not None and dwgu.dtype != wgu.dtype:
