@@ -30,9 +30,6 @@ constexpr int kMaxEGemm = 1024;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-// Source of masked lanes' direct loads: 64 zero bytes.
-__device__ __attribute__((aligned(64))) uint16_t g_zero_page[32];
-
 template <int BM_, int BN_, int WM_, int WN_, int GM_>
 struct Cfg {
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, GM = GM_;
@@ -59,12 +56,36 @@ __device__ __forceinline__ int swz_k(int row) { return (row >> 2) & 3; }
 __device__ __forceinline__ int swz_mn(int k) { return ((2 * (k & 3)) | ((k >> 3) & 1)) & 7; }
 __device__ __forceinline__ int mn_chunk(int k, int c) { return (c & ~7) | ((c ^ swz_mn(k)) & 7); }
 
-// Direct global -> LDS copy of 16 bytes per lane: lane l's bytes land at lds + 16 l (lds is wave-uniform; it goes
-// to M0).  Issued as inline asm so the compiler does not guard every later LDS read with a vmcnt(0) wait for it:
-// completion of these copies is tracked explicitly (wait_vm + barrier before a slice is read).
-__device__ __forceinline__ void g2lds(const uint16_t* src, char* lds) {
+// ----------------------------------------------------------------------------------------------------------------
+// Direct global -> LDS copies through buffer loads.  Each operand tile has a wave-uniform buffer descriptor whose
+// base is the tile's (or expert's) origin; a lane's 32-bit byte offset inside it is fixed for the whole tile and the
+// k-slice advance is the uniform scalar offset, so a slice costs one scalar add per operand plus one instruction
+// per copy.  Lanes whose source lies outside the operand (ragged expert ends, N tails, K tails) use an offset of
+// 2^31, beyond the descriptor's range: the hardware returns zeros for them and writes those zeros to LDS, so every
+// LDS slot is written each slice.  Offsets of real data must stay below 2^31 - 16 bytes from the base (checked on the
+// host).
+// ----------------------------------------------------------------------------------------------------------------
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t kOOB = 0x80000000u;
+
+__device__ __forceinline__ i32x4 make_rsrc(const void* base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  // the base is the same for every lane; readfirstlane tells the compiler so, which puts the descriptor in SGPRs
+  r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  r.y = __builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));  // base[47:32]; stride 0, no swizzle
+  r.z = 0x7FFFFFF0;                // range in bytes (offsets at or above it read zeros)
+  r.w = 0x00020000;                // 32-bit data format: a raw dword buffer
+  return r;
+}
+
+// 16 bytes per lane from base + voff + soff into LDS at lds + 16 * lane (lds is wave-uniform; it goes to M0).
+// Issued as inline asm so the compiler does not guard every later LDS read with a vmcnt(0) wait for it: completion
+// of these copies is tracked explicitly (wait_vm + barrier before a slice is read).
+__device__ __forceinline__ void buf2lds(uint32_t voff, i32x4 rsrc, uint32_t soff, char* lds) {
   const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(lds);
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src) : "memory", "m0");
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :: "s"(m0), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
 }
 
 // K-major operand: ROWS rows x 32 k per slice; ROWS/16 copy instructions per slice (each 16 rows x 64 bytes),
@@ -74,17 +95,21 @@ struct KTile {
   static constexpr int INSTR = ROWS / 16;
   static constexpr int PER_WAVE = INSTR / NWAVES;
   static_assert(INSTR % NWAVES == 0, "K tile copy instructions must divide over the waves");
-  const uint16_t* rowp[PER_WAVE];  // row base (k = 0) of the row this lane copies, or the zero page
-  int chunk[PER_WAVE];             // logical k-chunk this lane copies
+  uint32_t voff[PER_WAVE];  // byte offset of (row, k = 8 * chunk) from the base, or kOOB
+  int chunk[PER_WAVE];      // logical k-chunk this lane copies
+  i32x4 rsrc;
   int K;
   // lane l of instruction (wave w, i) fills LDS row 16*(w*PER_WAVE + i) + l/4, physical chunk l%4
   __device__ __forceinline__ int row_of(int wave, int lane, int i) const { return 16 * (wave * PER_WAVE + i) + lane / 4; }
   __device__ __forceinline__ void issue(char* lds_tile, int wave, int lane, int k0) const {
+    const uint32_t soff = (uint32_t)k0 * 2u;
+    if (k0 + kBK <= K) {
 #pragma unroll
-    for (int i = 0; i < PER_WAVE; ++i) {
-      const int kk = k0 + chunk[i] * 8;
-      const uint16_t* src = (rowp[i] != g_zero_page && kk < K) ? rowp[i] + kk : g_zero_page;
-      g2lds(src, lds_tile + (wave * PER_WAVE + i) * 1024);
+      for (int i = 0; i < PER_WAVE; ++i) buf2lds(voff[i], rsrc, soff, lds_tile + (wave * PER_WAVE + i) * 1024);
+    } else {  // K tail: chunks at or past K read zeros
+#pragma unroll
+      for (int i = 0; i < PER_WAVE; ++i)
+        buf2lds(k0 + chunk[i] * 8 < K ? voff[i] : kOOB, rsrc, soff, lds_tile + (wave * PER_WAVE + i) * 1024);
     }
   }
   // Lane part of a fragment read address: row w32*32 + lane%32, k-chunk lane/32 (ks = 0), swizzled.  The
@@ -108,16 +133,20 @@ struct MNTile {
   static constexpr int CPR = ROWS / 8;      // 16-byte chunks per k-row
   static constexpr int KPI = 64 / CPR;      // k-rows per copy instruction
   static_assert(INSTR % NWAVES == 0, "MN tile copy instructions must divide over the waves");
-  const uint16_t* colp[PER_WAVE];  // (k = 0, first of the 8 columns) of the chunk this lane copies, or zero page
-  int krow[PER_WAVE];              // k-row within the slice
-  int64_t ld;
+  uint32_t voff[PER_WAVE];  // byte offset of (k-row, first of the lane's 8 columns) from the base, or kOOB
+  int krow[PER_WAVE];       // k-row within the slice
+  i32x4 rsrc;
+  uint32_t kstep;           // bytes per k-row (ld * 2)
   int Kvalid;
   __device__ __forceinline__ void issue(char* lds_tile, int wave, int lane, int k0) const {
+    const uint32_t soff = (uint32_t)k0 * kstep;
+    if (k0 + kBK <= Kvalid) {
 #pragma unroll
-    for (int i = 0; i < PER_WAVE; ++i) {
-      const int k = k0 + krow[i];
-      const uint16_t* src = (colp[i] != g_zero_page && k < Kvalid) ? colp[i] + (int64_t)k * ld : g_zero_page;
-      g2lds(src, lds_tile + (wave * PER_WAVE + i) * 1024);
+      for (int i = 0; i < PER_WAVE; ++i) buf2lds(voff[i], rsrc, soff, lds_tile + (wave * PER_WAVE + i) * 1024);
+    } else {  // K tail: k-rows at or past Kvalid read zeros
+#pragma unroll
+      for (int i = 0; i < PER_WAVE; ++i)
+        buf2lds(k0 + krow[i] < Kvalid ? voff[i] : kOOB, rsrc, soff, lds_tile + (wave * PER_WAVE + i) * 1024);
     }
   }
   // lane l of instruction (wave w, i): k-row (w*PER_WAVE + i)*KPI + l / CPR, physical chunk l % CPR
@@ -178,11 +207,17 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// Pins an accumulator fragment in AGPRs up to this point of the program.  Without it the register allocator may copy
+// every accumulator to VGPRs at the end of the main loop (256 values: a spill); with it each fragment is read out of
+// the AGPRs only where the epilogue uses it.  The empty asm counts as the fragment's last writer, so the MFMA -> VALU
+// read wait states must be provided explicitly after the main loop (see the kernel).
+__device__ __forceinline__ void pin_agpr(f32x16& v) { asm volatile("" : "+a"(v)); }
+
 // ----------------------------------------------------------------------------------------------------------------
 // Kernel parameters
 // ----------------------------------------------------------------------------------------------------------------
 enum Mode { MGROUP = 0, KGROUP = 1 };
-enum Epi { EPI_STORE = 0, EPI_SWIGLU = 1, EPI_SWIGLU_BWD = 2, EPI_WGRAD = 3 };
+enum Epi { EPI_STORE = 0, EPI_SWIGLU = 1, EPI_SWIGLU_BWD = 2, EPI_WGRAD = 3, EPI_STORE_F32 = 4 };
 
 struct GemmParams {
   // M side (A).  MGROUP: rows of A (sorted row r, or a_idx[r] when gather), K contiguous, row stride lda.
@@ -222,6 +257,11 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   __shared__ int64_t s_rstart[kMaxEGemm + 1];
   __shared__ int s_tstart[kMaxEGemm + 1];
+  // per-row epilogue inputs of the tile (scatter index, routing weight), double-buffered by tile parity: a wave
+  // that has finished its epilogue may already fill the next tile's while others still read this one
+  // (2 KB each: 256 rows plus up to 3 leading rows, since the copy starts at the 16-byte boundary below row0)
+  __shared__ __attribute__((aligned(16))) int s_rowy[2][512];
+  __shared__ __attribute__((aligned(16))) float s_rowsc[2][512];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -295,7 +335,8 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
   int slot = blockIdx.x;
   if ((G & 7) == 0) slot = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
 
-  for (int tile = slot; tile < total; tile += G) {
+  int tile_iter = 0;
+  for (int tile = slot; tile < total; tile += G, ++tile_iter) {
     // ---- tile decode ----
     int mt, nb;
     {
@@ -333,23 +374,26 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
     }
     const int n0 = nb * (EPI == EPI_SWIGLU ? C::BN / 2 : C::BN);
 
-    // ---- copy sources for this tile ----
+    // ---- copy sources for this tile (buffer bases and per-lane byte offsets) ----
     if constexpr (MODE == MGROUP) {
       static_assert(!A_MN, "MGROUP A is K-contiguous");
       ta.K = p.K;
+      // gathered rows are addressed from A itself; contiguous rows from the tile's first row
+      ta.rsrc = make_rsrc(p.a_idx ? p.A : p.A + row0 * p.lda);
 #pragma unroll
       for (int i = 0; i < ta.PER_WAVE; ++i) {
         const int rr = ta.row_of(wave, lane, i);
         const int64_t r = row0 + rr;
-        const uint16_t* ptr = g_zero_page;
+        const int c = (lane & 3) ^ swz_k(rr);
+        uint32_t vo = kOOB;
         if (r < row_end) {
-          const int64_t src = p.a_idx ? (int64_t)p.a_idx[r] : r;
-          ptr = p.A + src * p.lda;
+          const int64_t src = p.a_idx ? (int64_t)p.a_idx[r] : (int64_t)rr;
+          vo = (uint32_t)(src * p.lda * 2 + c * 16);
         }
-        ta.rowp[i] = ptr;
-        ta.chunk[i] = (lane & 3) ^ swz_k(rr);
+        ta.voff[i] = vo;
+        ta.chunk[i] = c;
       }
-      const uint16_t* Be = p.B + (int64_t)e * p.strideBe;
+      tb.rsrc = make_rsrc(p.B + (int64_t)e * p.strideBe);
       auto gcol = [&](int nn, int& col) -> bool {  // tile column -> weight column
         if (EPI == EPI_SWIGLU) {
           const int half = nn / (C::BN / 2);  // tile columns [0, BN/2) gate, [BN/2, BN) the matching up
@@ -362,45 +406,74 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
         }
       };
       if constexpr (B_MN) {
-        tb.ld = p.ldb;
+        tb.kstep = (uint32_t)(p.ldb * 2);
         tb.Kvalid = p.K;
 #pragma unroll
         for (int i = 0; i < tb.PER_WAVE; ++i) {
           int k, nn, col;
           tb.slot(wave, lane, i, k, nn);
           tb.krow[i] = k;
-          tb.colp[i] = gcol(nn, col) ? Be + col : g_zero_page;
+          tb.voff[i] = gcol(nn, col) ? (uint32_t)(((int64_t)k * p.ldb + col) * 2) : kOOB;
         }
       } else {
         tb.K = p.K;
 #pragma unroll
         for (int i = 0; i < tb.PER_WAVE; ++i) {
           const int nn = tb.row_of(wave, lane, i);
+          const int c = (lane & 3) ^ swz_k(nn);
           int col;
-          tb.rowp[i] = gcol(nn, col) ? Be + (int64_t)col * p.ldb : g_zero_page;
-          tb.chunk[i] = (lane & 3) ^ swz_k(nn);
+          tb.voff[i] = gcol(nn, col) ? (uint32_t)((int64_t)col * p.ldb * 2 + c * 16) : kOOB;
+          tb.chunk[i] = c;
         }
       }
     } else {
       static_assert(A_MN && B_MN, "KGROUP operands are MN-contiguous");
-      ta.ld = p.lda;
+      ta.rsrc = make_rsrc(p.A + kstart * p.lda + i0);
+      ta.kstep = (uint32_t)(p.lda * 2);
       ta.Kvalid = kvalid;
-      tb.ld = p.ldb;
+      tb.rsrc = make_rsrc(p.B + kstart * p.ldb + n0);
+      tb.kstep = (uint32_t)(p.ldb * 2);
       tb.Kvalid = kvalid;
 #pragma unroll
       for (int i = 0; i < ta.PER_WAVE; ++i) {
         int k, ic;
         ta.slot(wave, lane, i, k, ic);
         ta.krow[i] = k;
-        ta.colp[i] = (i0 + ic < p.P) ? p.A + kstart * p.lda + i0 + ic : g_zero_page;
+        ta.voff[i] = (i0 + ic < p.P) ? (uint32_t)(((int64_t)k * p.lda + ic) * 2) : kOOB;
       }
 #pragma unroll
       for (int i = 0; i < tb.PER_WAVE; ++i) {
         int k, nc;
         tb.slot(wave, lane, i, k, nc);
         tb.krow[i] = k;
-        tb.colp[i] = (n0 + nc < p.N) ? p.B + kstart * p.ldb + n0 + nc : g_zero_page;
+        tb.voff[i] = (n0 + nc < p.N) ? (uint32_t)(((int64_t)k * p.ldb + nc) * 2) : kOOB;
       }
+    }
+
+    // ---- per-row epilogue inputs: copied into LDS by wave 0 with the same direct loads as the operand tiles,
+    // ahead of the first slice, so they are complete when slice 0 is and no compiler-visible load stays pending ----
+    const int par = tile_iter & 1;
+    constexpr bool ROWDATA = MODE == MGROUP && (EPI == EPI_STORE || EPI == EPI_STORE_F32 || EPI == EPI_SWIGLU_BWD);
+    static_assert(!ROWDATA || C::BM <= 256, "row data buffers hold 256 rows");
+    // The copies start at the 16-byte boundary at or below row0 (the direct loads move aligned 16-byte chunks) and
+    // take two instructions (1 KB + 16 bytes) so that the shifted 256 rows are always covered.
+    [[maybe_unused]] int y_sh = 0, sc_sh = 0;  // leading rows in front of row0
+    if constexpr (ROWDATA) {
+      auto copy_rows = [&](const void* arr, int esz, char* dst) -> int {
+        const uintptr_t first = reinterpret_cast<uintptr_t>(arr) + (uintptr_t)row0 * esz;
+        const uintptr_t base = first & ~(uintptr_t)15;
+        const int sh = (int)(first - base) / esz;
+        const int64_t bytes = (p.M - row0) * esz + (int64_t)(first - base);  // valid bytes from the aligned base
+        if (wave == 0) {
+          i32x4 rs = make_rsrc(reinterpret_cast<const void*>(base));
+          rs.z = __builtin_amdgcn_readfirstlane((int)min(bytes, (int64_t)0x7FFFFFF0));
+          buf2lds((uint32_t)lane * 16u, rs, 0u, dst);
+          buf2lds(lane == 0 ? 1024u : kOOB, rs, 0u, dst + 1024);
+        }
+        return sh;
+      };
+      if (EPI != EPI_SWIGLU_BWD && p.y_idx) y_sh = copy_rows(p.y_idx, 4, reinterpret_cast<char*>(s_rowy[par]));
+      if (p.scale) sc_sh = copy_rows(p.scale, p.scale_f32 ? 4 : 2, reinterpret_cast<char*>(s_rowsc[par]));
     }
 
     // ---- main loop: NSTAGE-deep ring of k-slices ----
@@ -501,164 +574,206 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
       mfmas(f1);
       interleave();
     }
-    lds_barrier();  // every wave is done with the ring before the epilogue reuses it
+    lds_barrier();  // every wave is done with the ring before the next tile refills it
+    // The epilogue's pin_agpr() hides the last MFMA write from the compiler's hazard tracking, so the wait states a
+    // VALU read of an MFMA result needs (19 for a 16-pass MFMA; the 32x32x16 bf16 MFMA has 8 passes) are given here.
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 
-    // ---- epilogue, through LDS in bands of 64 rows ----
-    // Pass a: every wave parks its fragment row a (rows a*64 + wm*32 + 0..31 of the tile, all its columns) in LDS
-    // as fp32 [64][BN + 4] (the padding makes both phases' 16-byte accesses bank-conflict free), then the workgroup
-    // walks the band row-contiguously: thread t owns band row t/4 and the 8-column groups (t%4)*8 + 32m, so each
-    // global store is a 16- or 32-byte vector and four neighbouring threads cover 64 contiguous bytes of a row.
-    constexpr int EP = C::BN + 4;  // band row pitch, floats
-    static_assert(64 * EP * 4 <= C::LDS_BYTES, "epilogue band must fit in the ring");
-    float* band = reinterpret_cast<float*>(smem);
+    // ---- epilogue: per-wave staging in LDS, then row-contiguous 16-byte stores ----
+    // Lane l of wave (wm, wn) holds, for fragment (a, b) and group g, output row a*FSM + wm*32 + l%32 and the 4
+    // consecutive columns b*FSN + wn*32 + 8g + 4*(l/32) + 0..3 (acc[a][b][4g + 0..3]).  Pass a converts the wave's
+    // 32 rows and parks them in "sub-planes" of 32 rows x 128 bytes, then reads them back row-contiguously: 8 lanes
+    // per 128-byte row, each storing 16 bytes, so a store instruction writes 64-byte segments instead of scattered
+    // 8-byte pieces.  The sub-planes live in the ring bytes this wave's own direct loads fill (its A and B parts of
+    // each stage), which no other wave writes: the epilogue needs no barrier, and the wave's next-tile loads are
+    // issued after its last read in program order.
     const int lrow = lane & 31;
     const int lcol = 4 * (lane >> 5);
-    const int q = tid >> 2, s = tid & 3;
+    constexpr int CH = C::A_BYTES / C::NWAVES;  // bytes per ring part filled by one wave
+    static_assert(C::A_BYTES == C::B_BYTES && CH >= 1024 && 4096 % CH == 0, "staging chunks");
+    auto chunk = [&](int q) -> char* { return smem + (q >> 1) * C::STAGE_BYTES + (q & 1) * C::A_BYTES + wave * CH; };
+    // sub-plane sp, row r (0..31), byte offset within the 128-byte row; 16-byte chunks XOR-swizzled by r & 7
+    auto sp_addr = [&](int sp, int r, int byte) -> char* {
+      const int lin = r * 128;
+      return chunk(sp * (4096 / CH) + lin / CH) + lin % CH + ((((byte >> 4) ^ r) & 7) << 4) + (byte & 15);
+    };
+    // park the 4 values of fragment (a, b), group g (rows lrow) into a bf16 / fp32 array starting at sub-plane sp0
+    auto park_bf16 = [&](int sp0, int b, int g, uint32_t lo, uint32_t hi) {
+      const int byte = (b * 32 + 8 * g + lcol) * 2;
+      *reinterpret_cast<uint2*>(sp_addr(sp0 + byte / 128, lrow, byte % 128)) = make_uint2(lo, hi);
+    };
+    [[maybe_unused]] auto park_f32 = [&](int sp0, int b, int g, float4 v) {
+      const int byte = (b * 32 + 8 * g + lcol) * 4;
+      *reinterpret_cast<float4*>(sp_addr(sp0 + byte / 128, lrow, byte % 128)) = v;
+    };
+    // read back an array of rowbytes bytes per row (es bytes per element) from sub-plane sp0 on: calls
+    // st(r, tile_col, uint4) for each of the lane's 16-byte pieces (row r of the wave's 32, tile column of its first
+    // element)
+    auto drain = [&](int sp0, int rowbytes, int es, auto&& st) {
+      for (int sp = 0; sp * 128 < rowbytes; ++sp)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int idx = j * 64 + lane, r = idx >> 3, c = idx & 7;
+          if (sp * 128 + c * 16 >= rowbytes) continue;  // a narrow array fills only part of its last sub-plane
+          const uint4 v = *reinterpret_cast<const uint4*>(sp_addr(sp0 + sp, r, c * 16));
+          const int cw = (sp * 128 + c * 16) / es;  // column within the wave's FN*32
+          st(r, (cw / 32) * C::FSN + wn * 32 + cw % 32, v);
+        }
+    };
+    [[maybe_unused]] auto row_scale = [&](int rt) -> float {
+      if (!p.scale) return 1.0f;
+      return p.scale_f32 ? s_rowsc[par][rt + sc_sh] : bf2f(reinterpret_cast<const uint16_t*>(s_rowsc[par])[rt + sc_sh]);
+    };
+    auto col_of = [&](int b, int g) { return b * C::FSN + wn * 32 + 8 * g + lcol; };  // tile column (write phase)
 #pragma unroll
     for (int a = 0; a < C::FM; ++a) {
-      // SwiGLU backward: issue this pass's [g | u] loads first, so their latency overlaps phase 1 and the barrier
-      // (rows / columns outside the tile load a valid location and are never used)
-      [[maybe_unused]] uint4 gpre[C::BN / 32], upre[C::BN / 32];
-      if constexpr (EPI == EPI_SWIGLU_BWD) {
-        const int64_t r = row0 + a * 64 + q;
-        const uint16_t* gurow = p.gu_in + (r < row_end ? r : row0) * (int64_t)(2 * p.h);
-#pragma unroll
-        for (int m = 0; m < C::BN / 32; ++m) {
-          const int j = n0 + 32 * m + 8 * s;
-          const int jc = j < p.N ? j : 0;
-          gpre[m] = *reinterpret_cast<const uint4*>(gurow + jc);
-          upre[m] = *reinterpret_cast<const uint4*>(gurow + p.h + jc);
-        }
-      }
-      // phase 1: park fragment row a
-#pragma unroll
-      for (int b = 0; b < C::FN; ++b)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          float* dst = band + (wm * 32 + lrow) * EP + b * C::FSN + wn * 32 + 8 * g + lcol;
-          *reinterpret_cast<float4*>(dst) =
-              make_float4(acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2], acc[a][b][4 * g + 3]);
-        }
-      lds_barrier();
-      // phase 2: band row q, columns 32m + 8s + 0..7
-      const float* brow = band + q * EP + 8 * s;
-      auto ld8 = [&](int col, float* v) {
-        const float4 x0 = *reinterpret_cast<const float4*>(brow + col);
-        const float4 x1 = *reinterpret_cast<const float4*>(brow + col + 4);
-        v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
-        v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
-      };
-      auto pack8 = [](const float* v) {
-        return make_uint4(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]), pack_bf2(v[4], v[5]), pack_bf2(v[6], v[7]));
-      };
+      const int rbase = a * C::FSM + wm * 32;  // tile row of the wave's row 0 in this pass
       if constexpr (EPI == EPI_WGRAD) {
-        const int i = i0 + a * 64 + q;
-        if (i < p.P) {
-          char* crow = reinterpret_cast<char*>(p.C) + ((int64_t)e * p.strideCe + (int64_t)i * p.ldc) * (p.c_f32 ? 4 : 2);
 #pragma unroll
-          for (int m = 0; m < C::BN / 32; ++m) {
-            const int n = n0 + 32 * m + 8 * s;
-            if (n >= p.N) continue;
-            float v[8];
-            ld8(32 * m, v);
-            if (p.c_f32) {
-              float4* d = reinterpret_cast<float4*>(crow + (int64_t)n * 4);
-              d[0] = make_float4(v[0], v[1], v[2], v[3]);
-              d[1] = make_float4(v[4], v[5], v[6], v[7]);
-            } else {
-              *reinterpret_cast<uint4*>(crow + (int64_t)n * 2) = pack8(v);
-            }
+        for (int b = 0; b < C::FN; ++b) {
+          pin_agpr(acc[a][b]);
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const f32x16& v = acc[a][b];
+            if (p.c_f32)
+              park_f32(0, b, g, make_float4(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]));
+            else
+              park_bf16(0, b, g, cvt_bf2(v[4 * g], v[4 * g + 1]), cvt_bf2(v[4 * g + 2], v[4 * g + 3]));
           }
         }
-      } else if constexpr (EPI == EPI_STORE) {
-        const int64_t r = row0 + a * 64 + q;
-        if (r < row_end) {
-          float sc = 1.0f;
-          if (p.scale) sc = p.scale_f32 ? reinterpret_cast<const float*>(p.scale)[r]
-                                        : bf2f(reinterpret_cast<const uint16_t*>(p.scale)[r]);
-          const int64_t yr = p.y_idx ? (int64_t)p.y_idx[r] : r;
-          char* yrow = reinterpret_cast<char*>(p.C) + yr * p.ldc * (p.c_f32 ? 4 : 2);
+        const int es = p.c_f32 ? 4 : 2;
+        drain(0, C::FN * 32 * es, es, [&](int r, int tc, uint4 v) {
+          const int i = i0 + rbase + r, n = n0 + tc;
+          if (i < p.P && n < p.N)
+            *reinterpret_cast<uint4*>(reinterpret_cast<char*>(p.C) +
+                                      ((int64_t)e * p.strideCe + (int64_t)i * p.ldc + n) * es) = v;
+        });
+      } else if constexpr (EPI == EPI_STORE || EPI == EPI_STORE_F32) {
+        constexpr int ES = EPI == EPI_STORE_F32 ? 4 : 2;
+        constexpr int RB = C::FN * 32 * ES, NSP = (RB + 127) / 128;  // y's row bytes, sub-planes; yhat (bf16) follows
+        const float sc = row_scale(rbase + lrow);   // 1 without a scale: the product is then exact
 #pragma unroll
-          for (int m = 0; m < C::BN / 32; ++m) {
-            const int n = n0 + 32 * m + 8 * s;
-            if (n >= p.N) continue;
-            float v[8];
-            ld8(32 * m, v);
-            if (p.aux) *reinterpret_cast<uint4*>(p.aux + r * p.ldc + n) = pack8(v);
-            if (p.scale) {
+        for (int b = 0; b < C::FN; ++b) {
+          pin_agpr(acc[a][b]);
 #pragma unroll
-              for (int t = 0; t < 8; ++t) v[t] = v[t] * sc;
-            }
-            if (p.c_f32) {
-              float4* d = reinterpret_cast<float4*>(yrow + (int64_t)n * 4);
-              d[0] = make_float4(v[0], v[1], v[2], v[3]);
-              d[1] = make_float4(v[4], v[5], v[6], v[7]);
-            } else {
-              *reinterpret_cast<uint4*>(yrow + (int64_t)n * 2) = pack8(v);
-            }
+          for (int g = 0; g < 4; ++g) {
+            const f32x16& v = acc[a][b];
+            if (p.aux) park_bf16(NSP, b, g, cvt_bf2(v[4 * g], v[4 * g + 1]), cvt_bf2(v[4 * g + 2], v[4 * g + 3]));
+            const float v0 = v[4 * g] * sc, v1 = v[4 * g + 1] * sc, v2 = v[4 * g + 2] * sc, v3 = v[4 * g + 3] * sc;
+            if constexpr (EPI == EPI_STORE_F32)
+              park_f32(0, b, g, make_float4(v0, v1, v2, v3));
+            else
+              park_bf16(0, b, g, cvt_bf2(v0, v1), cvt_bf2(v2, v3));
           }
         }
+        drain(0, RB, ES, [&](int r, int tc, uint4 v) {
+          const int rt = rbase + r;
+          const int64_t row = row0 + rt;
+          const int n = n0 + tc;
+          if (row < row_end && n < p.N) {
+            const int64_t yr = p.y_idx ? (int64_t)s_rowy[par][rt + y_sh] : row;
+            *reinterpret_cast<uint4*>(reinterpret_cast<char*>(p.C) + (yr * p.ldc + n) * ES) = v;
+          }
+        });
+        if (p.aux)
+          drain(NSP, C::FN * 32 * 2, 2, [&](int r, int tc, uint4 v) {
+            const int64_t row = row0 + rbase + r;
+            const int n = n0 + tc;
+            if (row < row_end && n < p.N) *reinterpret_cast<uint4*>(p.aux + row * p.ldc + n) = v;
+          });
       } else if constexpr (EPI == EPI_SWIGLU) {
-        // tile columns [0, BN/2) are gate, [BN/2, BN) the matching up columns
-        const int64_t r = row0 + a * 64 + q;
-        if (r < row_end) {
-          uint16_t* arow = reinterpret_cast<uint16_t*>(p.C) + r * p.ldc;
-          uint16_t* grow = p.aux ? p.aux + r * (int64_t)(2 * p.h) : nullptr;
+        // fragments b < FN/2 hold gate columns, b + FN/2 the matching up columns (tile columns + BN/2); the wave's
+        // activation columns are b*32 + ... for b < FN/2: sub-plane 0 = act, 1 = g, 2 = u (one each for FN = 4)
+        constexpr int RB = C::FN / 2 * 32 * 2, NSP = (RB + 127) / 128;  // row bytes and sub-planes of each array
 #pragma unroll
-          for (int m = 0; m < C::BN / 64; ++m) {
-            const int j = n0 + 32 * m + 8 * s;
-            if (j >= p.N) continue;
-            float gv[8], uv[8], o[8];
-            ld8(32 * m, gv);
-            ld8(C::BN / 2 + 32 * m, uv);
-            uint32_t gb[8], ub[8];
+        for (int b = 0; b < C::FN / 2; ++b) {
+          pin_agpr(acc[a][b]);
+          pin_agpr(acc[a][b + C::FN / 2]);
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-              gb[t] = f2bf(gv[t]);
-              ub[t] = f2bf(uv[t]);
-              const float sl = bf2f(f2bf(silu_f(bf2f(gb[t]))));
-              o[t] = sl * bf2f(ub[t]);
-            }
-            *reinterpret_cast<uint4*>(arow + j) = pack8(o);
-            if (grow) {
-              *reinterpret_cast<uint4*>(grow + j) = make_uint4(gb[0] | (gb[1] << 16), gb[2] | (gb[3] << 16),
-                                                               gb[4] | (gb[5] << 16), gb[6] | (gb[7] << 16));
-              *reinterpret_cast<uint4*>(grow + p.h + j) = make_uint4(ub[0] | (ub[1] << 16), ub[2] | (ub[3] << 16),
-                                                                     ub[4] | (ub[5] << 16), ub[6] | (ub[7] << 16));
+          for (int g = 0; g < 4; ++g) {
+            const f32x16& gv = acc[a][b];
+            const f32x16& uv = acc[a][b + C::FN / 2];
+            const uint32_t gb0 = cvt_bf2(gv[4 * g], gv[4 * g + 1]), gb1 = cvt_bf2(gv[4 * g + 2], gv[4 * g + 3]);
+            const uint32_t ub0 = cvt_bf2(uv[4 * g], uv[4 * g + 1]), ub1 = cvt_bf2(uv[4 * g + 2], uv[4 * g + 3]);
+            const float gg[4] = {bf_lo(gb0), bf_hi(gb0), bf_lo(gb1), bf_hi(gb1)};
+            const float uu[4] = {bf_lo(ub0), bf_hi(ub0), bf_lo(ub1), bf_hi(ub1)};
+            // act = bf16(bf16(silu(g)) * u) with g, u the bf16-rounded projections
+            const uint32_t sl0 = cvt_bf2(silu_f(gg[0]), silu_f(gg[1])), sl1 = cvt_bf2(silu_f(gg[2]), silu_f(gg[3]));
+            park_bf16(0, b, g, cvt_bf2(bf_lo(sl0) * uu[0], bf_hi(sl0) * uu[1]),
+                      cvt_bf2(bf_lo(sl1) * uu[2], bf_hi(sl1) * uu[3]));
+            if (p.aux) {
+              park_bf16(NSP, b, g, gb0, gb1);
+              park_bf16(2 * NSP, b, g, ub0, ub1);
             }
           }
+        }
+        drain(0, RB, 2, [&](int r, int tc, uint4 v) {
+          const int64_t row = row0 + rbase + r;
+          const int j = n0 + tc;
+          if (row < row_end && j < p.N) *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p.C) + row * p.ldc + j) = v;
+        });
+        if (p.aux) {
+          drain(NSP, RB, 2, [&](int r, int tc, uint4 v) {
+            const int64_t row = row0 + rbase + r;
+            const int j = n0 + tc;
+            if (row < row_end && j < p.N) *reinterpret_cast<uint4*>(p.aux + row * (int64_t)(2 * p.h) + j) = v;
+          });
+          drain(2 * NSP, RB, 2, [&](int r, int tc, uint4 v) {
+            const int64_t row = row0 + rbase + r;
+            const int j = n0 + tc;
+            if (row < row_end && j < p.N) *reinterpret_cast<uint4*>(p.aux + row * (int64_t)(2 * p.h) + p.h + j) = v;
+          });
         }
       } else if constexpr (EPI == EPI_SWIGLU_BWD) {
-        const int64_t r = row0 + a * 64 + q;
-        if (r < row_end) {
-          float sc = 1.0f;
-          if (p.scale) sc = bf2f(reinterpret_cast<const uint16_t*>(p.scale)[r]);
-          uint16_t* drow = reinterpret_cast<uint16_t*>(p.C) + r * (int64_t)(2 * p.h);
+        constexpr int RB = C::FN * 32 * 2, NSP = (RB + 127) / 128;  // dg row bytes and sub-planes; du follows
+        const int64_t r = row0 + rbase + lrow;
+        const int64_t rc = r < row_end ? r : row0;
+        const uint16_t* gurow = p.gu_in + rc * (int64_t)(2 * p.h);
+        const float sc = row_scale(rbase + lrow);
+        // the pass's [g | u] in the accumulator layout (8 bytes per column group), all loads issued before use
+        uint2 gl[C::FN][4], ul[C::FN][4];
 #pragma unroll
-          for (int m = 0; m < C::BN / 32; ++m) {
-            const int j = n0 + 32 * m + 8 * s;
-            if (j >= p.N) continue;
-            float v[8];
-            ld8(32 * m, v);
-            const uint4 gv = gpre[m];
-            const uint4 uv = upre[m];
-            const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
-            float dg[8], du[8];
+        for (int b = 0; b < C::FN; ++b)
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-              const float gg = (t & 1) ? bf_hi(gw[t >> 1]) : bf_lo(gw[t >> 1]);
-              const float uu = (t & 1) ? bf_hi(uw[t >> 1]) : bf_lo(uw[t >> 1]);
-              const float da = v[t] * sc;
-              const float sig = sigmoid_f(gg);
-              du[t] = da * bf2f(f2bf(gg * sig));  // the forward's stored factor bf16(silu(g)), silu_f(g) = g*sig
-              dg[t] = da * uu * sig * (1.0f + gg * (1.0f - sig));
+          for (int g = 0; g < 4; ++g) {
+            const int j = n0 + col_of(b, g);
+            const int jc = j < p.N ? j : 0;
+            gl[b][g] = *reinterpret_cast<const uint2*>(gurow + jc);
+            ul[b][g] = *reinterpret_cast<const uint2*>(gurow + p.h + jc);
+          }
+#pragma unroll
+        for (int b = 0; b < C::FN; ++b) {
+          pin_agpr(acc[a][b]);
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const float gg[4] = {bf_lo(gl[b][g].x), bf_hi(gl[b][g].x), bf_lo(gl[b][g].y), bf_hi(gl[b][g].y)};
+            const float uu[4] = {bf_lo(ul[b][g].x), bf_hi(ul[b][g].x), bf_lo(ul[b][g].y), bf_hi(ul[b][g].y)};
+            float dg[4], du[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              const float da = acc[a][b][4 * g + t] * sc;
+              const float sig = sigmoid_f(gg[t]);
+              const float sl = gg[t] * sig;
+              // du uses the forward's stored factor bf16(silu(g)); silu_f(g) = g * sig
+              du[t] = da * bf_lo(cvt_bf2(sl, sl));
+              dg[t] = da * uu[t] * sig * (1.0f + gg[t] * (1.0f - sig));
             }
-            *reinterpret_cast<uint4*>(drow + j) = pack8(dg);
-            *reinterpret_cast<uint4*>(drow + p.h + j) = pack8(du);
+            park_bf16(0, b, g, cvt_bf2(dg[0], dg[1]), cvt_bf2(dg[2], dg[3]));
+            park_bf16(NSP, b, g, cvt_bf2(du[0], du[1]), cvt_bf2(du[2], du[3]));
           }
         }
+        drain(0, RB, 2, [&](int rr, int tc, uint4 v) {
+          const int64_t row = row0 + rbase + rr;
+          const int j = n0 + tc;
+          if (row < row_end && j < p.N) *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p.C) + row * (int64_t)(2 * p.h) + j) = v;
+        });
+        drain(NSP, RB, 2, [&](int rr, int tc, uint4 v) {
+          const int64_t row = row0 + rbase + rr;
+          const int j = n0 + tc;
+          if (row < row_end && j < p.N)
+            *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p.C) + row * (int64_t)(2 * p.h) + p.h + j) = v;
+        });
       }
-      lds_barrier();  // the band is reused by the next pass / the ring by the next tile
     }
   }
 }
@@ -892,7 +1007,8 @@ int hmoe_gate_up_dgrad(const void* dgu, const void* wgu, int64_t E, int64_t d, i
   p.N = (int)d;
   p.C = dxs;
   p.ldc = d;
-  p.c_f32 = dxs_dtype == HMOE_DT_F32;
+  if (dxs_dtype == HMOE_DT_F32)
+    return launch_mgroup<MGROUP, false, false, EPI_STORE_F32>(p, d, reinterpret_cast<hipStream_t>(stream));
   return launch_mgroup<MGROUP, false, false, EPI_STORE>(p, d, reinterpret_cast<hipStream_t>(stream));
 }
 

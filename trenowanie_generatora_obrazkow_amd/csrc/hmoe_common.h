@@ -26,6 +26,16 @@ __device__ __forceinline__ uint32_t f2bf(float f) {
 }
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
 
+// Two floats -> packed bf16 pair with the gfx950 conversion instruction (v_cvt_pk_bf16_f32, round to nearest even).
+// Identical to pack_bf2 for every non-NaN input; a NaN becomes a quiet NaN that keeps its sign (pack_bf2 gives
+// 0x7fc0).
+typedef __bf16 bf16x2_hw __attribute__((ext_vector_type(2)));
+typedef float f32x2_hw __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t cvt_bf2(float lo, float hi) {
+  const f32x2_hw v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_hw));
+}
+
 // exp for x <= 0 by Cody-Waite reduction (Cephes split of ln 2) + degree-7 Taylor polynomial (Horner, fma) +
 // exponent scaling.  Bit-identical to the host restatement used by the tests: every step is an explicitly rounded
 // IEEE operation.  Arguments below -87 return 0 (results above that are normal floats).
