@@ -112,6 +112,11 @@ struct KTile {
         buf2lds(k0 + chunk[i] * 8 < K ? voff[i] : kOOB, rsrc, soff, lds_tile + (wave * PER_WAVE + i) * 1024);
     }
   }
+  // the i-th of issue()'s copies alone (the caller spreads them between MFMAs)
+  __device__ __forceinline__ void issue_one(char* lds_tile, int wave, int i, int k0) const {
+    const uint32_t vo = (k0 + kBK <= K || k0 + chunk[i] * 8 < K) ? voff[i] : kOOB;
+    buf2lds(vo, rsrc, (uint32_t)k0 * 2u, lds_tile + (wave * PER_WAVE + i) * 1024);
+  }
   // Lane part of a fragment read address: row w32*32 + lane%32, k-chunk lane/32 (ks = 0), swizzled.  The
   // swizzle of row grp64 + w32*32 + lane%32 is that of lane%32, and chunk 2 + c stored at (2 + c) ^ s = (c ^ s) ^ 2,
   // so the 64-row group and ks parts are compile-time offsets.
@@ -148,6 +153,10 @@ struct MNTile {
       for (int i = 0; i < PER_WAVE; ++i)
         buf2lds(k0 + krow[i] < Kvalid ? voff[i] : kOOB, rsrc, soff, lds_tile + (wave * PER_WAVE + i) * 1024);
     }
+  }
+  __device__ __forceinline__ void issue_one(char* lds_tile, int wave, int i, int k0) const {
+    const uint32_t vo = (k0 + kBK <= Kvalid || k0 + krow[i] < Kvalid) ? voff[i] : kOOB;
+    buf2lds(vo, rsrc, (uint32_t)k0 * kstep, lds_tile + (wave * PER_WAVE + i) * 1024);
   }
   // lane l of instruction (wave w, i): k-row (w*PER_WAVE + i)*KPI + l / CPR, physical chunk l % CPR
   __device__ __forceinline__ static void slot(int wave, int lane, int i, int& k, int& col) {
@@ -567,12 +576,54 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
       else
         wait_vm<0>();
       lds_barrier();
-      if (kt + kNStage < nk) issue(kt + kNStage);  // into the slot of slice kt (fill == cons here)
+      if constexpr (MODE == KGROUP) {  // (measured: weight gradients run faster with the copies issued together)
+        if (kt + kNStage < nk) issue(kt + kNStage);  // into the slot of slice kt (fill == cons here)
+        cons += C::STAGE_BYTES;
+        if (cons == ring_end) cons = smem;
+        f0 = read(cons, 0);
+        mfmas(f1);
+        interleave();
+        continue;
+      }
+      // Second half: MFMAs on the ks1 fragments, the next slice's ks0 fragment reads and the refill of slice kt's
+      // slot with slice kt+4 (fill == cons here), one step per MFMA so the reads and copies issue in its shadow.
+      const bool refill = kt + kNStage < nk;
+      const int kr = (kt + kNStage) * kBK;
+      char* const dst = fill;
       cons += C::STAGE_BYTES;
       if (cons == ring_end) cons = smem;
-      f0 = read(cons, 0);
-      mfmas(f1);
-      interleave();
+      if (refill) {
+        fill += C::STAGE_BYTES;
+        if (fill == ring_end) fill = smem;
+      }
+#pragma unroll
+      for (int a = 0; a < C::FM; ++a)
+#pragma unroll
+        for (int b = 0; b < C::FN; ++b) {
+          const int i = a * C::FN + b;
+          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f1.wb[b], f1.xa[a], acc[a][b], 0, 0, 0);
+          if (i < C::FM)
+            f0.xa[i] = TA::frag(cons, i * C::FSM, loff_a, 0);
+          else if (i < C::FM + C::FN)
+            f0.wb[i - C::FM] = TB::frag(cons + C::A_BYTES, (i - C::FM) * C::FSN, loff_b, 0);
+          if ((i & 1) && refill) {
+            const int l = i >> 1;  // copy number: A's first, then B's
+            if (l < TA::PER_WAVE)
+              ta.issue_one(dst, wave, l, kr);
+            else if (l < LOADS)
+              tb.issue_one(dst + C::A_BYTES, wave, l - TA::PER_WAVE, kr);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      // copies left over when there are fewer MFMA pairs than copies (small tiles)
+#pragma unroll
+      for (int l = C::FM * C::FN / 2; l < LOADS; ++l) {
+        if (!refill) break;
+        if (l < TA::PER_WAVE)
+          ta.issue_one(dst, wave, l, kr);
+        else
+          tb.issue_one(dst + C::A_BYTES, wave, l - TA::PER_WAVE, kr);
+      }
     }
     lds_barrier();  // every wave is done with the ring before the next tile refills it
     // The epilogue's pin_agpr() hides the last MFMA write from the compiler's hazard tracking, so the wait states a
