@@ -91,10 +91,11 @@ int hmoe_make_schedule(const void* counts, int counts_dtype, int E, int64_t M, i
 
 /* grouped_mm: replaces aurora/moe_triton.py:65-90 (_grouped_kernel :22-56).
  * y[y_idx[r] or r, :] = bf16((a[a_idx[r] or r, :] @ w[e(r)]) * w_scale[e, :] * scale[r]) for the M sorted rows r,
- * e(r) the expert owning row r under counts.  a bf16 (rows of lda elements), w (E, K, N) bf16 with element
- * strides (stride_we, stride_wk, 1), scale (M,) bf16 or fp32 or NULL, w_scale: must be NULL (int8 weights are not
- * supported yet: HMOE_ERR_DTYPE), y bf16 with row stride ldy.  K % 8 == 0, N % 8 == 0, lda/ldy/stride_wk % 8 == 0.
- * Rows of y not named by the schedule are not written. */
+ * e(r) the expert owning row r under counts, the two scale products in that order on the fp32 sum.  a bf16 (rows of
+ * lda elements), w (E, K, N) with element strides (stride_we, stride_wk, 1): bf16 (w_scale NULL) or int8
+ * (HMOE_DT_I8, weight-only quantisation of aurora/moe_triton.py:44-51: w_scale (E, N) bf16 or fp32 required, N,
+ * stride_wk and stride_we multiples of 16); scale (M,) bf16 or fp32 or NULL; y bf16 with row stride ldy.
+ * K % 8 == 0, N % 8 == 0, lda/ldy/stride_wk % 8 == 0.  Rows of y not named by the schedule are not written. */
 int hmoe_grouped_mm(const void* a, int64_t lda, int a_dtype, const void* w, int w_dtype, int64_t E, int64_t K,
                     int64_t N, int64_t stride_we, int64_t stride_wk, const void* counts, int counts_dtype, int64_t M,
                     const int32_t* a_idx, const int32_t* y_idx, const void* scale, int scale_dtype,
@@ -115,6 +116,19 @@ int hmoe_gate_up_swiglu(const void* x, int64_t ldx, const int32_t* a_idx, const 
 int hmoe_down_scatter(const void* act, const void* wd, int64_t E, int64_t h, int64_t d, const void* counts,
                       int counts_dtype, int64_t M, const uint16_t* w_sorted, const int32_t* y_idx, void* y,
                       void* yhat, hmoe_stream_t stream);
+
+/* int8-weight forms of the two fused projections: replace aurora/hf_compat.py:79-80 on a layer fused with
+ * quant="int8" (weights and scales from aurora/hf_compat.py:106-110, the kernel's int8 branch at
+ * aurora/moe_triton.py:44-51).  wgu_q (E, d, 2h) int8 with scales wgu_s (E, 2h); wd_q (E, h, d) int8 with scales
+ * wd_s (E, d); scales bf16 or fp32 (*_s_dtype).  Same outputs as hmoe_gate_up_swiglu / hmoe_down_scatter with the
+ * per-column scale applied to the fp32 sum before any other step (inference only: no gu / yhat).  h % 16 == 0 and
+ * d % 16 == 0. */
+int hmoe_gate_up_swiglu_i8(const void* x, int64_t ldx, const int32_t* a_idx, const void* wgu_q, const void* wgu_s,
+                           int wgu_s_dtype, int64_t E, int64_t d, int64_t h, const void* counts, int counts_dtype,
+                           int64_t M, void* act, hmoe_stream_t stream);
+int hmoe_down_scatter_i8(const void* act, const void* wd_q, const void* wd_s, int wd_s_dtype, int64_t E, int64_t h,
+                         int64_t d, const void* counts, int counts_dtype, int64_t M, const uint16_t* w_sorted,
+                         const int32_t* y_idx, void* y, hmoe_stream_t stream);
 
 /* Combine: replaces aurora/hf_compat.py:82 (y.view(n, k, -1).sum(1)): out[t] = bf16(sum_j fp32(y[t*k + j])). */
 int hmoe_combine(const void* y, int64_t T, int k, int64_t d, void* out, hmoe_stream_t stream);

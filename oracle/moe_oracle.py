@@ -14,8 +14,11 @@ Pinning (what each function is checked against, in tests/test_oracle.py):
                              invariants (permutation, sortedness, stability)
   make_schedule              numpy restatement vs the C block-by-block restatement vs brute-force coverage
   grouped_mm                 per-expert float64 matmul of the reference's _self_test construction
-                             (aurora/hf_compat.py:112-121) and torch._grouped_mm on CPU; bf16 rounding bracket
-  moe_forward                per-token loop (pure Python) on tiny shapes; rounding points of the Triton path
+                             (aurora/hf_compat.py:112-121) and torch._grouped_mm on CPU; bf16 rounding bracket;
+                             int8 w_scale: equals the product with the dequantised (float64) weights, and a column
+                             permutation of (w, w_scale) permutes the output columns
+  moe_forward                per-token loop (pure Python) on tiny shapes; rounding points of the Triton path;
+                             int8 scales: equals the forward with dequantised float64 weights
   moe_backward               torch float64 autograd of the forward and central finite differences on tiny shapes
   router_backward            torch float64 autograd of softmax -> gather -> renormalise
   quant_int8                 closed form: |q| <= 127, dequantised error <= scale / 2
@@ -248,11 +251,12 @@ def quant_int8(w):
 # ----------------------------------------------------------------------------------------------------------------
 # layer forward: the Triton path of aurora/hf_compat.py:75-82
 # ----------------------------------------------------------------------------------------------------------------
-def moe_forward(x, ids, topk_w, wgu, wd, tokens=None):
+def moe_forward(x, ids, topk_w, wgu, wd, tokens=None, wgu_s=None, wd_s=None):
     """x (T, d) bf16 values (float32 array), ids (T, k), topk_w (T, k) fp32, wgu (E, d, 2h), wd (E, h, d).
     Returns dict with out (T, d) and the per-flat-row intermediates (gb, ub, act, yhat, y) in flat order
     f = t*k + j.  tokens: optional subset of token indices (then only those tokens' rows are computed; arrays are
-    indexed by position in `tokens`)."""
+    indexed by position in `tokens`).  wgu_s (E, 2h) / wd_s (E, d): int8 weights' per-column scales, applied to
+    the sums before any rounding (aurora/moe_triton.py:48-51 on a layer fused with quant="int8")."""
     T, k = ids.shape
     E = wgu.shape[0]
     h = wgu.shape[2] // 2
@@ -272,10 +276,14 @@ def moe_forward(x, ids, topk_w, wgu, wd, tokens=None):
         if sel.size == 0:
             continue
         gu = x[rows_t[sel]].astype(np.float64) @ wgu[e].astype(np.float64)
+        if wgu_s is not None:
+            gu = gu * np.asarray(wgu_s[e], dtype=np.float64)[None, :]
         gb[sel] = round_bf16(gu[:, :h])
         ub[sel] = round_bf16(gu[:, h:])
         act[sel] = swiglu_fwd(gb[sel], ub[sel])
         yh = act[sel].astype(np.float64) @ wd[e].astype(np.float64)
+        if wd_s is not None:
+            yh = yh * np.asarray(wd_s[e], dtype=np.float64)[None, :]
         yhat[sel] = yh
         y[sel] = round_bf16(yh * wb[sel].astype(np.float64)[:, None])
     out = round_bf16(y.reshape(n, k, d).astype(np.float64).sum(1))

@@ -81,6 +81,20 @@ def test_argument_validation_codes(lib):
                              None) == 0  # M == 0: nothing to do
     assert L.hmoe_grouped_mm(P, 64, 0, P, 0, 3, 64, 32, 64 * 32, 32, None, 4, 48, None, None, None, 0, None, 0, P,
                              32, None) == -1
+    # int8 weights: scales required, N % 16, scale dtype
+    assert L.hmoe_grouped_mm(P, 64, 0, P, 5, 3, 64, 32, 64 * 32, 32, P, 4, 48, None, None, None, 0, None, 0, P, 32,
+                             None) == -1
+    assert L.hmoe_grouped_mm(P, 64, 0, P, 5, 3, 64, 40, 64 * 48, 48, P, 4, 48, None, None, None, 0, P, 0, P, 40,
+                             None) == -2
+    assert L.hmoe_grouped_mm(P, 64, 0, P, 5, 3, 64, 32, 64 * 32, 32, P, 4, 48, None, None, None, 0, P, 3, P, 32,
+                             None) == -3
+    assert L.hmoe_gate_up_swiglu_i8(P, 64, None, P, P, 0, 3, 64, 24, P, 4, 48, P, None) == -2  # h % 16
+    assert L.hmoe_gate_up_swiglu_i8(P, 64, None, P, P, 0, 3, 64, 32, P, 4, 0, P, None) == 0
+    assert L.hmoe_gate_up_swiglu_i8(P, 64, None, None, P, 0, 3, 64, 32, P, 4, 48, P, None) == -1
+    assert L.hmoe_down_scatter_i8(P, P, P, 4, 3, 32, 64, P, 4, 48, P, P, P, None) == -3  # scale dtype
+    assert L.hmoe_down_scatter_i8(P, P, P, 0, 3, 32, 72, P, 4, 48, P, P, P, None) == -2  # d % 16
+    # direct-load offsets beyond 2^31 bytes
+    assert L.hmoe_gate_up_swiglu(P, 4096, P, P, 3, 4096, 65536, P, 4, 1 << 20, P, None, None) == -2
     # wgrad: output dtype, shapes
     assert L.hmoe_grouped_wgrad(P, 64, P, 64, 3, 64, 64, P, 4, 48, P, 3, None) == -3
     assert L.hmoe_grouped_wgrad(P, 64, P, 64, 3, 60, 64, P, 4, 48, P, 2, None) == -2

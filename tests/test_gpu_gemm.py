@@ -29,7 +29,8 @@ def test_self_test_shape(oracle, tile):
     y = moe_triton.grouped_mm(a.cuda(), w.cuda(), counts.cuda())
     ref = oracle.grouped_mm(f32(a), f32(w), counts.numpy())
     assert_close_bf16(f32(y), ref, "self-test shape")
-    assert _self_test(lambda a_, w_, c_: moe_triton.grouped_mm(a_, w_, c_), torch.device("cuda"), torch.bfloat16)
+    assert _self_test(lambda a_, w_, s_, c_: moe_triton.grouped_mm(a_, w_, c_, w_scale=s_), torch.device("cuda"),
+                      torch.bfloat16)
 
 
 @pytest.mark.parametrize("T,K,N,E,k,skew", [(1024, 256, 512, 8, 2, 0), (700, 520, 264, 5, 2, 1),

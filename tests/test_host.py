@@ -35,8 +35,12 @@ def test_facade_rejects_cpu_and_unsupported():
         moe_triton.grouped_mm(a, w, counts)
     with pytest.raises(AssertionError):
         moe_triton.grouped_mm(a, w.transpose(1, 2).contiguous().transpose(1, 2), counts)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError):  # bf16 weights take no scale, int8 weights need one
         moe_triton.grouped_mm(a, w, counts, w_scale=torch.ones(3, 32))
+    with pytest.raises(ValueError):
+        moe_triton.grouped_mm(a, w.to(torch.int8), counts)
+    with pytest.raises(RuntimeError, match="GPU"):
+        moe_triton.grouped_mm(a, w.to(torch.int8), counts, w_scale=torch.ones(3, 32, dtype=torch.bfloat16))
     with pytest.raises(TypeError):
         moe_triton.grouped_mm(a.float(), w.float(), counts)
     with pytest.raises(RuntimeError, match="GPU"):
@@ -79,8 +83,26 @@ def test_fuse_moe_stacks_reference_layout():
         assert b.experts == list(range(E))
         with pytest.raises(RuntimeError, match="GPU"):
             b.moe_infer(torch.randn(4, d), torch.zeros(4, 2, dtype=torch.long), torch.ones(4, 2))
-    with pytest.raises(NotImplementedError):
-        hf_compat.fuse_moe(nn.Sequential(_Block(d, h, E)), quant="int8")
+
+
+def test_fuse_moe_int8_buffers():
+    """quant="int8" (aurora/hf_compat.py:159-162): int8 stacked weights with (E, out) bf16 scales that dequantise
+    to within half a step of the stacked bf16 weights."""
+    torch.manual_seed(1)
+    d, h, E = 32, 24, 5
+    blk = _Block(d, h, E)
+    wgu = torch.stack([torch.cat([e.gate_proj.weight, e.up_proj.weight]).t() for e in blk.experts]).detach()
+    wd = torch.stack([e.down_proj.weight.t() for e in blk.experts]).detach()
+    assert hf_compat.fuse_moe(nn.Sequential(blk), quant="int8") == 1
+    assert blk._wgu.dtype == torch.int8 and blk._wgu.shape == (E, d, 2 * h)
+    assert blk._wd.dtype == torch.int8 and blk._wd.shape == (E, h, d)
+    assert blk._wgu_s.shape == (E, 2 * h) and blk._wd_s.shape == (E, d) and blk._wgu_s.dtype == torch.bfloat16
+    for q, s, w in ((blk._wgu, blk._wgu_s, wgu), (blk._wd, blk._wd_s, wd)):
+        deq = hf_compat._dequant(q, s, torch.float32)
+        # half a step from rounding q, plus 127 x the bf16 rounding of the scale (<= 2^-8 relative)
+        assert ((deq - w).abs() <= s.float().unsqueeze(1) * (0.5 + 127 * 2.0 ** -8) * 1.01).all()
+    with pytest.raises(RuntimeError, match="GPU"):
+        blk.moe_infer(torch.randn(4, d), torch.zeros(4, 2, dtype=torch.long), torch.ones(4, 2))
 
 
 def test_quant_int8_matches_reference_rule():

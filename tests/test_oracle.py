@@ -212,6 +212,28 @@ def test_quant_int8_closed_form(oracle):
     assert (np.abs(q).max(axis=1) == 127).all()
 
 
+def test_grouped_mm_int8_scale_is_dequantised_product(oracle):
+    """(a @ q) * s[e, n] equals a @ (q * s) column by column (exact in float64 up to rounding); permuting the columns
+    of (q, s) together permutes y's columns -- a transposed or mis-indexed scale fails both."""
+    rng = np.random.default_rng(11)
+    T, K, N, E, k = 40, 48, 32, 3, 2
+    x = oracle.round_bf16(rng.standard_normal((T, K)))
+    w = rng.standard_normal((E, K, N)).astype(np.float32) * np.linspace(0.1, 3.0, N, dtype=np.float32)
+    q, s = oracle.quant_int8(w)
+    ids = rng.integers(0, E, (T, k))
+    d = oracle.dispatch(ids, E)
+    sc = rng.random(T * k).astype(np.float32)
+    kw = dict(a_idx=d["a_idx"], y_idx=d["y_idx"], scale=sc, round_out=False)
+    y = oracle.grouped_mm(x, q, d["counts"], w_scale=s, **kw)
+    deq = q.astype(np.float64) * s.astype(np.float64)[:, None, :]
+    np.testing.assert_allclose(y, oracle.grouped_mm(x, deq, d["counts"], **kw), rtol=1e-12, atol=1e-12)
+    perm = rng.permutation(N)
+    yp = oracle.grouped_mm(x, q[:, :, perm], d["counts"], w_scale=s[:, perm], **kw)
+    np.testing.assert_array_equal(yp, y[:, perm])
+    # the dequantised weights stay within half a step (q rounding) plus 127 x the bf16 rounding of the scale
+    assert (np.abs(deq - w) <= s.astype(np.float64)[:, None, :] * (0.5 + 127 * 2.0 ** -8) * 1.01).all()
+
+
 # ------------------------------------------------------------------------------------------------- layer forward
 def test_moe_forward_vs_token_loop(oracle):
     """The per-expert batched oracle against a per-token loop with the same rounding points (tiny shapes)."""
@@ -237,6 +259,23 @@ def test_moe_forward_vs_token_loop(oracle):
             wb = float(R(np.array([tw[t, j]]))[0])
             acc += R(np.array(yh) * wb).astype(np.float64)
         np.testing.assert_array_equal(f["out"][t], R(acc))
+
+
+def test_moe_forward_int8_scales(oracle):
+    """Scales applied to the sums (the int8 form) give what the dequantised float64 weights give at every rounding
+    point; the scales of the gate and up halves are indexed by the wgu column (2h), those of down by d."""
+    rng = np.random.default_rng(12)
+    T, d, E, k, h = 24, 32, 4, 2, 16
+    x = oracle.round_bf16(rng.standard_normal((T, d)))
+    colw = np.linspace(0.2, 2.0, 2 * h, dtype=np.float32)
+    qgu, sgu = oracle.quant_int8(rng.standard_normal((E, d, 2 * h)).astype(np.float32) * colw * 0.3)
+    qd, sd = oracle.quant_int8(rng.standard_normal((E, h, d)).astype(np.float32) * 0.3)
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)])
+    tw = rng.random((T, k)).astype(np.float32)
+    f = oracle.moe_forward(x, ids, tw, qgu, qd, wgu_s=sgu, wd_s=sd)
+    g = oracle.moe_forward(x, ids, tw, qgu * sgu.astype(np.float64)[:, None, :], qd * sd.astype(np.float64)[:, None, :])
+    for key in ("gb", "ub", "act", "y", "out"):
+        np.testing.assert_array_equal(f[key], g[key], err_msg=key)
 
 
 def test_moe_forward_vs_reference_cpu_path(oracle):

@@ -35,6 +35,8 @@ SIGNATURES = {
                                _I32, _P, _I32, _P, _I64, _P]),
     "hmoe_gate_up_swiglu": (_I32, [_P, _I64, _P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P]),
     "hmoe_down_scatter": (_I32, [_P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P, _P, _P]),
+    "hmoe_gate_up_swiglu_i8": (_I32, [_P, _I64, _P, _P, _P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _P, _P]),
+    "hmoe_down_scatter_i8": (_I32, [_P, _P, _P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P, _P]),
     "hmoe_combine": (_I32, [_P, _I64, _I32, _I64, _P, _P]),
     "hmoe_combine_bwd": (_I32, [_P, _P, _P, _P, _P, _I64, _I32, _I64, _P, _P, _P]),
     "hmoe_down_dgrad_swiglu": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P]),

@@ -30,16 +30,17 @@ constexpr int kMaxEGemm = 1024;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-template <int BM_, int BN_, int WM_, int WN_, int GM_>
+template <int BM_, int BN_, int WM_, int WN_, int GM_, int BE_ = 2>
 struct Cfg {
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, GM = GM_;
+  static constexpr int BE = BE_;  // bytes per B element: 2 (bf16) or 1 (int8 weights)
   static constexpr int NWAVES = WM * WN, NT = NWAVES * 64;
   static constexpr int TM = BM / WM, TN = BN / WN;
   static constexpr int FM = TM / 32, FN = TN / 32;
   // a wave's fragments are interleaved with the other waves' along each dimension: fragment f of wave w covers
   // 32 rows / columns from f * FS + 32 w (FS = 32 * waves along that dimension)
   static constexpr int FSM = 32 * WM, FSN = 32 * WN;
-  static constexpr int A_BYTES = BM * kBK * 2, B_BYTES = BN * kBK * 2;  // per slice
+  static constexpr int A_BYTES = BM * kBK * 2, B_BYTES = BN * kBK * BE;  // per slice
   static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
   static constexpr int LDS_BYTES = kNStage * STAGE_BYTES;
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be a multiple of 32");
@@ -188,15 +189,78 @@ struct MNTile {
   }
 };
 
-template <bool MN, int ROWS, int NWAVES>
+// int8 MN-major operand (weights (K, N), N contiguous, as int8): 32 k-rows x ROWS columns = ROWS bytes per k-row.
+// Each 16-byte chunk holds 16 columns.  Logical chunk c = 4b + 2wn + h of a k-row (fragment b of wave column wn,
+// half h of its 32 columns) is stored at b + FN*((2wn + h) ^ (k & 3)), so the k-rows a transpose read touches spread
+// over the banks while fragment b stays a compile-time offset.
+template <int ROWS, int NWAVES, int FN>
+struct MNTile8 {
+  static constexpr int INSTR = ROWS * kBK / 1024;
+  static constexpr int PER_WAVE = INSTR / NWAVES;
+  static constexpr int CPR = ROWS / 16;  // 16-byte chunks per k-row
+  static constexpr int KPI = 64 / CPR;   // k-rows per copy instruction
+  static_assert(INSTR % NWAVES == 0 && CPR == 4 * FN, "int8 tile: 4 chunks per fragment column group");
+  uint32_t voff[PER_WAVE];  // byte offset of (k-row, first of the lane's 16 columns) from the base, or kOOB
+  int krow[PER_WAVE];
+  i32x4 rsrc;
+  uint32_t kstep;  // bytes per k-row (ld)
+  int Kvalid;
+  __device__ __forceinline__ void issue(char* lds_tile, int wave, int lane, int k0) const {
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) issue_one(lds_tile, wave, i, k0);
+  }
+  __device__ __forceinline__ void issue_one(char* lds_tile, int wave, int i, int k0) const {
+    const uint32_t vo = (k0 + kBK <= Kvalid || k0 + krow[i] < Kvalid) ? voff[i] : kOOB;
+    buf2lds(vo, rsrc, (uint32_t)k0 * kstep, lds_tile + (wave * PER_WAVE + i) * 1024);
+  }
+  // lane l of instruction (wave w, i): k-row (w*PER_WAVE + i)*KPI + l / CPR, physical chunk l % CPR; col = the first
+  // logical column the slot holds
+  __device__ __forceinline__ static void slot(int wave, int lane, int i, int& k, int& col) {
+    k = (wave * PER_WAVE + i) * KPI + lane / CPR;
+    const int pp = lane % CPR, b = pp % FN, q = (pp / FN) ^ (k & 3);
+    col = (4 * b + q) * 16;
+  }
+  // Transpose read (ds_read_b64_tr_b8): lane l = 16G + 8h + c receives byte c of the 8 lanes 16G + h + 2m, m = 0..7.
+  // Lane S therefore points at k-row (S/32)*8 + (S%16)/2 and column 16*((S/16)%2) + 8*(S%2) of the fragment, so
+  // lane l ends with column l%32 and the 8 consecutive k (l/32)*8 + 0..7 of it.
+  __device__ __forceinline__ static int lane_off(int w32, int lane) {
+    const int kr = (lane >> 5) * 8 + ((lane & 15) >> 1);
+    const int h = (lane >> 4) & 1;
+    return kr * ROWS + 16 * FN * ((2 * w32 + h) ^ (kr & 3)) + 8 * (lane & 1);
+  }
+  // fragment b (columns b*FSN + 32 w32 + 0..31) x 16 k (ks*16 + ...), converted exactly to bf16
+  __device__ __forceinline__ static bf16x8 frag(const char* lds_tile, int grp64, int loff, int ks) {
+    typedef int i32x2 __attribute__((ext_vector_type(2)));
+    typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
+    const int b = grp64 / 64;
+    const i32x2 v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(lds_tile + loff + ks * 16 * ROWS + 16 * b));
+    // signed bytes -> exact floats (|q| <= 127 has at most 7 significant bits) -> bf16
+    const uint32_t lo = (uint32_t)v[0] ^ 0x80808080u, hi = (uint32_t)v[1] ^ 0x80808080u;
+    float f[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      f[j] = (float)((lo >> (8 * j)) & 0xffu) - 128.0f;
+      f[4 + j] = (float)((hi >> (8 * j)) & 0xffu) - 128.0f;
+    }
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 w = {cvt_bf2(f[0], f[1]), cvt_bf2(f[2], f[3]), cvt_bf2(f[4], f[5]), cvt_bf2(f[6], f[7])};
+    return __builtin_bit_cast(bf16x8, w);
+  }
+};
+
+template <bool MN, int ROWS, int NWAVES, int ES = 2, int FN = 4>
 struct TileSel;
-template <int ROWS, int NWAVES>
-struct TileSel<false, ROWS, NWAVES> {
+template <int ROWS, int NWAVES, int FN>
+struct TileSel<false, ROWS, NWAVES, 2, FN> {
   using type = KTile<ROWS, NWAVES>;
 };
-template <int ROWS, int NWAVES>
-struct TileSel<true, ROWS, NWAVES> {
+template <int ROWS, int NWAVES, int FN>
+struct TileSel<true, ROWS, NWAVES, 2, FN> {
   using type = MNTile<ROWS, NWAVES>;
+};
+template <int ROWS, int NWAVES, int FN>
+struct TileSel<true, ROWS, NWAVES, 1, FN> {
+  using type = MNTile8<ROWS, NWAVES, FN>;
 };
 
 // Workgroup barrier that orders LDS only.  __syncthreads() is a workgroup release/acquire fence over all address
@@ -236,7 +300,7 @@ struct GemmParams {
   const int32_t* a_idx;
   // N side (B).  MGROUP: weights of expert e at B + e*strideBe; B_MN: element (k, n) at k*ldb + n, else n*ldb + k.
   //              KGROUP: Y (M, N) with N contiguous, row stride ldb.
-  const uint16_t* B;
+  const void* B;             // bf16, or int8 weights (with w_scale)
   int64_t ldb, strideBe;
   // groups
   const void* counts;
@@ -256,6 +320,9 @@ struct GemmParams {
   int scale_f32;
   uint16_t* aux;            // EPI_STORE: yhat (unscaled, sorted); EPI_SWIGLU: gu store
   const uint16_t* gu_in;    // EPI_SWIGLU_BWD: [g | u]
+  const void* w_scale;      // int8 weights: per-(expert, column) scale (E, ldws), bf16 or fp32
+  int w_scale_f32;
+  int64_t ldws;             // scale row length (columns of the weight)
 };
 
 // ----------------------------------------------------------------------------------------------------------------
@@ -271,6 +338,8 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
   // (2 KB each: 256 rows plus up to 3 leading rows, since the copy starts at the 16-byte boundary below row0)
   __shared__ __attribute__((aligned(16))) int s_rowy[2][512];
   __shared__ __attribute__((aligned(16))) float s_rowsc[2][512];
+  // int8 weights: the tile's per-column weight scales (bf16 or fp32), by tile parity like the row data
+  __shared__ __attribute__((aligned(16))) float s_colsc[2][256];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -333,7 +402,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
   const int total = total_m * nb_n;
 
   typename TileSel<A_MN, C::BM, C::NWAVES>::type ta;
-  typename TileSel<B_MN, C::BN, C::NWAVES>::type tb;
+  typename TileSel<B_MN, C::BN, C::NWAVES, C::BE, C::FN>::type tb;
   static_assert(C::FSM == 64 && C::FSN == 64, "fragment reads assume two waves along each tile dimension");
   const int loff_a = decltype(ta)::lane_off(wm, lane);
   const int loff_b = decltype(tb)::lane_off(wn, lane);
@@ -402,7 +471,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
         ta.voff[i] = vo;
         ta.chunk[i] = c;
       }
-      tb.rsrc = make_rsrc(p.B + (int64_t)e * p.strideBe);
+      tb.rsrc = make_rsrc(static_cast<const char*>(p.B) + (int64_t)e * p.strideBe * C::BE);
       auto gcol = [&](int nn, int& col) -> bool {  // tile column -> weight column
         if (EPI == EPI_SWIGLU) {
           const int half = nn / (C::BN / 2);  // tile columns [0, BN/2) gate, [BN/2, BN) the matching up
@@ -415,16 +484,17 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
         }
       };
       if constexpr (B_MN) {
-        tb.kstep = (uint32_t)(p.ldb * 2);
+        tb.kstep = (uint32_t)(p.ldb * C::BE);
         tb.Kvalid = p.K;
 #pragma unroll
         for (int i = 0; i < tb.PER_WAVE; ++i) {
           int k, nn, col;
           tb.slot(wave, lane, i, k, nn);
           tb.krow[i] = k;
-          tb.voff[i] = gcol(nn, col) ? (uint32_t)(((int64_t)k * p.ldb + col) * 2) : kOOB;
+          tb.voff[i] = gcol(nn, col) ? (uint32_t)(((int64_t)k * p.ldb + col) * C::BE) : kOOB;
         }
       } else {
+        static_assert(C::BE == 2, "int8 weights are read N-contiguous only");
         tb.K = p.K;
 #pragma unroll
         for (int i = 0; i < tb.PER_WAVE; ++i) {
@@ -440,7 +510,8 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
       ta.rsrc = make_rsrc(p.A + kstart * p.lda + i0);
       ta.kstep = (uint32_t)(p.lda * 2);
       ta.Kvalid = kvalid;
-      tb.rsrc = make_rsrc(p.B + kstart * p.ldb + n0);
+      static_assert(C::BE == 2, "weight gradients take bf16 operands");
+      tb.rsrc = make_rsrc(static_cast<const uint16_t*>(p.B) + kstart * p.ldb + n0);
       tb.kstep = (uint32_t)(p.ldb * 2);
       tb.Kvalid = kvalid;
 #pragma unroll
@@ -484,6 +555,28 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
       if (EPI != EPI_SWIGLU_BWD && p.y_idx) y_sh = copy_rows(p.y_idx, 4, reinterpret_cast<char*>(s_rowy[par]));
       if (p.scale) sc_sh = copy_rows(p.scale, p.scale_f32 ? 4 : 2, reinterpret_cast<char*>(s_rowsc[par]));
     }
+    // int8 weights: the tile's column scales (w_scale[e][column], in tile-column order) by wave 1 (wave 0 with one
+    // wave), ahead of the first slice like the row data
+    if constexpr (C::BE == 1) {
+      if (wave == (C::NWAVES > 1 ? 1 : 0)) {
+        const int es = p.w_scale_f32 ? 4 : 2;
+        const int per = 16 / es;  // columns per 16-byte copy
+        i32x4 rs = make_rsrc(static_cast<const char*>(p.w_scale) + (int64_t)e * p.ldws * es);
+        rs.z = __builtin_amdgcn_readfirstlane((int)min(p.ldws * es, (int64_t)0x7FFFFFF0));
+        const int tc = lane * per;  // tile column of this lane's first scale
+        int col = 0;
+        bool ok = tc < C::BN;
+        if (EPI == EPI_SWIGLU) {
+          const int ac = n0 + tc % (C::BN / 2);
+          col = (tc / (C::BN / 2)) * p.h + ac;
+          ok = ok && ac < p.N;
+        } else {
+          col = n0 + tc;
+          ok = ok && col < p.N;
+        }
+        buf2lds(ok ? (uint32_t)(col * es) : kOOB, rs, 0u, reinterpret_cast<char*>(s_colsc[par]));
+      }
+    }
 
     // ---- main loop: NSTAGE-deep ring of k-slices ----
     f32x16 acc[C::FM][C::FN];
@@ -512,7 +605,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
     // The barrier comes after every wave has read all of slice kt, so its slot can be refilled at once: four
     // slices are in flight while one is consumed, and LDS read latency hides under the MFMAs.
     typedef typename TileSel<A_MN, C::BM, C::NWAVES>::type TA;
-    typedef typename TileSel<B_MN, C::BN, C::NWAVES>::type TB;
+    typedef typename TileSel<B_MN, C::BN, C::NWAVES, C::BE, C::FN>::type TB;
     constexpr int RD = C::FM * (A_MN ? 2 : 1) + C::FN * (B_MN ? 2 : 1);  // LDS reads per k16 step
     constexpr int NMF = C::FM * C::FN;                                     // MFMAs per k16 step
     constexpr int PAIRS = RD < NMF ? RD : NMF;
@@ -641,8 +734,26 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
     const int lrow = lane & 31;
     const int lcol = 4 * (lane >> 5);
     constexpr int CH = C::A_BYTES / C::NWAVES;  // bytes per ring part filled by one wave
-    static_assert(C::A_BYTES == C::B_BYTES && CH >= 1024 && 4096 % CH == 0, "staging chunks");
-    auto chunk = [&](int q) -> char* { return smem + (q >> 1) * C::STAGE_BYTES + (q & 1) * C::A_BYTES + wave * CH; };
+    static_assert(CH >= 1024 && 4096 % CH == 0 && (C::BE == 1 || C::A_BYTES == C::B_BYTES), "staging chunks");
+    // chunk q: the A and B parts of each stage (bf16 weights), or the A parts only (int8 weights: smaller B parts)
+    auto chunk = [&](int q) -> char* {
+      if constexpr (C::BE == 1) return smem + q * C::STAGE_BYTES + wave * CH;
+      return smem + (q >> 1) * C::STAGE_BYTES + (q & 1) * C::A_BYTES + wave * CH;
+    };
+    // column scale of int8 weights for tile column tc (1 for bf16 weights)
+    [[maybe_unused]] auto col_scale4 = [&](int tc, float* ws) {
+      if constexpr (C::BE == 1) {
+        if (p.w_scale_f32) {
+          const float4 v = *reinterpret_cast<const float4*>(&s_colsc[par][tc]);
+          ws[0] = v.x; ws[1] = v.y; ws[2] = v.z; ws[3] = v.w;
+        } else {
+          const uint2 v = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(s_colsc[par]) + tc);
+          ws[0] = bf_lo(v.x); ws[1] = bf_hi(v.x); ws[2] = bf_lo(v.y); ws[3] = bf_hi(v.y);
+        }
+      } else {
+        ws[0] = ws[1] = ws[2] = ws[3] = 1.0f;
+      }
+    };
     // sub-plane sp, row r (0..31), byte offset within the 128-byte row; 16-byte chunks XOR-swizzled by r & 7
     auto sp_addr = [&](int sp, int r, int byte) -> char* {
       const int lin = r * 128;
@@ -710,7 +821,15 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
           for (int g = 0; g < 4; ++g) {
             const f32x16& v = acc[a][b];
             if (p.aux) park_bf16(NSP, b, g, cvt_bf2(v[4 * g], v[4 * g + 1]), cvt_bf2(v[4 * g + 2], v[4 * g + 3]));
-            const float v0 = v[4 * g] * sc, v1 = v[4 * g + 1] * sc, v2 = v[4 * g + 2] * sc, v3 = v[4 * g + 3] * sc;
+            float v0, v1, v2, v3;
+            if constexpr (C::BE == 1) {  // int8 weights: column scale first, then the row scale (two products)
+              float ws[4];
+              col_scale4(col_of(b, g), ws);
+              v0 = (v[4 * g] * ws[0]) * sc, v1 = (v[4 * g + 1] * ws[1]) * sc;
+              v2 = (v[4 * g + 2] * ws[2]) * sc, v3 = (v[4 * g + 3] * ws[3]) * sc;
+            } else {
+              v0 = v[4 * g] * sc, v1 = v[4 * g + 1] * sc, v2 = v[4 * g + 2] * sc, v3 = v[4 * g + 3] * sc;
+            }
             if constexpr (EPI == EPI_STORE_F32)
               park_f32(0, b, g, make_float4(v0, v1, v2, v3));
             else
@@ -744,8 +863,20 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
           for (int g = 0; g < 4; ++g) {
             const f32x16& gv = acc[a][b];
             const f32x16& uv = acc[a][b + C::FN / 2];
-            const uint32_t gb0 = cvt_bf2(gv[4 * g], gv[4 * g + 1]), gb1 = cvt_bf2(gv[4 * g + 2], gv[4 * g + 3]);
-            const uint32_t ub0 = cvt_bf2(uv[4 * g], uv[4 * g + 1]), ub1 = cvt_bf2(uv[4 * g + 2], uv[4 * g + 3]);
+            float gs[4] = {gv[4 * g], gv[4 * g + 1], gv[4 * g + 2], gv[4 * g + 3]};
+            float us[4] = {uv[4 * g], uv[4 * g + 1], uv[4 * g + 2], uv[4 * g + 3]};
+            if constexpr (C::BE == 1) {  // int8 weights: per-column scales of the gate and up columns
+              float wg[4], wu[4];
+              col_scale4(col_of(b, g), wg);
+              col_scale4(col_of(b + C::FN / 2, g), wu);
+#pragma unroll
+              for (int t = 0; t < 4; ++t) {
+                gs[t] *= wg[t];
+                us[t] *= wu[t];
+              }
+            }
+            const uint32_t gb0 = cvt_bf2(gs[0], gs[1]), gb1 = cvt_bf2(gs[2], gs[3]);
+            const uint32_t ub0 = cvt_bf2(us[0], us[1]), ub1 = cvt_bf2(us[2], us[3]);
             const float gg[4] = {bf_lo(gb0), bf_hi(gb0), bf_lo(gb1), bf_hi(gb1)};
             const float uu[4] = {bf_lo(ub0), bf_hi(ub0), bf_lo(ub1), bf_hi(ub1)};
             // act = bf16(bf16(silu(g)) * u) with g, u the bf16-rounded projections
@@ -873,6 +1004,8 @@ static int launch(const GemmParams& p, int64_t tiles_upper, hipStream_t s) {
 // with few tiles.
 using CfgL = Cfg<256, 256, 2, 2, 4>;
 using CfgS = Cfg<128, 128, 2, 2, 4>;
+using CfgL8 = Cfg<256, 256, 2, 2, 4, 1>;  // int8 weights (N-contiguous), bf16 activations
+using CfgS8 = Cfg<128, 128, 2, 2, 4, 1>;
 
 template <class C, int EPI>
 static inline int64_t mgroup_tiles(int64_t M, int64_t E, int64_t ncols) {
@@ -907,7 +1040,31 @@ static int launch_mgroup(const GemmParams& p, int64_t ncols, hipStream_t s) {
   return launch<CfgS, MODE, A_MN, B_MN, EPI>(p, mgroup_tiles<CfgS, EPI>(p.M, p.E, ncols), s);
 }
 
+// int8 weights: same tile choice, int8 tile configurations
+template <int EPI>
+static int launch_mgroup_i8(const GemmParams& p, int64_t ncols, hipStream_t s) {
+  const int64_t tl = mgroup_tiles<CfgL8, EPI>(p.M, p.E, ncols);
+  if (pick_large(tl)) return launch<CfgL8, MGROUP, false, true, EPI>(p, tl, s);
+  return launch<CfgS8, MGROUP, false, true, EPI>(p, mgroup_tiles<CfgS8, EPI>(p.M, p.E, ncols), s);
+}
+
 static inline bool al16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// The direct loads address an operand with a 32-bit byte offset from a per-tile (or per-expert) base: a span that
+// must stay below 2^31 bytes.
+static inline bool off32(int64_t bytes) { return bytes < ((int64_t)1 << 31); }
+
+// int8 weight arguments: (E, K, N) int8 with N contiguous (row stride ld), scales (E, N) bf16 or fp32 with 16-byte
+// aligned rows; every offset a tile reads must stay below 2^31 bytes from the expert's base.
+static int check_i8(const void* w, int64_t ld, int64_t K, int64_t N, int64_t stride_we, const void* w_scale,
+                    int w_scale_dtype) {
+  if (!w || !w_scale) return HMOE_ERR_ARG;
+  if (w_scale_dtype != HMOE_DT_BF16 && w_scale_dtype != HMOE_DT_F32) return HMOE_ERR_DTYPE;
+  if (ld % 16 || stride_we % 16 || !al16(w) || !al16(w_scale)) return HMOE_ERR_ARG;
+  if (N % 16) return HMOE_ERR_SHAPE;  // 16 int8 columns per direct-load chunk
+  if (K * ld >= (int64_t)1 << 31) return HMOE_ERR_SHAPE;
+  return HMOE_OK;
+}
 
 static GemmParams base_params(const void* counts, int counts_dtype, int64_t E, int64_t M) {
   GemmParams p = {};
@@ -935,22 +1092,26 @@ int hmoe_grouped_mm(const void* a, int64_t lda, int a_dtype, const void* w, int 
                     int64_t N, int64_t stride_we, int64_t stride_wk, const void* counts, int counts_dtype, int64_t M,
                     const int32_t* a_idx, const int32_t* y_idx, const void* scale, int scale_dtype,
                     const void* w_scale, int w_scale_dtype, void* y, int64_t ldy, hmoe_stream_t stream) {
-  (void)w_scale_dtype;
   int rc = check_common(counts, counts_dtype, E, M);
   if (rc) return rc;
   if (M == 0) return HMOE_OK;
   if (!a || !w || !y || K <= 0 || N <= 0) return HMOE_ERR_ARG;
-  if (a_dtype != HMOE_DT_BF16 || w_dtype != HMOE_DT_BF16) return HMOE_ERR_DTYPE;
-  if (w_scale) return HMOE_ERR_DTYPE;
+  if (a_dtype != HMOE_DT_BF16) return HMOE_ERR_DTYPE;
+  const bool i8 = w_dtype == HMOE_DT_I8;
+  if (!i8 && w_dtype != HMOE_DT_BF16) return HMOE_ERR_DTYPE;
+  if (i8 != (w_scale != nullptr)) return i8 ? HMOE_ERR_ARG : HMOE_ERR_DTYPE;  // int8 weights come with scales
   if (scale && scale_dtype != HMOE_DT_BF16 && scale_dtype != HMOE_DT_F32) return HMOE_ERR_DTYPE;
   if (K % 8 || N % 8 || lda % 8 || ldy % 8 || stride_wk % 8 || stride_we % 8) return HMOE_ERR_SHAPE;
   if (lda < K || ldy < N || stride_wk < N || !al16(a) || !al16(w) || !al16(y)) return HMOE_ERR_ARG;
   if (K > INT32_MAX || N > INT32_MAX || M > INT32_MAX) return HMOE_ERR_SHAPE;
+  // direct-load offsets are 32-bit: gathered rows (a_idx < M) and one expert's weights within 2 GiB
+  if ((a_idx && !off32(M * lda * 2)) || !off32(K * stride_wk * (i8 ? 1 : 2))) return HMOE_ERR_SHAPE;
+  if (i8 && (rc = check_i8(w, stride_wk, K, N, stride_we, w_scale, w_scale_dtype))) return rc;
   GemmParams p = base_params(counts, counts_dtype, E, M);
   p.A = static_cast<const uint16_t*>(a);
   p.lda = lda;
   p.a_idx = a_idx;
-  p.B = static_cast<const uint16_t*>(w);
+  p.B = w;
   p.ldb = stride_wk;
   p.strideBe = stride_we;
   p.K = (int)K;
@@ -960,7 +1121,14 @@ int hmoe_grouped_mm(const void* a, int64_t lda, int a_dtype, const void* w, int 
   p.y_idx = y_idx;
   p.scale = scale;
   p.scale_f32 = scale_dtype == HMOE_DT_F32;
-return launch_mgroup<MGROUP, false, true, EPI_STORE>(p, N, reinterpret_cast<hipStream_t>(stream));
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (i8) {
+    p.w_scale = w_scale;
+    p.w_scale_f32 = w_scale_dtype == HMOE_DT_F32;
+    p.ldws = N;
+    return launch_mgroup_i8<EPI_STORE>(p, N, s);
+  }
+  return launch_mgroup<MGROUP, false, true, EPI_STORE>(p, N, s);
 }
 
 int hmoe_gate_up_swiglu(const void* x, int64_t ldx, const int32_t* a_idx, const void* wgu, int64_t E, int64_t d,
@@ -972,11 +1140,12 @@ int hmoe_gate_up_swiglu(const void* x, int64_t ldx, const int32_t* a_idx, const 
   if (!x || !wgu || !act || d <= 0 || h <= 0) return HMOE_ERR_ARG;
   if (d % 8 || h % 8 || ldx % 8 || ldx < d) return HMOE_ERR_SHAPE;
   if (!al16(x) || !al16(wgu) || !al16(act) || !al16(gu)) return HMOE_ERR_ARG;
+  if ((a_idx && !off32(M * ldx * 2)) || !off32(d * 2 * h * 2)) return HMOE_ERR_SHAPE;
   GemmParams p = base_params(counts, counts_dtype, E, M);
   p.A = static_cast<const uint16_t*>(x);
   p.lda = ldx;
   p.a_idx = a_idx;
-  p.B = static_cast<const uint16_t*>(wgu);
+  p.B = (wgu);
   p.ldb = 2 * h;
   p.strideBe = d * 2 * h;
   p.K = (int)d;
@@ -997,10 +1166,11 @@ int hmoe_down_scatter(const void* act, const void* wd, int64_t E, int64_t h, int
   if (!act || !wd || !y || d <= 0 || h <= 0) return HMOE_ERR_ARG;
   if (d % 8 || h % 8) return HMOE_ERR_SHAPE;
   if (!al16(act) || !al16(wd) || !al16(y) || !al16(yhat)) return HMOE_ERR_ARG;
+  if (!off32(h * d * 2)) return HMOE_ERR_SHAPE;
   GemmParams p = base_params(counts, counts_dtype, E, M);
   p.A = static_cast<const uint16_t*>(act);
   p.lda = h;
-  p.B = static_cast<const uint16_t*>(wd);
+  p.B = (wd);
   p.ldb = d;
   p.strideBe = h * d;
   p.K = (int)h;
@@ -1014,6 +1184,65 @@ int hmoe_down_scatter(const void* act, const void* wd, int64_t E, int64_t h, int
   return launch_mgroup<MGROUP, false, true, EPI_STORE>(p, d, reinterpret_cast<hipStream_t>(stream));
 }
 
+int hmoe_gate_up_swiglu_i8(const void* x, int64_t ldx, const int32_t* a_idx, const void* wgu_q, const void* wgu_s,
+                           int wgu_s_dtype, int64_t E, int64_t d, int64_t h, const void* counts, int counts_dtype,
+                           int64_t M, void* act, hmoe_stream_t stream) {
+  int rc = check_common(counts, counts_dtype, E, M);
+  if (rc) return rc;
+  if (M == 0) return HMOE_OK;
+  if (!x || !act || d <= 0 || h <= 0) return HMOE_ERR_ARG;
+  if (d % 8 || h % 16 || ldx % 8 || ldx < d) return HMOE_ERR_SHAPE;
+  if (!al16(x) || !al16(act)) return HMOE_ERR_ARG;
+  if ((a_idx && !off32(M * ldx * 2)) || !off32(d * 2 * h)) return HMOE_ERR_SHAPE;
+  if ((rc = check_i8(wgu_q, 2 * h, d, 2 * h, d * 2 * h, wgu_s, wgu_s_dtype))) return rc;
+  GemmParams p = base_params(counts, counts_dtype, E, M);
+  p.A = static_cast<const uint16_t*>(x);
+  p.lda = ldx;
+  p.a_idx = a_idx;
+  p.B = wgu_q;
+  p.ldb = 2 * h;
+  p.strideBe = d * 2 * h;
+  p.K = (int)d;
+  p.N = (int)h;
+  p.h = (int)h;
+  p.C = act;
+  p.ldc = h;
+  p.w_scale = wgu_s;
+  p.w_scale_f32 = wgu_s_dtype == HMOE_DT_F32;
+  p.ldws = 2 * h;
+  return launch_mgroup_i8<EPI_SWIGLU>(p, h, reinterpret_cast<hipStream_t>(stream));
+}
+
+int hmoe_down_scatter_i8(const void* act, const void* wd_q, const void* wd_s, int wd_s_dtype, int64_t E, int64_t h,
+                         int64_t d, const void* counts, int counts_dtype, int64_t M, const uint16_t* w_sorted,
+                         const int32_t* y_idx, void* y, hmoe_stream_t stream) {
+  int rc = check_common(counts, counts_dtype, E, M);
+  if (rc) return rc;
+  if (M == 0) return HMOE_OK;
+  if (!act || !y || d <= 0 || h <= 0) return HMOE_ERR_ARG;
+  if (h % 8 || d % 16) return HMOE_ERR_SHAPE;
+  if (!al16(act) || !al16(y)) return HMOE_ERR_ARG;
+  if (!off32(h * d)) return HMOE_ERR_SHAPE;
+  if ((rc = check_i8(wd_q, d, h, d, h * d, wd_s, wd_s_dtype))) return rc;
+  GemmParams p = base_params(counts, counts_dtype, E, M);
+  p.A = static_cast<const uint16_t*>(act);
+  p.lda = h;
+  p.B = wd_q;
+  p.ldb = d;
+  p.strideBe = h * d;
+  p.K = (int)h;
+  p.N = (int)d;
+  p.C = y;
+  p.ldc = d;
+  p.y_idx = y_idx;
+  p.scale = w_sorted;
+  p.scale_f32 = 0;
+  p.w_scale = wd_s;
+  p.w_scale_f32 = wd_s_dtype == HMOE_DT_F32;
+  p.ldws = d;
+  return launch_mgroup_i8<EPI_STORE>(p, d, reinterpret_cast<hipStream_t>(stream));
+}
+
 int hmoe_down_dgrad_swiglu(const void* dy, const int32_t* a_idx, const uint16_t* w_sorted, const void* wd,
                            int64_t E, int64_t h, int64_t d, const void* counts, int counts_dtype, int64_t M,
                            const void* gu, void* dgu, hmoe_stream_t stream) {
@@ -1023,11 +1252,12 @@ int hmoe_down_dgrad_swiglu(const void* dy, const int32_t* a_idx, const uint16_t*
   if (!dy || !wd || !gu || !dgu || d <= 0 || h <= 0) return HMOE_ERR_ARG;
   if (d % 8 || h % 8) return HMOE_ERR_SHAPE;
   if (!al16(dy) || !al16(wd) || !al16(gu) || !al16(dgu)) return HMOE_ERR_ARG;
+  if ((a_idx && !off32(M * d * 2)) || !off32(h * d * 2)) return HMOE_ERR_SHAPE;
   GemmParams p = base_params(counts, counts_dtype, E, M);
   p.A = static_cast<const uint16_t*>(dy);
   p.lda = d;
   p.a_idx = a_idx;
-  p.B = static_cast<const uint16_t*>(wd);  // (E, h, d): row n = h index, k = d contiguous
+  p.B = (wd);  // (E, h, d): row n = h index, k = d contiguous
   p.ldb = d;
   p.strideBe = h * d;
   p.K = (int)d;
@@ -1048,10 +1278,11 @@ int hmoe_gate_up_dgrad(const void* dgu, const void* wgu, int64_t E, int64_t d, i
   if (dxs_dtype != HMOE_DT_BF16 && dxs_dtype != HMOE_DT_F32) return HMOE_ERR_DTYPE;
   if (d % 8 || h % 8) return HMOE_ERR_SHAPE;
   if (!al16(dgu) || !al16(wgu) || !al16(dxs)) return HMOE_ERR_ARG;
+  if (!off32(d * 2 * h * 2)) return HMOE_ERR_SHAPE;
   GemmParams p = base_params(counts, counts_dtype, E, M);
   p.A = static_cast<const uint16_t*>(dgu);
   p.lda = 2 * h;
-  p.B = static_cast<const uint16_t*>(wgu);  // (E, d, 2h): row n = d index, k = 2h contiguous
+  p.B = (wgu);  // (E, d, 2h): row n = d index, k = 2h contiguous
   p.ldb = 2 * h;
   p.strideBe = d * 2 * h;
   p.K = (int)(2 * h);
@@ -1072,10 +1303,11 @@ int hmoe_grouped_wgrad(const void* a, int64_t lda, const void* b, int64_t ldb, i
   if (dw_dtype != HMOE_DT_F32 && dw_dtype != HMOE_DT_BF16) return HMOE_ERR_DTYPE;
   if (P % 8 || N % 8 || lda % 8 || ldb % 8 || lda < P || ldb < N) return HMOE_ERR_SHAPE;
   if (!al16(a) || !al16(b) || !al16(dw)) return HMOE_ERR_ARG;
+  if (!off32(M * lda * 2) || !off32(M * ldb * 2)) return HMOE_ERR_SHAPE;  // an expert's rows from its first
   GemmParams p = base_params(counts, counts_dtype, E, M);
   p.A = static_cast<const uint16_t*>(a);
   p.lda = lda;
-  p.B = static_cast<const uint16_t*>(b);
+  p.B = (b);
   p.ldb = ldb;
   p.P = (int)P;
   p.N = (int)N;

@@ -17,20 +17,19 @@ from .moe_triton import grouped_mm
 def _fused_moe_infer(self, x, topk_ids, topk_weight):
     """aurora/hf_compat.py:63-82 (the fused branch): stable sort of the flat routed rows by expert, gate/up GEMM
     over gathered token rows with the SwiGLU fused into its epilogue, down GEMM scaled by the bf16-rounded routing
-    weight and scattered back to (token, slot) order, sum over the k slots."""
+    weight and scattered back to (token, slot) order, sum over the k slots.  Layers fused with quant="int8" run the
+    int8-weight forms of the two GEMMs (per-column scales applied to the fp32 sums)."""
     n, k = topk_ids.shape
     E = self._wgu.shape[0]
     if self._mode is None:  # decided on the device the weights ended up on
         self._mode = _pick_mode(x.device, x.dtype)
-    if getattr(self, "_wgu_s", None) is not None or getattr(self, "_wd_s", None) is not None:
-        raise NotImplementedError("int8 expert weights are not supported by the hmoe kernels yet")
     if self._act is not torch.nn.functional.silu and not isinstance(self._act, torch.nn.SiLU):
         raise NotImplementedError("the hmoe SwiGLU epilogue implements silu(g) * u only")
     x = x.contiguous()
     disp = ops.dispatch(topk_ids.contiguous(), E, topk_w=topk_weight.contiguous(), want_inv=False)
     M = n * k
-    act, _ = ops.gate_up_swiglu(x, self._wgu, disp.counts, M, a_idx=disp.a_idx)
-    y, _ = ops.down_scatter(act, self._wd, disp.counts, M, disp.w_sorted, disp.order)
+    act, _ = ops.gate_up_swiglu(x, self._wgu, disp.counts, M, a_idx=disp.a_idx, wgu_s=self._wgu_s)
+    y, _ = ops.down_scatter(act, self._wd, disp.counts, M, disp.w_sorted, disp.order, wd_s=self._wd_s)
     return ops.combine(y, n, k)
 
 
@@ -45,15 +44,18 @@ def _quant_int8(w):
     return (w.float() / scale.unsqueeze(1)).round().clamp(-127, 127).to(torch.int8), scale.to(torch.bfloat16)
 
 
-def _self_test(fn, device, dtype):
-    """aurora/hf_compat.py:112-121: fn(a, w, counts) against plain matmuls on 48x64 @ (3, 64, 32) with counts
-    [16, 0, 32] (an empty expert in the middle), allclose(atol=0.1, rtol=0.05)."""
+def _self_test(fn, device, dtype, quant=False):
+    """aurora/hf_compat.py:112-121: fn(a, w, w_scale, counts) against plain matmuls on 48x64 @ (3, 64, 32) with
+    counts [16, 0, 32] (an empty expert in the middle), allclose(atol=0.1, rtol=0.05).  quant: fn gets int8 weights
+    and their scales, the reference product their dequantised values."""
     g = torch.Generator(device="cpu").manual_seed(0)
     a = torch.randn(48, 64, generator=g).to(device=device, dtype=dtype)
     b = torch.randn(3, 64, 32, generator=g).to(device=device, dtype=dtype)
     counts = torch.tensor([16, 0, 32], device=device)
-    ref = torch.cat([a[:16].float() @ b[0].float(), a[16:].float() @ b[2].float()])
-    return torch.allclose(fn(a, b, counts).float(), ref, atol=1e-1, rtol=5e-2)
+    w, ws = _quant_int8(b) if quant else (b, None)
+    ref_w = _dequant(w, ws, dtype).float()
+    ref = torch.cat([a[:16].float() @ ref_w[0], a[16:].float() @ ref_w[2]])
+    return torch.allclose(fn(a, w, ws, counts).float(), ref, atol=1e-1, rtol=5e-2)
 
 
 def _pick_mode(device, dtype):
@@ -62,17 +64,18 @@ def _pick_mode(device, dtype):
         raise RuntimeError("hmoe fused MoE needs a ROCm GPU device (the kernels have no CPU path)")
     if dtype != torch.bfloat16:
         raise TypeError(f"hmoe fused MoE runs bf16 activations (got {dtype})")
-    if not _self_test(lambda a, w, c: grouped_mm(a, w, c), device, dtype):
+    fn = lambda a, w, s, c: grouped_mm(a, w, c, w_scale=s)
+    if not (_self_test(fn, device, dtype) and _self_test(fn, device, dtype, quant=True)):
         raise RuntimeError("hmoe grouped_mm failed its known-answer self-test on this device")
     return "hip"
 
 
 def fuse_moe(model, quant=""):
     """aurora/hf_compat.py:142-169: swap every MoE block's per-expert loop for the batched version; the per-expert
-    modules are dropped (the stacked weights replace them).  Inference only.  quant="int8" is not supported yet."""
+    modules are dropped (the stacked weights replace them).  Inference only.  quant="int8" (aurora/hf_compat.py:
+    159-162): expert weights stored as int8 with a per-(expert, output column) bf16 scale, half the memory; the
+    GEMMs read the int8 weights directly and still multiply in bf16."""
     assert quant in ("", "int8"), quant
-    if quant:
-        raise NotImplementedError("int8 expert weights are not supported by the hmoe kernels yet")
     n = 0
     for mod in model.modules():
         experts = getattr(mod, "experts", None)
@@ -81,10 +84,10 @@ def fuse_moe(model, quant=""):
         # (E, in, out) contiguous: wgu = [gate | up] along out, wd = down; buffers, so .to() moves them
         wgu = torch.stack([torch.cat([e.gate_proj.weight, e.up_proj.weight]).t() for e in experts]).contiguous()
         wd = torch.stack([e.down_proj.weight.t() for e in experts]).contiguous()
-        mod.register_buffer("_wgu", wgu, persistent=False)
-        mod.register_buffer("_wgu_s", None, persistent=False)
-        mod.register_buffer("_wd", wd, persistent=False)
-        mod.register_buffer("_wd_s", None, persistent=False)
+        for name, w in (("_wgu", wgu), ("_wd", wd)):
+            w, sc = _quant_int8(w) if quant else (w, None)
+            mod.register_buffer(name, w, persistent=False)
+            mod.register_buffer(name + "_s", sc, persistent=False)
         del wgu, wd
         mod._act = experts[0].act_fn
         mod._mode = None

@@ -35,17 +35,18 @@ def grouped_mm(a: torch.Tensor, w: torch.Tensor, counts: torch.Tensor, sched=Non
     names the row to read --, w (E, K, N) with contiguous rows, counts (E,) rows per expert (sum = M) -> (M, N) of
     a.dtype.  scale[r] multiplies output row r; y_idx[r] is where row r is written.  `sched` (make_schedule's
     output) is accepted for call compatibility; the kernel derives its own tile map from `counts` on the device.
-    w may not be int8 (w_scale): that variant is not implemented in this build."""
+    w may be int8 with w_scale (E, N) (aurora/moe_triton.py:44-51): the integers enter the bf16 products exactly and
+    the per-column scale multiplies the fp32 sum, before `scale`."""
     M = a_idx.numel() if a_idx is not None else a.shape[0]
     assert w.stride(2) == 1, "w must be (E, K, N) with contiguous rows"
-    if w_scale is not None:
-        raise NotImplementedError("int8 expert weights (w_scale) are not supported by the hmoe kernels yet")
-    if a.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
-        raise TypeError(f"hmoe grouped_mm supports bf16 a and w (got {a.dtype}, {w.dtype})")
+    if a.dtype != torch.bfloat16 or w.dtype not in (torch.bfloat16, torch.int8):
+        raise TypeError(f"hmoe grouped_mm supports bf16 a and bf16 or int8 w (got {a.dtype}, {w.dtype})")
+    if (w.dtype == torch.int8) != (w_scale is not None):
+        raise ValueError("int8 weights need w_scale (E, N); bf16 weights take none")
     a = a.contiguous()
     if a_idx is not None and a_idx.dtype != torch.int32:
         a_idx = a_idx.to(torch.int32)
     if y_idx is not None and y_idx.dtype != torch.int32:
         y_idx = y_idx.to(torch.int32)
     return ops.grouped_mm(a, w, counts, M, a_idx=a_idx.contiguous() if a_idx is not None else None,
-                          y_idx=y_idx.contiguous() if y_idx is not None else None, scale=scale)
+                          y_idx=y_idx.contiguous() if y_idx is not None else None, scale=scale, w_scale=w_scale)

@@ -139,6 +139,12 @@ def grouped_mm(a, w, counts, M, a_idx=None, y_idx=None, scale=None, w_scale=None
     counts = _counts(counts)
     if a.stride(1) != 1:
         a = a.contiguous()
+    if w.stride(2) != 1:
+        w = w.contiguous()
+    if w_scale is not None:
+        w_scale = _contig(w_scale, "w_scale")
+        if w_scale.shape != (E, N):
+            raise ValueError(f"w_scale must be (E, N) = {(E, N)}, got {tuple(w_scale.shape)}")
     y = out if out is not None else torch.empty(M, N, device=a.device, dtype=a.dtype)
     if scale is not None:
         scale = _contig(scale, "scale")
@@ -155,13 +161,34 @@ def grouped_mm(a, w, counts, M, a_idx=None, y_idx=None, scale=None, w_scale=None
     return y
 
 
-def gate_up_swiglu(x, wgu, counts, M, a_idx=None, keep_gu=False):
+def _w_scale(w, w_s, n):
+    """int8 weights need their (E, n) per-column scales; bf16 weights take none."""
+    if (w.dtype == torch.int8) != (w_s is not None):
+        raise ValueError("int8 weights come with a scale (E, N); bf16 weights take none")
+    if w_s is not None:
+        w_s = _contig(w_s, "weight scale")
+        if w_s.shape != (w.shape[0], n) or w_s.dtype not in (torch.bfloat16, torch.float32):
+            raise ValueError(f"weight scale must be bf16 or fp32 of shape {(w.shape[0], n)}")
+    return w_s
+
+
+def gate_up_swiglu(x, wgu, counts, M, a_idx=None, keep_gu=False, wgu_s=None):
+    """act = bf16(bf16(silu(g)) * u) for [g | u] = x[a_idx] @ wgu[e]; wgu bf16, or int8 with per-column scales
+    wgu_s (E, 2h) (inference only: no gu)."""
     E, d, h2 = wgu.shape
     h = h2 // 2
     s = _dev_stream(x)
     wgu = _contig(wgu, "wgu")
     counts = _counts(counts)
+    wgu_s = _w_scale(wgu, wgu_s, h2)
     act = torch.empty(M, h, device=x.device, dtype=torch.bfloat16)
+    if wgu_s is not None:
+        if keep_gu:
+            raise ValueError("int8 weights are inference only (no gu kept)")
+        with _Probe("gate_up_swiglu"):
+            L.call("hmoe_gate_up_swiglu_i8", L.ptr(x), x.stride(0), L.ptr(a_idx), L.ptr(wgu), L.ptr(wgu_s),
+                   L.dt(wgu_s), E, d, h, L.ptr(counts), L.dt(counts), M, L.ptr(act), s)
+        return act, None
     gu = torch.empty(M, h2, device=x.device, dtype=torch.bfloat16) if keep_gu else None
     with _Probe("gate_up_swiglu"):
         L.call("hmoe_gate_up_swiglu", L.ptr(x), x.stride(0), L.ptr(a_idx), L.ptr(wgu), E, d, h, L.ptr(counts),
@@ -169,12 +196,21 @@ def gate_up_swiglu(x, wgu, counts, M, a_idx=None, keep_gu=False):
     return act, gu
 
 
-def down_scatter(act, wd, counts, M, w_sorted, y_idx, keep_yhat=False):
+def down_scatter(act, wd, counts, M, w_sorted, y_idx, keep_yhat=False, wd_s=None):
+    """y[y_idx[r]] = bf16(act[r] @ wd[e] * w_sorted[r]); wd bf16, or int8 with per-column scales wd_s (E, d)."""
     E, h, d = wd.shape
     s = _dev_stream(act)
     wd = _contig(wd, "wd")
     counts = _counts(counts)
+    wd_s = _w_scale(wd, wd_s, d)
     y = torch.empty(M, d, device=act.device, dtype=torch.bfloat16)
+    if wd_s is not None:
+        if keep_yhat:
+            raise ValueError("int8 weights are inference only (no yhat kept)")
+        with _Probe("down_scatter"):
+            L.call("hmoe_down_scatter_i8", L.ptr(act), L.ptr(wd), L.ptr(wd_s), L.dt(wd_s), E, h, d, L.ptr(counts),
+                   L.dt(counts), M, L.ptr(w_sorted), L.ptr(y_idx), L.ptr(y), s)
+        return y, None
     yhat = torch.empty(M, d, device=act.device, dtype=torch.bfloat16) if keep_yhat else None
     with _Probe("down_scatter"):
         L.call("hmoe_down_scatter", L.ptr(act), L.ptr(wd), E, h, d, L.ptr(counts), L.dt(counts), M, L.ptr(w_sorted),
