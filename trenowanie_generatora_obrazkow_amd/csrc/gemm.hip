@@ -907,29 +907,44 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
           });
         }
       } else if constexpr (EPI == EPI_SWIGLU_BWD) {
-        constexpr int RB = C::FN * 32 * 2, NSP = (RB + 127) / 128;  // dg row bytes and sub-planes; du follows
-        const int64_t r = row0 + rbase + lrow;
-        const int64_t rc = r < row_end ? r : row0;
-        const uint16_t* gurow = p.gu_in + rc * (int64_t)(2 * p.h);
+        // sub-planes: dg [0, NSP), du [NSP, 2 NSP), then the pass's forward [g | u] inputs: g [2 NSP, 3 NSP),
+        // u [3 NSP, 4 NSP), in the same layout park_bf16 writes (so a lane reads its accumulator-shaped 8 bytes back)
+        constexpr int RB = C::FN * 32 * 2, NSP = (RB + 127) / 128;
+        static_assert(4 * NSP * 4096 <= 8 * CH, "SwiGLU backward staging: dg, du, g, u sub-planes");
         const float sc = row_scale(rbase + lrow);
-        // the pass's [g | u] in the accumulator layout (8 bytes per column group), all loads issued before use
-        uint2 gl[C::FN][4], ul[C::FN][4];
+        // this pass's g and u rows copied into their sub-planes with direct loads: instruction (array, sp, i) fills
+        // rows 8i..8i+7 of a sub-plane, lane l row 8i + l/8, physical chunk l%8 = logical chunk (l%8) ^ (l/8)
+        auto issue_gu = [&](int pa) {
+          const int rb = pa * C::FSM + wm * 32;
+          i32x4 rs = make_rsrc(p.gu_in + row0 * (int64_t)(2 * p.h));
+          const int rl = lane >> 3, cl = (lane & 7) ^ rl;
 #pragma unroll
-        for (int b = 0; b < C::FN; ++b)
+          for (int arr = 0; arr < 2; ++arr)
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int j = n0 + col_of(b, g);
-            const int jc = j < p.N ? j : 0;
-            gl[b][g] = *reinterpret_cast<const uint2*>(gurow + jc);
-            ul[b][g] = *reinterpret_cast<const uint2*>(gurow + p.h + jc);
-          }
+            for (int sp = 0; sp < NSP; ++sp)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const int r = 8 * i + rl;
+                const int cw = sp * 64 + 8 * cl;  // column within the wave's FN*32
+                const int tc = (cw / 32) * C::FSN + wn * 32 + cw % 32;
+                const bool ok = row0 + rb + r < row_end && n0 + tc < p.N && sp * 128 + cl * 16 < RB;
+                const uint32_t vo = ok ? (uint32_t)(((rb + r) * (2 * p.h) + arr * p.h + n0 + tc) * 2) : kOOB;
+                buf2lds(vo, rs, 0u, sp_addr((2 + arr) * NSP + sp, 8 * i, 0));
+              }
+        };
+        if (a == 0) issue_gu(0);
+        wait_vm<0>();  // this pass's [g | u] (and the previous pass's stores: in-order counter)
+        asm volatile("" ::: "memory");
 #pragma unroll
         for (int b = 0; b < C::FN; ++b) {
           pin_agpr(acc[a][b]);
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
-            const float gg[4] = {bf_lo(gl[b][g].x), bf_hi(gl[b][g].x), bf_lo(gl[b][g].y), bf_hi(gl[b][g].y)};
-            const float uu[4] = {bf_lo(ul[b][g].x), bf_hi(ul[b][g].x), bf_lo(ul[b][g].y), bf_hi(ul[b][g].y)};
+            const int byte = (b * 32 + 8 * g + lcol) * 2;
+            const uint2 gl = *reinterpret_cast<const uint2*>(sp_addr(2 * NSP + byte / 128, lrow, byte % 128));
+            const uint2 ul = *reinterpret_cast<const uint2*>(sp_addr(3 * NSP + byte / 128, lrow, byte % 128));
+            const float gg[4] = {bf_lo(gl.x), bf_hi(gl.x), bf_lo(gl.y), bf_hi(gl.y)};
+            const float uu[4] = {bf_lo(ul.x), bf_hi(ul.x), bf_lo(ul.y), bf_hi(ul.y)};
             float dg[4], du[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
@@ -944,6 +959,8 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
             park_bf16(NSP, b, g, cvt_bf2(du[0], du[1]), cvt_bf2(du[2], du[3]));
           }
         }
+        // the next pass's inputs load while this pass drains (its g / u sub-planes have been read above)
+        if (a + 1 < C::FM) issue_gu(a + 1);
         drain(0, RB, 2, [&](int rr, int tc, uint4 v) {
           const int64_t row = row0 + rbase + rr;
           const int j = n0 + tc;
