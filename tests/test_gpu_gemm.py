@@ -65,6 +65,37 @@ def test_grouped_mm_fused(oracle, tile, T, K, N, E, k, skew):
     assert_close_bf16(f32(y2), ref2, "grouped_mm sorted")
 
 
+@pytest.mark.parametrize("counts", [[257, 320, 321, 128, 129, 0, 255, 512, 1, 64],
+                                    [63, 65, 191, 193, 0, 0, 700, 2]])
+def test_grouped_mm_partial_tiles(oracle, tile, counts):
+    """Expert ends that leave 1, 63-65, 127-129, 191-193 or 255 rows in a partial m-tile (run with the empty 64-row
+    fragment rows skipped), a last sorted row whose bf16 routing weight sits in the low half of a dword at the end of
+    the array, plain and with gather / scale / scatter, bf16 and int8 weights."""
+    from trenowanie_generatora_obrazkow_amd import moe_triton
+    print(f"partial tiles counts={counts} tile={tile}", flush=True)
+    E, K, N = len(counts), 264, 320
+    M = sum(counts)
+    g = torch.Generator().manual_seed(M)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(E, K, N, generator=g) * 0.05).bfloat16()
+    c = torch.tensor(counts)
+    perm = torch.randperm(M, generator=g)
+    a_idx, y_idx = perm.int(), torch.randperm(M, generator=g).int()
+    sc = torch.rand(M, generator=g).bfloat16()
+    dev = torch.device("cuda")
+    y = moe_triton.grouped_mm(x.to(dev), w.to(dev), c.to(dev))
+    assert_close_bf16(f32(y), oracle.grouped_mm(f32(x), f32(w), c.numpy()), "partial plain")
+    y = moe_triton.grouped_mm(x.to(dev), w.to(dev), c.to(dev), a_idx=a_idx.to(dev), y_idx=y_idx.to(dev),
+                              scale=sc.to(dev))
+    ref = oracle.grouped_mm(f32(x), f32(w), c.numpy(), a_idx=a_idx.numpy(), y_idx=y_idx.numpy(), scale=f32(sc))
+    assert_close_bf16(f32(y), ref, "partial fused")
+    q, s = oracle.quant_int8(f32(w))
+    y = moe_triton.grouped_mm(x.to(dev), torch.from_numpy(q).to(dev), c.to(dev),
+                              w_scale=torch.from_numpy(s).bfloat16().to(dev))
+    ref = oracle.grouped_mm(f32(x), q.astype(np.float32), c.numpy(), w_scale=s.astype(np.float64))
+    assert_close_bf16(f32(y), ref, "partial int8")
+
+
 @pytest.mark.parametrize("M,P,N,E,skew", [(4096, 256, 512, 8, 0), (3000, 520, 264, 5, 1), (777, 128, 1024, 16, 1)])
 def test_grouped_wgrad(oracle, tile, M, P, N, E, skew):
     from trenowanie_generatora_obrazkow_amd import ops

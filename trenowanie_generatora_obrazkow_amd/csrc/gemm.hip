@@ -332,7 +332,7 @@ template <class C, int MODE, bool A_MN, bool B_MN, int EPI>
 __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   __shared__ int64_t s_rstart[kMaxEGemm + 1];
-  __shared__ int s_tstart[kMaxEGemm + 1];
+  __shared__ int s_tstart[kMaxEGemm + 1];  // MGROUP: prefix of ceil(count / BM); KGROUP: one m-tile per expert
   // per-row epilogue inputs of the tile (scatter index, routing weight), double-buffered by tile parity: a wave
   // that has finished its epilogue may already fill the next tile's while others still read this one
   // (2 KB each: 256 rows plus up to 3 leading rows, since the copy starts at the 16-byte boundary below row0)
@@ -418,7 +418,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
     // ---- tile decode ----
     int mt, nb;
     {
-      const int per_group = C::GM * nb_n;
+      const int per_group = C::GM * nb_n;  // bands of GM m-tiles x all n-tiles
       const int g = tile / per_group;
       const int first = g * C::GM;
       const int gsz = min(total_m - first, C::GM);
@@ -543,7 +543,10 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
         const uintptr_t first = reinterpret_cast<uintptr_t>(arr) + (uintptr_t)row0 * esz;
         const uintptr_t base = first & ~(uintptr_t)15;
         const int sh = (int)(first - base) / esz;
-        const int64_t bytes = (p.M - row0) * esz + (int64_t)(first - base);  // valid bytes from the aligned base
+        // valid bytes from the aligned base, rounded up to the 16-byte chunk: the range check zeroes every dword
+        // that reaches past the range, so an unrounded end would drop a last 2-byte element in the dword's low half
+        // (the chunk never crosses a page, so reading its tail is safe)
+        const int64_t bytes = ((p.M - row0) * esz + (int64_t)(first - base) + 15) & ~(int64_t)15;
         if (wave == 0) {
           i32x4 rs = make_rsrc(reinterpret_cast<const void*>(base));
           rs.z = __builtin_amdgcn_readfirstlane((int)min(bytes, (int64_t)0x7FFFFFF0));
@@ -604,120 +607,148 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
     //                  read ks0 fragments of slice kt+1    | MFMAs on ks1 fragments of slice kt
     // The barrier comes after every wave has read all of slice kt, so its slot can be refilled at once: four
     // slices are in flight while one is consumed, and LDS read latency hides under the MFMAs.
+    // FE = fragment rows (of FM) that hold tile rows: a partial m-tile (an expert's last rows) with at most 64 or 128
+    // rows runs the loop with FE = 1 or 2, skipping the MFMAs and fragment reads of the empty rows (its copies are
+    // unchanged, so the wait counts hold); the accumulators of the other rows stay zero and are not stored.  Such a
+    // tile takes about FE/FM of a full tile's time.
     typedef typename TileSel<A_MN, C::BM, C::NWAVES>::type TA;
     typedef typename TileSel<B_MN, C::BN, C::NWAVES, C::BE, C::FN>::type TB;
-    constexpr int RD = C::FM * (A_MN ? 2 : 1) + C::FN * (B_MN ? 2 : 1);  // LDS reads per k16 step
-    constexpr int NMF = C::FM * C::FN;                                     // MFMAs per k16 step
-    constexpr int PAIRS = RD < NMF ? RD : NMF;
     struct Frags {
       bf16x8 xa[C::FM], wb[C::FN];
     };
-    auto read = [&](const char* slot, int ks) {
-      Frags f;
-#pragma unroll
-      for (int a = 0; a < C::FM; ++a) f.xa[a] = TA::frag(slot, a * C::FSM, loff_a, ks);
-#pragma unroll
-      for (int b = 0; b < C::FN; ++b) f.wb[b] = TB::frag(slot + C::A_BYTES, b * C::FSN, loff_b, ks);
-      return f;
-    };
-    auto mfmas = [&](const Frags f) {
-#pragma unroll
-      for (int a = 0; a < C::FM; ++a)
-#pragma unroll
-        for (int b = 0; b < C::FN; ++b)
-          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.wb[b], f.xa[a], acc[a][b], 0, 0, 0);
-    };
-    // one LDS read after each MFMA while both last, then whichever is left
-    auto interleave = [&]() {
-#pragma unroll
-      for (int i = 0; i < PAIRS; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-      }
-      if constexpr (NMF > PAIRS) __builtin_amdgcn_sched_group_barrier(0x008, NMF - PAIRS, 0);
-      if constexpr (RD > PAIRS) __builtin_amdgcn_sched_group_barrier(0x100, RD - PAIRS, 0);
-    };
     static_assert(kNStage == 4 && kBK == 32, "pipeline written for a 4-deep ring of two-step slices");
+    auto main_loop = [&](auto fe_tag) {
+      constexpr int FE = decltype(fe_tag)::value;
+      constexpr int RD = FE * (A_MN ? 2 : 1) + C::FN * (B_MN ? 2 : 1);  // LDS reads per k16 step
+      constexpr int NMF = FE * C::FN;                                      // MFMAs per k16 step
+      constexpr int PAIRS = RD < NMF ? RD : NMF;
+      auto read = [&](const char* slot, int ks) {
+        Frags f;
 #pragma unroll
-    for (int s = 0; s < kNStage; ++s)
-      if (s < nk) issue(s);
-    Frags f0 = {}, f1 = {};
-    if (nk > 0) {
-      const int ahead = min(nk - 1, kNStage - 1);  // slices issued after slice 0
-      if (ahead >= 3)
-        wait_vm<3 * LOADS>();
-      else if (ahead == 2)
-        wait_vm<2 * LOADS>();
-      else if (ahead == 1)
-        wait_vm<LOADS>();
-      else
-        wait_vm<0>();
-      lds_barrier();
-      f0 = read(cons, 0);
-    }
-    // The two MFMA blocks are unconditional (a conditional copy would split the accumulators' live ranges); on the
-    // last slice the ks0 read of the "next" slot reads stale LDS that is never used.
-    for (int kt = 0; kt < nk; ++kt) {
-      f1 = read(cons, 1);
-      mfmas(f0);
-      interleave();
-      const int ahead = min(nk - 1, kt + kNStage - 1) - (kt + 1);  // slices issued after slice kt+1
-      if (ahead >= 2)
-        wait_vm<2 * LOADS>();
-      else if (ahead == 1)
-        wait_vm<LOADS>();
-      else
-        wait_vm<0>();
-      lds_barrier();
-      if constexpr (MODE == KGROUP) {  // (measured: weight gradients run faster with the copies issued together)
-        if (kt + kNStage < nk) issue(kt + kNStage);  // into the slot of slice kt (fill == cons here)
+        for (int a = 0; a < FE; ++a) f.xa[a] = TA::frag(slot, a * C::FSM, loff_a, ks);
+#pragma unroll
+        for (int b = 0; b < C::FN; ++b) f.wb[b] = TB::frag(slot + C::A_BYTES, b * C::FSN, loff_b, ks);
+        return f;
+      };
+      auto mfmas = [&](const Frags f) {
+#pragma unroll
+        for (int a = 0; a < FE; ++a)
+#pragma unroll
+          for (int b = 0; b < C::FN; ++b)
+            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.wb[b], f.xa[a], acc[a][b], 0, 0, 0);
+      };
+      // one LDS read after each MFMA while both last, then whichever is left
+      auto interleave = [&]() {
+#pragma unroll
+        for (int i = 0; i < PAIRS; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+        }
+        if constexpr (NMF > PAIRS) __builtin_amdgcn_sched_group_barrier(0x008, NMF - PAIRS, 0);
+        if constexpr (RD > PAIRS) __builtin_amdgcn_sched_group_barrier(0x100, RD - PAIRS, 0);
+      };
+#pragma unroll
+      for (int s = 0; s < kNStage; ++s)
+        if (s < nk) issue(s);
+      Frags f0 = {}, f1 = {};
+      if (nk > 0) {
+        const int ahead = min(nk - 1, kNStage - 1);  // slices issued after slice 0
+        if (ahead >= 3)
+          wait_vm<3 * LOADS>();
+        else if (ahead == 2)
+          wait_vm<2 * LOADS>();
+        else if (ahead == 1)
+          wait_vm<LOADS>();
+        else
+          wait_vm<0>();
+        lds_barrier();
+        f0 = read(cons, 0);
+      }
+      // The two MFMA blocks are unconditional (a conditional copy would split the accumulators' live ranges); on
+      // the last slice the ks0 read of the "next" slot reads stale LDS that is never used.
+      for (int kt = 0; kt < nk; ++kt) {
+        f1 = read(cons, 1);
+        mfmas(f0);
+        interleave();
+        const int ahead = min(nk - 1, kt + kNStage - 1) - (kt + 1);  // slices issued after slice kt+1
+        if (ahead >= 2)
+          wait_vm<2 * LOADS>();
+        else if (ahead == 1)
+          wait_vm<LOADS>();
+        else
+          wait_vm<0>();
+        lds_barrier();
+        if constexpr (MODE == KGROUP) {  // (measured: weight gradients run faster with the copies issued together)
+          if (kt + kNStage < nk) issue(kt + kNStage);  // into the slot of slice kt (fill == cons here)
+          cons += C::STAGE_BYTES;
+          if (cons == ring_end) cons = smem;
+          f0 = read(cons, 0);
+          mfmas(f1);
+          interleave();
+          continue;
+        }
+        // Second half: MFMAs on the ks1 fragments, the next slice's ks0 fragment reads and the refill of slice
+        // kt's slot with slice kt+4 (fill == cons here), one step per MFMA so the reads and copies issue in its
+        // shadow.
+        const bool refill = kt + kNStage < nk;
+        const int kr = (kt + kNStage) * kBK;
+        char* const dst = fill;
         cons += C::STAGE_BYTES;
         if (cons == ring_end) cons = smem;
-        f0 = read(cons, 0);
-        mfmas(f1);
-        interleave();
-        continue;
-      }
-      // Second half: MFMAs on the ks1 fragments, the next slice's ks0 fragment reads and the refill of slice kt's
-      // slot with slice kt+4 (fill == cons here), one step per MFMA so the reads and copies issue in its shadow.
-      const bool refill = kt + kNStage < nk;
-      const int kr = (kt + kNStage) * kBK;
-      char* const dst = fill;
-      cons += C::STAGE_BYTES;
-      if (cons == ring_end) cons = smem;
-      if (refill) {
-        fill += C::STAGE_BYTES;
-        if (fill == ring_end) fill = smem;
-      }
-#pragma unroll
-      for (int a = 0; a < C::FM; ++a)
-#pragma unroll
-        for (int b = 0; b < C::FN; ++b) {
-          const int i = a * C::FN + b;
-          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f1.wb[b], f1.xa[a], acc[a][b], 0, 0, 0);
-          if (i < C::FM)
-            f0.xa[i] = TA::frag(cons, i * C::FSM, loff_a, 0);
-          else if (i < C::FM + C::FN)
-            f0.wb[i - C::FM] = TB::frag(cons + C::A_BYTES, (i - C::FM) * C::FSN, loff_b, 0);
-          if ((i & 1) && refill) {
-            const int l = i >> 1;  // copy number: A's first, then B's
-            if (l < TA::PER_WAVE)
-              ta.issue_one(dst, wave, l, kr);
-            else if (l < LOADS)
-              tb.issue_one(dst + C::A_BYTES, wave, l - TA::PER_WAVE, kr);
-          }
-          __builtin_amdgcn_sched_barrier(0);
+        if (refill) {
+          fill += C::STAGE_BYTES;
+          if (fill == ring_end) fill = smem;
         }
-      // copies left over when there are fewer MFMA pairs than copies (small tiles)
 #pragma unroll
-      for (int l = C::FM * C::FN / 2; l < LOADS; ++l) {
-        if (!refill) break;
-        if (l < TA::PER_WAVE)
-          ta.issue_one(dst, wave, l, kr);
-        else
-          tb.issue_one(dst + C::A_BYTES, wave, l - TA::PER_WAVE, kr);
+        for (int a = 0; a < FE; ++a)
+#pragma unroll
+          for (int b = 0; b < C::FN; ++b) {
+            const int i = a * C::FN + b;
+            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f1.wb[b], f1.xa[a], acc[a][b], 0, 0, 0);
+            if (i < FE)
+              f0.xa[i] = TA::frag(cons, i * C::FSM, loff_a, 0);
+            else if (i < FE + C::FN)
+              f0.wb[i - FE] = TB::frag(cons + C::A_BYTES, (i - FE) * C::FSN, loff_b, 0);
+            if ((i & 1) && refill) {
+              const int l = i >> 1;  // copy number: A's first, then B's
+              if (l < TA::PER_WAVE)
+                ta.issue_one(dst, wave, l, kr);
+              else if (l < LOADS)
+                tb.issue_one(dst + C::A_BYTES, wave, l - TA::PER_WAVE, kr);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        // fragment reads and copies left over when there are fewer MFMAs than reads or copy pairs
+#pragma unroll
+        for (int i = FE * C::FN; i < FE + C::FN; ++i) {
+          if (i < FE)
+            f0.xa[i] = TA::frag(cons, i * C::FSM, loff_a, 0);
+          else
+            f0.wb[i - FE] = TB::frag(cons + C::A_BYTES, (i - FE) * C::FSN, loff_b, 0);
+        }
+#pragma unroll
+        for (int l = FE * C::FN / 2; l < LOADS; ++l) {
+          if (!refill) break;
+          if (l < TA::PER_WAVE)
+            ta.issue_one(dst, wave, l, kr);
+          else
+            tb.issue_one(dst + C::A_BYTES, wave, l - TA::PER_WAVE, kr);
+        }
       }
+    };
+    if constexpr (MODE == MGROUP) {
+      const int64_t rows = row_end - row0;
+      if (C::FM >= 4 && rows <= C::FSM)
+        main_loop(std::integral_constant<int, 1>{});
+      else if (C::FM >= 4 && rows <= 2 * C::FSM)
+        main_loop(std::integral_constant<int, 2>{});
+      else
+        main_loop(std::integral_constant<int, C::FM>{});
+    } else {
+      main_loop(std::integral_constant<int, C::FM>{});
     }
+    // fragment rows holding tile rows (the epilogue passes to run)
+    const int fe_rows = MODE == MGROUP ? (int)min((row_end - row0 + C::FSM - 1) / C::FSM, (int64_t)C::FM) : C::FM;
     lds_barrier();  // every wave is done with the ring before the next tile refills it
     // The epilogue's pin_agpr() hides the last MFMA write from the compiler's hazard tracking, so the wait states a
     // VALU read of an MFMA result needs (19 for a 16-pass MFMA; the 32x32x16 bf16 MFMA has 8 passes) are given here.
@@ -789,6 +820,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
     auto col_of = [&](int b, int g) { return b * C::FSN + wn * 32 + 8 * g + lcol; };  // tile column (write phase)
 #pragma unroll
     for (int a = 0; a < C::FM; ++a) {
+      if (a >= fe_rows) break;  // no tile rows in this or later passes (partial m-tile)
       const int rbase = a * C::FSM + wm * 32;  // tile row of the wave's row 0 in this pass
       if constexpr (EPI == EPI_WGRAD) {
 #pragma unroll
@@ -960,7 +992,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
           }
         }
         // the next pass's inputs load while this pass drains (its g / u sub-planes have been read above)
-        if (a + 1 < C::FM) issue_gu(a + 1);
+        if (a + 1 < fe_rows) issue_gu(a + 1);
         drain(0, RB, 2, [&](int rr, int tc, uint4 v) {
           const int64_t row = row0 + rbase + rr;
           const int j = n0 + tc;
