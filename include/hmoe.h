@@ -63,6 +63,19 @@ int hmoe_route_topk(const void* x, int64_t ldx, const void* wr, const float* bia
                     int k, int renorm, float scaling, float* logits, int32_t* topk_ids, float* topk_w,
                     hmoe_stream_t stream);
 
+/* Sigmoid, group-limited top-k router of BailingMoeV2: replaces the routing of aurora/hf_pipeline.py:352-359
+ * (PoziomkaMoE.forward).  Logits as in hmoe_route_topk (same fixed order, no bias in them); score = 1 / (1 +
+ * exp(-logit)) (the exp of the softmax router, IEEE division); routing = score + expert_bias (fp32, NULL = 0) for
+ * selection only; the experts form n_group groups of E / n_group, a group's value is the sum of its two largest
+ * routing values, the topk_group best groups are kept (ties to the lower group) and the k best experts among them
+ * selected (descending, ties to the lower expert); topk_w = selected scores / (their sum in slot order + 1e-20) *
+ * scaling.  scores (T, E) fp32 receives the sigmoid scores (NULL to skip).  E % n_group == 0; unless
+ * topk_group >= n_group (every group kept), E / n_group is a power of two in [2, 64] and k <= topk_group *
+ * E / n_group.  Other limits as hmoe_route_topk. */
+int hmoe_route_sigmoid_group(const void* x, int64_t ldx, const void* wr, const float* expert_bias, int64_t T,
+                             int64_t d, int E, int k, int n_group, int topk_group, float scaling, float* scores,
+                             int32_t* topk_ids, float* topk_w, hmoe_stream_t stream);
+
 /* Workspace bytes for hmoe_dispatch. */
 size_t hmoe_dispatch_workspace_size(int64_t T, int k, int E);
 
@@ -132,6 +145,12 @@ int hmoe_down_scatter_i8(const void* act, const void* wd_q, const void* wd_s, in
 
 /* Combine: replaces aurora/hf_compat.py:82 (y.view(n, k, -1).sum(1)): out[t] = bf16(sum_j fp32(y[t*k + j])). */
 int hmoe_combine(const void* y, int64_t T, int k, int64_t d, void* out, hmoe_stream_t stream);
+
+/* Combine plus a per-token addend: replaces aurora/hf_pipeline.py:370 (out.to(x.dtype) + self.shared_experts(x)):
+ * out[t] = bf16(bf16(sum_j fp32(y[t*k + j])) + add[t]), add (T, d) bf16 (the shared expert's output).  The
+ * reference sums the slots with index_add_ in expert order (:369); here they are summed in slot order (the same
+ * terms, fp32 accumulation). */
+int hmoe_combine_add(const void* y, int64_t T, int k, int64_t d, const void* add, void* out, hmoe_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------------------------
  * Backward.  The reference has no backward for this path (aurora/hf_compat.py:62 is @torch.no_grad); each entry

@@ -10,6 +10,9 @@ half of the oracle (oracle/router.c), loaded here through ctypes.
 Pinning (what each function is checked against, in tests/test_oracle.py):
   route / topk_from_logits   C restatement; ids vs torch.softmax + torch.topk on the same logits, logits vs
                              float64 matmul, hexp vs math.exp (ulp bound), brute force on tiny inputs, ties, -inf bias
+  sigmoid_group_from_logits  C restatement; ids / weights vs the reference's torch steps (sigmoid, group top-2 sums,
+                             group topk, masked topk, renormalise) run on CPU torch from the same scores; brute force
+                             over all group subsets on tiny inputs; sigmoid vs float64 within 3 ulp; tie rules
   dispatch                   numpy stable argsort vs the C counting sort vs torch.argsort(stable=True)/bincount, plus
                              invariants (permutation, sortedness, stability)
   make_schedule              numpy restatement vs the C block-by-block restatement vs brute-force coverage
@@ -88,6 +91,7 @@ def lib():
         L.orc_router_logits.argtypes = [P, I64, P, P, I64, I64, I32, P]
         L.orc_topk_from_logits.argtypes = [P, I64, I32, I32, I32, F32, P, P, P]
         L.orc_route.argtypes = [P, I64, P, P, I64, I64, I32, I32, I32, F32, P, P, P]
+        L.orc_sigmoid_group_from_logits.argtypes = [P, I64, I32, I32, I32, I32, P, F32, P, P, P]
         L.orc_dispatch.argtypes = [P, I64, I32, I32, P, P, P, P]
         L.orc_dispatch.restype = I32
         L.orc_make_schedule.argtypes = [P, I32, I64, I32, P, P, P]
@@ -128,6 +132,26 @@ def topk_from_logits(logits: np.ndarray, k: int, renorm: bool = True, scaling: f
     probs = np.empty((T, E), dtype=np.float32) if with_probs else None
     lib().orc_topk_from_logits(_ptr(logits), T, E, k, int(renorm), float(scaling), _ptr(ids), _ptr(w), _ptr(probs))
     return (ids, w, probs) if with_probs else (ids, w)
+
+
+def sigmoid_group_from_logits(logits, k, n_group, topk_group, bias=None, scaling=1.0):
+    """The BailingMoeV2 sigmoid, group-limited top-k (aurora/hf_pipeline.py:352-359; orders in router.c) on given fp32
+    logits (without bias).  Returns ids (T, k) int32, weights (T, k) fp32 and scores (T, E) fp32."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    T, E = logits.shape
+    ids = np.empty((T, k), dtype=np.int32)
+    w = np.empty((T, k), dtype=np.float32)
+    sc = np.empty((T, E), dtype=np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    lib().orc_sigmoid_group_from_logits(_ptr(logits), T, E, k, n_group, topk_group, _ptr(b), float(scaling),
+                                        _ptr(ids), _ptr(w), _ptr(sc))
+    return ids, w, sc
+
+
+def route_sigmoid_group(x_bits, wr_bits, k, n_group, topk_group, bias=None, scaling=1.0):
+    logits = router_logits(x_bits, wr_bits)
+    ids, w, sc = sigmoid_group_from_logits(logits, k, n_group, topk_group, bias, scaling)
+    return logits, ids, w, sc
 
 
 def route(x_bits, wr_bits, k, bias=None, renorm=True, scaling=1.0):

@@ -18,9 +18,11 @@
  *         torch.topk's order wherever two probabilities are not rounded to the same float);
  *       * weights: w_j = p_{e_j}; renorm: s = w_0 + w_1 + ... (in j order), w_j = w_j / (s + 1e-20f) * scaling;
  *         otherwise w_j = w_j * scaling.
+ *   - the sigmoid, group-limited router of BailingMoeV2 (aurora/hf_pipeline.py:352-359), from the same logits
+ *     (orc_sigmoid_group_from_logits below states its orders);
  *   - hexp: exp by Cody-Waite range reduction (Cephes split ln2 = 0.693359375 - 2.12194440e-4), a degree-7 Taylor
- *     polynomial in Horner form with fmaf, and exponent scaling by ldexpf; arguments below -87 give 0.  Used for
- *     x <= 0 only (softmax), where every non-zero result is a normal float.
+ *     polynomial in Horner form with fmaf, and exponent scaling by ldexpf; arguments below -87 give 0, above 88
+ *     infinity.  The softmax uses it for x <= 0; the sigmoid 1 / (1 + hexp(-x)) for any x.
  *   - the stable counting sort of aurora/hf_compat.py:69-72 (flat = topk_ids.reshape(-1); order =
  *     flat.argsort(stable=True); counts = bincount(flat)) and the index derivation of :78 (a_idx = order // k,
  *     y_idx = order) -- as a second, loop-based restatement next to numpy's stable argsort.
@@ -147,6 +149,73 @@ void orc_route(const uint16_t* x, int64_t ldx, const uint16_t* wr, const float* 
                int k, int renorm, float scaling, float* logits, int32_t* ids, float* w) {
     orc_router_logits(x, ldx, wr, bias, T, d, E, logits);
     orc_topk_from_logits(logits, T, E, k, renorm, scaling, ids, w, NULL);
+}
+
+/* The sigmoid, group-limited router of BailingMoeV2 (aurora/hf_pipeline.py:352-359) from given fp32 logits (no
+ * bias in them).  Follows the reference's steps, with the orders the kernel fixes:
+ *   score_e = 1 / (1 + hexp(-logit_e)) (IEEE division); routing_e = score_e + bias_e (selection only, :353);
+ *   groups of eg = E / n_group consecutive experts; a group's value = the sum of its two largest routing values
+ *   (the largest plus the second largest with multiplicity, :354); the topk_group groups with the largest values
+ *   are kept (ties to the lower group, :355); experts of the other groups are masked to -inf (:356-357);
+ *   the k largest masked routing values are selected in descending order (ties to the lower expert, :357);
+ *   weights: w_j = score_{e_j}; s = w_0 + w_1 + ... in j order; w_j = w_j / (s + 1e-20f) * scaling (:358-359).
+ * scores (T, E) optional.  topk_group >= n_group keeps every group. */
+void orc_sigmoid_group_from_logits(const float* logits, int64_t T, int E, int k, int n_group, int topk_group,
+                                   const float* bias, float scaling, int32_t* ids, float* w, float* scores) {
+    float* sc = (float*)malloc(sizeof(float) * E);
+    float* key = (float*)malloc(sizeof(float) * E);
+    unsigned char* taken = (unsigned char*)malloc(E);
+    float gval[256];
+    unsigned char gkeep[256];
+    int eg = E / n_group;
+    for (int64_t t = 0; t < T; ++t) {
+        const float* lg = logits + t * E;
+        for (int e = 0; e < E; ++e) {
+            sc[e] = 1.0f / (1.0f + orc_hexp(-lg[e]));
+            key[e] = bias ? sc[e] + bias[e] : sc[e];
+            if (scores) scores[t * E + e] = sc[e];
+        }
+        if (topk_group < n_group) {
+            for (int g = 0; g < n_group; ++g) {
+                /* largest, then the largest of the rest with one instance of it removed */
+                int i1 = g * eg;
+                for (int e = g * eg + 1; e < (g + 1) * eg; ++e)
+                    if (key[e] > key[i1]) i1 = e;
+                float m2 = -INFINITY;
+                for (int e = g * eg; e < (g + 1) * eg; ++e)
+                    if (e != i1 && key[e] > m2) m2 = key[e];
+                gval[g] = key[i1] + m2;
+                gkeep[g] = 0;
+            }
+            for (int j = 0; j < topk_group; ++j) {
+                int best = -1;
+                for (int g = 0; g < n_group; ++g)
+                    if (!gkeep[g] && (best < 0 || gval[g] > gval[best])) best = g;
+                gkeep[best] = 1;
+            }
+            for (int e = 0; e < E; ++e)
+                if (!gkeep[e / eg]) key[e] = -INFINITY;
+        }
+        memset(taken, 0, E);
+        float sel[64];
+        for (int j = 0; j < k; ++j) {
+            int best = -1;
+            for (int e = 0; e < E; ++e) {
+                if (taken[e]) continue;
+                if (best < 0 || key[e] > key[best]) best = e;
+            }
+            taken[best] = 1;
+            ids[t * k + j] = best;
+            sel[j] = sc[best];
+        }
+        float s = sel[0];
+        for (int j = 1; j < k; ++j) s = s + sel[j];
+        float den = s + 1e-20f;
+        for (int j = 0; j < k; ++j) w[t * k + j] = sel[j] / den * scaling;
+    }
+    free(sc);
+    free(key);
+    free(taken);
 }
 
 /* Stable counting sort of the flat (token-major, slot-minor) expert ids: counts, order, a_idx, inv_pos.

@@ -63,6 +63,12 @@ def test_argument_validation_codes(lib):
     assert L.hmoe_route_topk(P, 8, P, None, 4, 8, 300, 2, 1, 1.0, None, P, P, None) == -2
     assert L.hmoe_route_topk(P + 2, 8, P, None, 4, 8, 4, 2, 1, 1.0, None, P, P, None) == -1
     assert L.hmoe_route_topk(P, 8, P, None, 4, 12, 4, 2, 1, 1.0, None, P, P, None) == -1  # d % 8
+    # sigmoid group router: E % n_group, group size a power of two in [2, 64], enough experts in the kept groups
+    assert L.hmoe_route_sigmoid_group(P, 8, P, None, 4, 8, 128, 8, 6, 2, 2.5, None, P, P, None) == -2
+    assert L.hmoe_route_sigmoid_group(P, 8, P, None, 4, 8, 96, 8, 8, 2, 2.5, None, P, P, None) == -2  # 12 per group
+    assert L.hmoe_route_sigmoid_group(P, 8, P, None, 4, 8, 128, 8, 8, 9, 2.5, None, P, P, None) == -2
+    assert L.hmoe_route_sigmoid_group(P, 8, P, None, 4, 8, 16, 5, 8, 2, 2.5, None, P, P, None) == -2  # 5 > 2 * 2
+    assert L.hmoe_route_sigmoid_group(P, 8, P, None, 0, 8, 128, 8, 8, 2, 2.5, None, P, P, None) == 0
     # dispatch: dtype, workspace, E bounds
     ws = L.hmoe_dispatch_workspace_size(16, 2, 4)
     assert L.hmoe_dispatch(P, 2, None, 0, 16, 2, 4, None, 0, 0, None, P, None, P, P, P, P, None, P, ws, None) == -3

@@ -1,0 +1,99 @@
+"""The BailingMoeV2 block (aurora/hf_pipeline.py:314-370) on the GPU against the oracle: the sigmoid, group-limited
+router bit for bit (ids, weights, scores), the combine with the shared expert's addend, and PoziomkaMoE's forward
+(int8 experts + shared expert) at small shapes and at the real one (E=128, top-8, d=2048, h=320)."""
+import numpy as np
+import pytest
+import torch
+
+from tests.util import assert_close_bf16, bits, f32
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("T,d,E,k,n_group,topk_group", [(1000, 2048, 128, 8, 8, 2), (333, 1536, 256, 8, 8, 4),
+                                                        (200, 520, 64, 6, 4, 2), (100, 256, 32, 4, 4, 4),
+                                                        (77, 1024, 16, 2, 1, 1)])
+def test_route_sigmoid_group(oracle, T, d, E, k, n_group, topk_group):
+    from trenowanie_generatora_obrazkow_amd import ops
+    print(f"sigmoid group router T={T} d={d} E={E} k={k} groups {topk_group}/{n_group}", flush=True)
+    g = torch.Generator().manual_seed(T + E)
+    x = torch.randn(T, d, generator=g).bfloat16()
+    wr = (torch.randn(E, d, generator=g) * 0.02).bfloat16()
+    bias = torch.randn(E, generator=g) * 0.05
+    dev = torch.device("cuda")
+    for b in (None, bias):
+        sc, ids, w = ops.route_sigmoid_group(x.to(dev), wr.to(dev), k, n_group, topk_group,
+                                             expert_bias=None if b is None else b.to(dev), scaling=2.5,
+                                             want_scores=True)
+        _, rids, rw, rsc = oracle.route_sigmoid_group(bits(x), bits(wr), k, n_group, topk_group,
+                                                      None if b is None else b.numpy(), 2.5)
+        np.testing.assert_array_equal(ids.cpu().numpy(), rids)
+        np.testing.assert_array_equal(w.cpu().numpy(), rw)
+        np.testing.assert_array_equal(sc.cpu().numpy(), rsc)
+
+
+def test_combine_add(oracle):
+    from trenowanie_generatora_obrazkow_amd import ops
+    T, k, d = 300, 8, 2048
+    g = torch.Generator().manual_seed(9)
+    y = torch.randn(T * k, d, generator=g).bfloat16()
+    add = torch.randn(T, d, generator=g).bfloat16()
+    out = ops.combine(y.cuda(), T, k, add=add.cuda())
+    s = f32(y).reshape(T, k, d)
+    acc = s[:, 0].copy()
+    for j in range(1, k):
+        acc = (acc + s[:, j]).astype(np.float32)  # fp32 sum in slot order
+    ref = oracle.round_bf16(oracle.round_bf16(acc).astype(np.float32) + f32(add))
+    np.testing.assert_array_equal(f32(out), ref)
+
+
+def _make_block(oracle, d, h, E, k, n_group, topk_group, shared_h, seed):
+    from trenowanie_generatora_obrazkow_amd.poziomka import PoziomkaMoE
+    g = torch.Generator().manual_seed(seed)
+    m = PoziomkaMoE(d, h, E, k, n_group, topk_group, 2.5, shared_h)
+    with torch.no_grad():
+        m.gate.weight.copy_(torch.randn(E, d, generator=g) * 0.02)
+        m.gate.expert_bias.copy_(torch.randn(E, generator=g) * 0.05)
+        for lin in (m.shared_experts.gate_proj, m.shared_experts.up_proj, m.shared_experts.down_proj):
+            lin.weight.copy_(torch.randn(lin.weight.shape, generator=g) * 0.02)
+        for name, shape in (("_wgu", (E, d, 2 * h)), ("_wd", (E, h, d))):
+            q, s = oracle.quant_int8((torch.randn(shape, generator=g) * 0.02).numpy())
+            getattr(m, name).copy_(torch.from_numpy(q))
+            getattr(m, name + "_s").copy_(torch.from_numpy(s).bfloat16())
+    return m.to(torch.bfloat16)  # the trunk runs in bf16: floating parameters and buffers become bf16
+
+
+def _oracle_forward(oracle, m, x, k, n_group, topk_group):
+    """Router, int8 experts and the shared expert from the module's own (bf16) tensors."""
+    sh = m.shared_experts
+    _, ids, w, _ = oracle.route_sigmoid_group(bits(x), bits(m.gate.weight), k, n_group, topk_group,
+                                              f32(m.gate.expert_bias), m.scaling)
+    xf = f32(x)
+    moe = oracle.moe_forward(xf, ids, w, m._wgu.cpu().numpy().astype(np.float32),
+                             m._wd.cpu().numpy().astype(np.float32), wgu_s=f32(m._wgu_s).astype(np.float64),
+                             wd_s=f32(m._wd_s).astype(np.float64))
+    wgu_sh = np.concatenate([f32(sh.gate_proj.weight), f32(sh.up_proj.weight)]).T[None]
+    wd_sh = f32(sh.down_proj.weight).T[None]
+    T = x.shape[0]
+    shared = oracle.moe_forward(xf, np.zeros((T, 1), np.int64), np.ones((T, 1), np.float32), wgu_sh, wd_sh)
+    return ids, oracle.round_bf16(moe["out"].astype(np.float64) + shared["out"].astype(np.float64)), shared["out"]
+
+
+@pytest.mark.parametrize("T,d,h,E,k,n_group,topk_group", [(300, 512, 320, 32, 4, 4, 2),
+                                                          (512, 2048, 320, 128, 8, 8, 2)])
+def test_poziomka_moe_forward(oracle, T, d, h, E, k, n_group, topk_group):
+    from trenowanie_generatora_obrazkow_amd import ops
+    print(f"PoziomkaMoE T={T} d={d} h={h} E={E} k={k} groups {topk_group}/{n_group}", flush=True)
+    m = _make_block(oracle, d, h, E, k, n_group, topk_group, h, seed=T + E)
+    g = torch.Generator().manual_seed(T)
+    x = torch.randn(2, T // 2, d, generator=g).bfloat16()
+    mc = m.cuda()
+    y = mc(x.cuda())
+    assert y.shape == x.shape and y.dtype == torch.bfloat16
+    x2 = x.reshape(T, d)
+    ids, ref, shared_ref = _oracle_forward(oracle, m, x2, k, n_group, topk_group)
+    _, gids, _ = ops.route_sigmoid_group(x2.cuda(), mc.gate.weight, k, n_group, topk_group,
+                                         expert_bias=mc.gate.expert_bias, scaling=2.5)
+    np.testing.assert_array_equal(gids.cpu().numpy(), ids)
+    assert_close_bf16(f32(y).reshape(T, d), ref, "PoziomkaMoE")
+    assert_close_bf16(f32(mc.shared_experts(x.cuda())).reshape(T, d), shared_ref, "shared expert")

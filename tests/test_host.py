@@ -122,3 +122,29 @@ def test_moe_swiglu_module_shapes():
     assert m.logit_bias.dtype == torch.float32 and (m.logit_bias == 0).all()
     with pytest.raises(RuntimeError, match="GPU"):
         m(torch.randn(2, 5, 64))
+
+
+def test_poziomka_module_layout():
+    """PoziomkaMoE keeps the reference's module tree, names, shapes and dtypes (aurora/hf_pipeline.py:314-346), so the
+    reference's state dicts load unchanged; its forward refuses CPU tensors (no CPU path)."""
+    from trenowanie_generatora_obrazkow_amd.poziomka import PoziomkaMLP, PoziomkaMoE
+    d, h, E, sh = 64, 32, 16, 48
+    m = PoziomkaMoE(d, h, E, 4, 4, 2, 2.5, sh)
+    sd = m.state_dict()
+    expect = {"gate.weight": ((E, d), torch.float32), "gate.expert_bias": ((E,), torch.float32),
+              "shared_experts.gate_proj.weight": ((sh, d), torch.float32),
+              "shared_experts.up_proj.weight": ((sh, d), torch.float32),
+              "shared_experts.down_proj.weight": ((d, sh), torch.float32),
+              "_wgu": ((E, d, 2 * h), torch.int8), "_wgu_s": ((E, 2 * h), torch.bfloat16),
+              "_wd": ((E, h, d), torch.int8), "_wd_s": ((E, d), torch.bfloat16)}
+    assert set(sd) == set(expect)
+    for key, (shape, dt) in expect.items():
+        assert tuple(sd[key].shape) == shape and sd[key].dtype == dt, key
+    assert (m.top_k, m.n_group, m.topk_group, m.scaling) == (4, 4, 2, 2.5)
+    m2 = PoziomkaMoE(d, h, E, 4, 4, 2, 2.5, sh)
+    m2.load_state_dict(sd)
+    mb = m.to(torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        mb(torch.zeros(3, d, dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="GPU"):
+        PoziomkaMLP(d, sh).bfloat16()(torch.zeros(2, d, dtype=torch.bfloat16))

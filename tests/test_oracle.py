@@ -463,3 +463,67 @@ def test_bf16_products_exact_in_fp32():
         prod32 = fa[ok] * fb[ok]
     assert ok.sum() > 50000
     np.testing.assert_array_equal(prod32.astype(np.float64), exact[ok])
+
+
+# ------------------------------------------------------------------------------------------- BailingMoeV2 router
+def _torch_sigmoid_group(scores, bias, k, n_group, topk_group, scaling):
+    """The routing steps of aurora/hf_pipeline.py:353-359 run with torch on CPU from given fp32 scores: group values
+    from torch.topk(2), kept groups from torch.topk, experts from torch.topk over the masked routing values."""
+    n, E = scores.shape
+    routing = scores + bias
+    group = routing.view(n, n_group, -1).topk(2, dim=-1)[0].sum(-1)
+    keep = torch.zeros_like(group).scatter_(1, group.topk(topk_group, dim=-1, sorted=False)[1], 1)
+    keep = keep.bool().unsqueeze(-1).expand(n, n_group, E // n_group).reshape(n, -1)
+    idx = routing.masked_fill(~keep, float("-inf")).topk(k, dim=-1)[1]
+    w = scores.gather(1, idx)
+    return idx, w / (w.sum(-1, keepdim=True) + 1e-20) * scaling
+
+
+@pytest.mark.parametrize("E,k,n_group,topk_group", [(128, 8, 8, 2), (64, 6, 4, 2), (256, 8, 8, 4), (32, 4, 4, 4)])
+def test_sigmoid_group_router_vs_torch_steps(oracle, E, k, n_group, topk_group):
+    rng = np.random.default_rng(E + k)
+    T = 300
+    logits = (rng.standard_normal((T, E)) * 2).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.3).astype(np.float32)
+    ids, w, sc = oracle.sigmoid_group_from_logits(logits, k, n_group, topk_group, bias, 2.5)
+    # sigmoid against float64: hexp (<= 1 ulp), the add and the division (0.5 ulp each) -- within 3 ulp of the result
+    ref_sc = 1.0 / (1.0 + np.exp(-logits.astype(np.float64)))
+    assert (np.abs(sc - ref_sc) <= 3 * np.spacing(np.abs(ref_sc).astype(np.float32))).all()
+    ti, tw = _torch_sigmoid_group(torch.from_numpy(sc), torch.from_numpy(bias), k, n_group, topk_group, 2.5)
+    np.testing.assert_array_equal(ids, ti.numpy())
+    # weights: same terms; torch's 8-term sum may associate differently (a few ulp)
+    np.testing.assert_allclose(w, tw.numpy(), rtol=4e-7 * k, atol=0)
+
+
+def test_sigmoid_group_router_brute_force(oracle):
+    """Tiny E: every kept-group subset enumerated; the expert set must be the best k among the best subset."""
+    import itertools
+    rng = np.random.default_rng(5)
+    E, n_group, topk_group, k = 12, 4, 2, 3
+    eg = E // n_group
+    for _ in range(200):
+        logits = rng.standard_normal((1, E)).astype(np.float32) * 3
+        bias = rng.standard_normal(E).astype(np.float32) * 0.2
+        ids, _, sc = oracle.sigmoid_group_from_logits(logits, k, n_group, topk_group, bias, 1.0)
+        r = sc[0].astype(np.float64) + bias
+        gv = [np.sort(r[g * eg:(g + 1) * eg])[-2:].sum() for g in range(n_group)]
+        best = max(itertools.combinations(range(n_group), topk_group), key=lambda s: sum(gv[g] for g in s))
+        allowed = [e for e in range(E) if e // eg in best]
+        expect = sorted(allowed, key=lambda e: -r[e])[:k]
+        assert list(ids[0]) == expect
+
+
+def test_sigmoid_group_router_ties(oracle):
+    """Equal group values keep the lower groups; equal routing values pick the lower experts; a group's value counts
+    a repeated maximum twice."""
+    E, n_group, topk_group, k = 8, 4, 2, 2
+    logits = np.zeros((1, E), dtype=np.float32)  # every score 0.5
+    ids, w, _ = oracle.sigmoid_group_from_logits(logits, k, n_group, topk_group, None, 1.0)
+    assert list(ids[0]) == [0, 1] and np.allclose(w, 0.5)
+    bias = np.zeros(E, np.float32)
+    bias[[2, 3]] = 0.25      # group 1: 0.75 + 0.75
+    bias[6] = 0.5            # group 3: 1.0 + 0.5 -- same value as group 1
+    ids, _, _ = oracle.sigmoid_group_from_logits(logits, k, n_group, 1, bias, 1.0)
+    assert list(ids[0]) == [2, 3]  # ties between groups 1 and 3 go to group 1
+    ids, _, _ = oracle.sigmoid_group_from_logits(logits, 3, n_group, 2, bias, 1.0)
+    assert list(ids[0]) == [6, 2, 3]

@@ -27,6 +27,8 @@ SIGNATURES = {
     "hmoe_abi_version": (_I32, []),
     "hmoe_error_string": (ctypes.c_char_p, [_I32]),
     "hmoe_route_topk": (_I32, [_P, _I64, _P, _P, _I64, _I64, _I32, _I32, _I32, _F32, _P, _P, _P, _P]),
+    "hmoe_route_sigmoid_group": (_I32, [_P, _I64, _P, _P, _I64, _I64, _I32, _I32, _I32, _I32, _F32, _P, _P, _P,
+                                        _P]),
     "hmoe_dispatch_workspace_size": (_SZ, [_I64, _I32, _I32]),
     "hmoe_dispatch": (_I32, [_P, _I32, _P, _I32, _I64, _I32, _I32, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P,
                              _P, _SZ, _P]),
@@ -38,6 +40,7 @@ SIGNATURES = {
     "hmoe_gate_up_swiglu_i8": (_I32, [_P, _I64, _P, _P, _P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _P, _P]),
     "hmoe_down_scatter_i8": (_I32, [_P, _P, _P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P, _P]),
     "hmoe_combine": (_I32, [_P, _I64, _I32, _I64, _P, _P]),
+    "hmoe_combine_add": (_I32, [_P, _I64, _I32, _I64, _P, _P, _P]),
     "hmoe_combine_bwd": (_I32, [_P, _P, _P, _P, _P, _I64, _I32, _I64, _P, _P, _P]),
     "hmoe_down_dgrad_swiglu": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P]),
     "hmoe_gate_up_dgrad": (_I32, [_P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P, _I32, _P]),

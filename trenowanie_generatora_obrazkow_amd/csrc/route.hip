@@ -88,12 +88,21 @@ __device__ __forceinline__ void wave_argmax(float& bv, int& be) {
 // per lane instead of reducing every expert separately; each value still meets exactly the partner the plain
 // butterfly would give it (fp addition is commutative), so the sums are bit-identical.  After log2(G) steps lane l
 // holds expert l >> (6 - log2 G) of the group, and the remaining steps are the plain butterfly.
-template <int NCH, int G>
+//
+// SIG = false: softmax router (bias added to the logits, selection on the logits, weights = softmax probabilities).
+// SIG = true: the sigmoid, group-limited router of BailingMoeV2 (aurora/hf_pipeline.py:352-359): score =
+// 1 / (1 + exp(-logit)); routing = score + bias (selection only); experts in n_group consecutive groups of
+// E / n_group, a group's value is the sum of its two largest routing values, the topk_group best groups are kept
+// (ties to the lower group) and the k experts with the largest routing values among them selected (ties to the
+// lower expert); weights = the selected scores, renormalised (w / (sum + 1e-20)) and scaled.  `logits` then
+// receives the scores.
+template <int NCH, int G, bool SIG>
 __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                          const uint16_t* __restrict__ wr,
                                                          const float* __restrict__ bias, int T, int d, int E, int k,
                                                          int renorm, float scaling, float* __restrict__ logits,
-                                                         int32_t* __restrict__ ids, float* __restrict__ wout) {
+                                                         int32_t* __restrict__ ids, float* __restrict__ wout,
+                                                         int n_group, int topk_group) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
   const int nwaves = blockDim.x >> 6;
@@ -139,7 +148,7 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restr
       if constexpr (H < 5) v = bfly_add<2>(v);
       if constexpr (H < 6) v = bfly_add<1>(v);
       const int my_e = g0 + (lane >> (6 - H));
-      if (bias && my_e < E) v = __fadd_rn(v, bias[my_e]);
+      if (!SIG && bias && my_e < E) v = __fadd_rn(v, bias[my_e]);
       // lane l collects expert i*64 + l from the lanes of its group slot
 #pragma unroll
       for (int i = 0; i < kRouteEPL; ++i) {
@@ -150,27 +159,87 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restr
         }
       }
     }
-    // softmax over the E logits held lane-wise (lane l: experts l, l+64, ...)
-    float m = -__builtin_inff();
-#pragma unroll
-    for (int i = 0; i < kRouteEPL; ++i)
-      if (i * 64 + lane < E) m = fmaxf(m, lg[i]);
-    m = wave_max_butterfly(m);
-    float ex[kRouteEPL];
-    float a = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kRouteEPL; ++i) {
-      ex[i] = 0.0f;
-      if (i * 64 + lane < E) {
-        ex[i] = hexp(__fsub_rn(lg[i], m));
-        a = __fadd_rn(a, ex[i]);
-      }
-    }
-    const float S = wave_sum_butterfly(a);
-    if (logits) {
+    // key[i]: the selection key of expert i*64 + lane; num[i]: the value its weight is made of (divided by S)
+    float key[kRouteEPL], num[kRouteEPL];
+    float S = 1.0f;
+    if constexpr (!SIG) {
+      // softmax over the E logits held lane-wise (lane l: experts l, l+64, ...)
+      float m = -__builtin_inff();
 #pragma unroll
       for (int i = 0; i < kRouteEPL; ++i)
-        if (i * 64 + lane < E) logits[(int64_t)t * E + i * 64 + lane] = lg[i];
+        if (i * 64 + lane < E) m = fmaxf(m, lg[i]);
+      m = wave_max_butterfly(m);
+      float a = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kRouteEPL; ++i) {
+        num[i] = 0.0f;
+        key[i] = lg[i];
+        if (i * 64 + lane < E) {
+          num[i] = hexp(__fsub_rn(lg[i], m));
+          a = __fadd_rn(a, num[i]);
+        }
+      }
+      S = wave_sum_butterfly(a);
+      if (logits) {
+#pragma unroll
+        for (int i = 0; i < kRouteEPL; ++i)
+          if (i * 64 + lane < E) logits[(int64_t)t * E + i * 64 + lane] = lg[i];
+      }
+    } else {
+      float rt[kRouteEPL];
+#pragma unroll
+      for (int i = 0; i < kRouteEPL; ++i) {
+        const int e = i * 64 + lane;
+        num[i] = 0.0f;
+        rt[i] = -__builtin_inff();
+        if (e < E) {
+          num[i] = __fdiv_rn(1.0f, __fadd_rn(1.0f, hexp(-lg[i])));
+          rt[i] = bias ? __fadd_rn(num[i], bias[e]) : num[i];
+          if (logits) logits[(int64_t)t * E + e] = num[i];
+        }
+      }
+      bool keep[kRouteEPL];
+#pragma unroll
+      for (int i = 0; i < kRouteEPL; ++i) keep[i] = true;
+      if (topk_group < n_group) {
+        const int eg = E / n_group;  // a power of two in [2, 64] (checked on the host): groups never straddle lanes'
+                                     // 64-expert slots, and the xor partners below stay inside the group
+        float gs[kRouteEPL];
+#pragma unroll
+        for (int i = 0; i < kRouteEPL; ++i) {
+          float m1 = rt[i], m2 = -__builtin_inff();  // the two largest values of the group (with multiplicity)
+#pragma unroll
+          for (int sft = 1; sft < 64; sft <<= 1) {
+            if (sft < eg) {
+              const float o1 = __shfl_xor(m1, sft, 64), o2 = __shfl_xor(m2, sft, 64);
+              const float n2 = fmaxf(fminf(m1, o1), fmaxf(m2, o2));
+              m1 = fmaxf(m1, o1);
+              m2 = n2;
+            }
+          }
+          gs[i] = __fadd_rn(m1, m2);
+        }
+        bool gsel[kRouteEPL];
+#pragma unroll
+        for (int i = 0; i < kRouteEPL; ++i) gsel[i] = false;
+        for (int j = 0; j < topk_group; ++j) {
+          float bv = 0.0f;
+          int be = 0x7fffffff;
+#pragma unroll
+          for (int i = 0; i < kRouteEPL; ++i) {
+            const int e = i * 64 + lane;
+            if (e < E && !gsel[i]) argmax_take(bv, be, gs[i], e / eg);
+          }
+          wave_argmax(bv, be);
+#pragma unroll
+          for (int i = 0; i < kRouteEPL; ++i)
+            if ((i * 64 + lane) / eg == be) gsel[i] = true;
+        }
+#pragma unroll
+        for (int i = 0; i < kRouteEPL; ++i) keep[i] = gsel[i];
+      }
+#pragma unroll
+      for (int i = 0; i < kRouteEPL; ++i) key[i] = keep[i] ? rt[i] : -__builtin_inff();
     }
     bool taken[kRouteEPL];
 #pragma unroll
@@ -187,21 +256,21 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restr
 #pragma unroll
         for (int i = 0; i < kRouteEPL; ++i) {
           int e = i * 64 + lane;
-          if (e < E && !taken[i] && (be == 0x7fffffff || lg[i] > bv)) {
-            bv = lg[i];
+          if (e < E && !taken[i] && (be == 0x7fffffff || key[i] > bv)) {
+            bv = key[i];
             be = e;
           }
         }
         wave_argmax(bv, be);
-        float myex = 0.0f;
+        float mynum = 0.0f;
 #pragma unroll
         for (int i = 0; i < kRouteEPL; ++i)
           if (be == i * 64 + lane) {
             taken[i] = true;
-            myex = ex[i];
+            mynum = num[i];
           }
-        float pex = __shfl(myex, be & 63, 64);
-        selp[j] = __fdiv_rn(pex, S);
+        const float pnum = __shfl(mynum, be & 63, 64);
+        selp[j] = SIG ? pnum : __fdiv_rn(pnum, S);
         sele[j] = be;
       }
     }
@@ -393,8 +462,10 @@ __global__ __launch_bounds__(256) void make_schedule_kernel(const void* __restri
 // ---------------------------------------------------------------------------------------------------------------
 // Combine (forward) and its backward.
 // ---------------------------------------------------------------------------------------------------------------
+// out[t] = bf16(sum_j y[t*k + j]) (fp32 sum in slot order), or with `add`: bf16(that + add[t]) (bf16 + bf16
+// computed in fp32 and rounded once, as torch adds two bf16 tensors)
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ y, int64_t T, int k, int64_t d,
-                                                      uint16_t* __restrict__ out) {
+                                                      const uint16_t* __restrict__ add, uint16_t* __restrict__ out) {
   const int64_t nvec = d / 8;
   const int64_t total = T * nvec;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
@@ -424,6 +495,15 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
     o.y = pack_bf2(s[2], s[3]);
     o.z = pack_bf2(s[4], s[5]);
     o.w = pack_bf2(s[6], s[7]);
+    if (add) {
+      const uint4 a = reinterpret_cast<const uint4*>(add + t * d)[c];
+      const uint32_t av[4] = {a.x, a.y, a.z, a.w};
+      uint32_t ov[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        ov[q] = pack_bf2(__fadd_rn(bf_lo(ov[q]), bf_lo(av[q])), __fadd_rn(bf_hi(ov[q]), bf_hi(av[q])));
+      o = make_uint4(ov[0], ov[1], ov[2], ov[3]);
+    }
     reinterpret_cast<uint4*>(out + t * d)[c] = o;
   }
 }
@@ -761,36 +841,10 @@ static inline int grid_for(int64_t work, int per_block, int cap = 8192) {
 
 static inline bool al16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-}  // namespace hmoe
-
-using namespace hmoe;
-
-extern "C" {
-
-int hmoe_abi_version(void) { return HMOE_ABI_VERSION; }
-
-const char* hmoe_error_string(int code) {
-  switch (code) {
-    case HMOE_OK: return "ok";
-    case HMOE_ERR_ARG: return "invalid argument (null pointer, negative size or misaligned pointer / stride)";
-    case HMOE_ERR_SHAPE: return "unsupported shape";
-    case HMOE_ERR_DTYPE: return "unsupported element type";
-    case HMOE_ERR_LAUNCH: return "kernel launch failed";
-    case HMOE_ERR_WORKSPACE: return "workspace missing or too small";
-    case HMOE_ERR_DEVICE: return "device query failed";
-    default: return "unknown error";
-  }
-}
-
-int hmoe_route_topk(const void* x, int64_t ldx, const void* wr, const float* bias, int64_t T, int64_t d, int E,
-                    int k, int renorm, float scaling, float* logits, int32_t* topk_ids, float* topk_w,
-                    hmoe_stream_t stream) {
-  if (T < 0 || d <= 0 || E <= 0 || k <= 0) return HMOE_ERR_ARG;
-  if (T == 0) return HMOE_OK;
-  if (!x || !wr || !topk_ids || !topk_w) return HMOE_ERR_ARG;
-  if (E > kRouteMaxE || k > kMaxK || k > E || T > INT32_MAX) return HMOE_ERR_SHAPE;
-  if (d % 8 || ldx % 8 || ldx < d || !al16(x) || !al16(wr)) return HMOE_ERR_ARG;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+template <bool SIG>
+static int route_launch(const void* x, int64_t ldx, const void* wr, const float* bias, int64_t T, int64_t d, int E,
+                        int k, int renorm, float scaling, float* logits, int32_t* topk_ids, float* topk_w,
+                        int n_group, int topk_group, hipStream_t s) {
   const int grid = grid_for(T, 4, 4096);
   const int nch = (int)((d + 511) / 512);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
@@ -798,9 +852,9 @@ int hmoe_route_topk(const void* x, int64_t ldx, const void* wr, const float* bia
   // experts per transposed-butterfly group; rows longer than 2048 hold more of x in registers, so smaller groups
   int group = E <= 8 ? 8 : E <= 16 ? 16 : E <= 32 ? 32 : 64;
   if (nch > 4 && group > 16) group = 16;
-#define HMOE_ROUTE(NC, GR)                                                                                           \
-  hipLaunchKernelGGL((route_topk_kernel<NC, GR>), dim3(grid), dim3(256), 0, s, xp, ldx, wp, bias, (int)T, (int)d, E, \
-                     k, renorm, scaling, logits, topk_ids, topk_w)
+#define HMOE_ROUTE(NC, GR)                                                                                        \
+  hipLaunchKernelGGL((route_topk_kernel<NC, GR, SIG>), dim3(grid), dim3(256), 0, s, xp, ldx, wp, bias, (int)T,    \
+                     (int)d, E, k, renorm, scaling, logits, topk_ids, topk_w, n_group, topk_group)
 #define HMOE_ROUTE_G(NC)        \
   if (group == 8)               \
     HMOE_ROUTE(NC, 8);          \
@@ -835,6 +889,61 @@ int hmoe_route_topk(const void* x, int64_t ldx, const void* wr, const float* bia
 #undef HMOE_ROUTE
   HMOE_CHECK_LAUNCH();
   return HMOE_OK;
+}
+
+static int route_check(const void* x, int64_t ldx, const void* wr, int64_t T, int64_t d, int E, int k,
+                       const int32_t* topk_ids, const float* topk_w) {
+  if (T < 0 || d <= 0 || E <= 0 || k <= 0) return HMOE_ERR_ARG;
+  if (T == 0) return HMOE_OK;
+  if (!x || !wr || !topk_ids || !topk_w) return HMOE_ERR_ARG;
+  if (E > kRouteMaxE || k > kMaxK || k > E || T > INT32_MAX) return HMOE_ERR_SHAPE;
+  if (d % 8 || ldx % 8 || ldx < d || !al16(x) || !al16(wr)) return HMOE_ERR_ARG;
+  return HMOE_OK;
+}
+
+}  // namespace hmoe
+
+using namespace hmoe;
+
+extern "C" {
+
+int hmoe_abi_version(void) { return HMOE_ABI_VERSION; }
+
+const char* hmoe_error_string(int code) {
+  switch (code) {
+    case HMOE_OK: return "ok";
+    case HMOE_ERR_ARG: return "invalid argument (null pointer, negative size or misaligned pointer / stride)";
+    case HMOE_ERR_SHAPE: return "unsupported shape";
+    case HMOE_ERR_DTYPE: return "unsupported element type";
+    case HMOE_ERR_LAUNCH: return "kernel launch failed";
+    case HMOE_ERR_WORKSPACE: return "workspace missing or too small";
+    case HMOE_ERR_DEVICE: return "device query failed";
+    default: return "unknown error";
+  }
+}
+
+int hmoe_route_topk(const void* x, int64_t ldx, const void* wr, const float* bias, int64_t T, int64_t d, int E,
+                    int k, int renorm, float scaling, float* logits, int32_t* topk_ids, float* topk_w,
+                    hmoe_stream_t stream) {
+  const int rc = route_check(x, ldx, wr, T, d, E, k, topk_ids, topk_w);
+  if (rc || T == 0) return rc;
+  return route_launch<false>(x, ldx, wr, bias, T, d, E, k, renorm, scaling, logits, topk_ids, topk_w, 1, 1,
+                             reinterpret_cast<hipStream_t>(stream));
+}
+
+int hmoe_route_sigmoid_group(const void* x, int64_t ldx, const void* wr, const float* expert_bias, int64_t T,
+                             int64_t d, int E, int k, int n_group, int topk_group, float scaling, float* scores,
+                             int32_t* topk_ids, float* topk_w, hmoe_stream_t stream) {
+  const int rc = route_check(x, ldx, wr, T, d, E, k, topk_ids, topk_w);
+  if (rc || T == 0) return rc;
+  if (n_group < 1 || topk_group < 1 || topk_group > n_group || E % n_group) return HMOE_ERR_SHAPE;
+  if (topk_group < n_group) {
+    const int eg = E / n_group;  // experts per group: a power of two in [2, 64]
+    if (eg < 2 || eg > 64 || (eg & (eg - 1))) return HMOE_ERR_SHAPE;
+    if (k > topk_group * eg) return HMOE_ERR_SHAPE;  // the kept groups must hold k experts
+  }
+  return route_launch<true>(x, ldx, wr, expert_bias, T, d, E, k, 1, scaling, scores, topk_ids, topk_w, n_group,
+                            topk_group, reinterpret_cast<hipStream_t>(stream));
 }
 
 size_t hmoe_dispatch_workspace_size(int64_t T, int k, int E) {
@@ -905,7 +1014,20 @@ int hmoe_combine(const void* y, int64_t T, int k, int64_t d, void* out, hmoe_str
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int64_t work = T * (d / 8);
   hipLaunchKernelGGL(combine_kernel, dim3(grid_for(work, 256, 65536)), dim3(256), 0, s,
-                     static_cast<const uint16_t*>(y), T, k, d, static_cast<uint16_t*>(out));
+                     static_cast<const uint16_t*>(y), T, k, d, nullptr, static_cast<uint16_t*>(out));
+  HMOE_CHECK_LAUNCH();
+  return HMOE_OK;
+}
+
+int hmoe_combine_add(const void* y, int64_t T, int k, int64_t d, const void* add, void* out, hmoe_stream_t stream) {
+  if (T < 0 || k <= 0 || d <= 0) return HMOE_ERR_ARG;
+  if (T == 0) return HMOE_OK;
+  if (!y || !add || !out || d % 8 || !al16(y) || !al16(add) || !al16(out)) return HMOE_ERR_ARG;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t work = T * (d / 8);
+  hipLaunchKernelGGL(combine_kernel, dim3(grid_for(work, 256, 65536)), dim3(256), 0, s,
+                     static_cast<const uint16_t*>(y), T, k, d, static_cast<const uint16_t*>(add),
+                     static_cast<uint16_t*>(out));
   HMOE_CHECK_LAUNCH();
   return HMOE_OK;
 }

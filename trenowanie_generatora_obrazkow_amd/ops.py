@@ -64,6 +64,29 @@ def route_topk(x: torch.Tensor, wr: torch.Tensor, k: int, bias=None, renorm=True
     return logits, ids, w
 
 
+def route_sigmoid_group(x: torch.Tensor, wr: torch.Tensor, k: int, n_group: int, topk_group: int, expert_bias=None,
+                        scaling=1.0, want_scores=False):
+    """BailingMoeV2 sigmoid, group-limited router -> (scores (T, E) fp32 or None, topk_ids (T, k) int32,
+    topk_w (T, k) fp32)."""
+    T, d = x.shape
+    E = wr.shape[0]
+    if x.dtype != torch.bfloat16 or wr.dtype != torch.bfloat16:
+        raise TypeError("router expects bf16 x and weight")
+    if x.stride(1) != 1:
+        raise ValueError("x rows must be contiguous")
+    wr = _contig(wr, "router weight")
+    if expert_bias is not None:
+        expert_bias = _contig(expert_bias.to(torch.float32), "expert bias")
+    s = _dev_stream(x)
+    scores = torch.empty(T, E, device=x.device, dtype=torch.float32) if want_scores else None
+    ids = torch.empty(T, k, device=x.device, dtype=torch.int32)
+    w = torch.empty(T, k, device=x.device, dtype=torch.float32)
+    with _Probe("route_topk"):
+        L.call("hmoe_route_sigmoid_group", L.ptr(x), x.stride(0), L.ptr(wr), L.ptr(expert_bias), T, d, E, k, n_group,
+               topk_group, float(scaling), L.ptr(scores), L.ptr(ids), L.ptr(w), s)
+    return scores, ids, w
+
+
 @dataclass
 class Dispatch:
     counts: torch.Tensor  # (E,) int32
@@ -218,11 +241,18 @@ def down_scatter(act, wd, counts, M, w_sorted, y_idx, keep_yhat=False, wd_s=None
     return y, yhat
 
 
-def combine(y, T, k):
+def combine(y, T, k, add=None):
+    """out[t] = bf16(sum_j y[t*k + j]) (+ add[t], rounded once more: bf16 + bf16)."""
     d = y.shape[1]
     out = torch.empty(T, d, device=y.device, dtype=y.dtype)
     with _Probe("combine"):
-        L.call("hmoe_combine", L.ptr(_contig(y, "y")), T, k, d, L.ptr(out), _dev_stream(y))
+        if add is None:
+            L.call("hmoe_combine", L.ptr(_contig(y, "y")), T, k, d, L.ptr(out), _dev_stream(y))
+        else:
+            if add.shape != (T, d) or add.dtype != torch.bfloat16:
+                raise ValueError(f"add must be bf16 of shape {(T, d)}")
+            L.call("hmoe_combine_add", L.ptr(_contig(y, "y")), T, k, d, L.ptr(_contig(add, "add")), L.ptr(out),
+                   _dev_stream(y))
     return out
 
 

@@ -1,0 +1,138 @@
+"""Drop-in for the reference's BailingMoeV2 MoE block (cpral/Poziomka-Baza), aurora/hf_pipeline.py:314-370:
+`PoziomkaMLP`, `PoziomkaGate` and `PoziomkaMoE` with the same constructor arguments, module tree, parameter and buffer
+names, shapes and dtypes, so a state dict written for the reference classes loads unchanged (export.py:62-72 stores
+the experts as int8 with bf16 per-column scales, exactly these buffers).
+
+Forward, inference only (the reference block is frozen), served by the hmoe kernels:
+
+  1. router (`hmoe_route_sigmoid_group`): fp32 logits, sigmoid scores, expert bias for selection, group-limited top-k
+     (best `topk_group` of `n_group` groups by the sum of their two largest routing values), weights = the selected
+     scores renormalised and scaled (aurora/hf_pipeline.py:352-359);
+  2. stable counting sort of the routed rows (`hmoe_dispatch`), the routing weight rounded to bf16 (:361);
+  3. gate/up grouped GEMM over the int8 experts with the SwiGLU in its epilogue, scale after the fp32 sum, one
+     rounding (:365-367); down grouped GEMM, per-column scale, routing weight, one rounding, rows scattered back to
+     (token, slot) order (:368-369);
+  4. the shared expert (a dense SwiGLU MLP, :342 / :322) as the same two GEMMs over one "expert" holding every token;
+  5. combine: the k slots summed in fp32, rounded, plus the shared expert's output (:369-370).
+
+The reference adds the k slot outputs with `index_add_` in expert order; here they are summed in slot order (same
+terms, fp32 accumulation; the bf16 results can differ in the last place).  There is no CPU path: tensors must live
+on a ROCm GPU.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from . import ops
+
+
+def _bf16_exact(w: torch.Tensor, name: str) -> torch.Tensor:
+    """The hmoe kernels read bf16 weights; a wider weight must hold bf16 values (the reference's exports do)."""
+    if w.dtype == torch.bfloat16:
+        return w
+    wb = w.to(torch.bfloat16)
+    if not torch.equal(wb.to(w.dtype), w):
+        raise TypeError(f"{name}: the hmoe kernels take bf16 weights; this {w.dtype} weight is not bf16-exact")
+    return wb
+
+
+class _StackedMLP:
+    """A dense SwiGLU MLP run as a one-expert grouped GEMM pair: [gate | up] stacked (1, d, 2h), down (1, h, d) --
+    the layout fuse_moe gives the routed experts (aurora/hf_compat.py:154-155).  Rebuilt when a weight changes."""
+
+    def __init__(self):
+        self.key = None
+        self.wgu = self.wd = None
+
+    def get(self, mlp: "PoziomkaMLP"):
+        ws = (mlp.gate_proj.weight, mlp.up_proj.weight, mlp.down_proj.weight)
+        key = tuple((w.data_ptr(), w._version, w.device, w.dtype) for w in ws)
+        if key != self.key:
+            g, u, dn = (_bf16_exact(w.detach(), n) for w, n in zip(ws, ("gate_proj", "up_proj", "down_proj")))
+            self.wgu = torch.cat([g, u]).t().contiguous().unsqueeze(0)
+            self.wd = dn.t().contiguous().unsqueeze(0)
+            self.key = key
+        return self.wgu, self.wd
+
+
+def _dense_swiglu(x2: torch.Tensor, wgu: torch.Tensor, wd: torch.Tensor) -> torch.Tensor:
+    """bf16(bf16(silu(bf16(x Wg))) * bf16(x Wu)) Wd rounded to bf16 -- F.linear / F.silu in bf16 (aurora/
+    hf_pipeline.py:322) -- for x2 (T, d) bf16."""
+    T = x2.shape[0]
+    one = torch.full((1,), T, dtype=torch.int32, device=x2.device)  # a fill kernel: no host-device copy
+    act, _ = ops.gate_up_swiglu(x2, wgu, one, T)
+    y, _ = ops.down_scatter(act, wd, one, T, None, None)
+    return y
+
+
+class PoziomkaMLP(nn.Module):
+    """aurora/hf_pipeline.py:314-322: down(silu(gate(x)) * up(x)), bias-free, bf16."""
+
+    def __init__(self, d, hidden):
+        super().__init__()
+        self.gate_proj = nn.Linear(d, hidden, bias=False)
+        self.up_proj = nn.Linear(d, hidden, bias=False)
+        self.down_proj = nn.Linear(hidden, d, bias=False)
+        self._stack = _StackedMLP()
+
+    @torch.no_grad()
+    def forward(self, x):
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1]).contiguous()
+        if x2.dtype != torch.bfloat16:
+            raise TypeError(f"hmoe PoziomkaMLP runs bf16 activations (got {x2.dtype})")
+        wgu, wd = self._stack.get(self)
+        return _dense_swiglu(x2, wgu, wd).view(shape)
+
+
+class PoziomkaGate(nn.Module):
+    """aurora/hf_pipeline.py:325-329: router weight (E, d) and the selection-only expert bias (E,)."""
+
+    def __init__(self, d, experts):
+        super().__init__()
+        self.weight = nn.Parameter(torch.zeros(experts, d))
+        self.register_buffer("expert_bias", torch.zeros(experts))
+
+
+class PoziomkaMoE(nn.Module):
+    """aurora/hf_pipeline.py:332-370: BailingMoeV2 sparse MoE with int8 experts and one shared expert, inference
+    only.  Buffers as the reference: _wgu (E, d, 2h) int8 = [gate | up], _wgu_s (E, 2h) bf16, _wd (E, h, d) int8,
+    _wd_s (E, d) bf16 (bf16 expert stacks with the scales set to None are accepted too)."""
+
+    def __init__(self, d, hidden, experts, top_k, n_group, topk_group, scaling, shared_hidden):
+        super().__init__()
+        self.top_k, self.n_group, self.topk_group, self.scaling = top_k, n_group, topk_group, scaling
+        self.gate = PoziomkaGate(d, experts)
+        self.shared_experts = PoziomkaMLP(d, shared_hidden)
+        self.register_buffer("_wgu", torch.zeros(experts, d, 2 * hidden, dtype=torch.int8))
+        self.register_buffer("_wgu_s", torch.zeros(experts, 2 * hidden, dtype=torch.bfloat16))
+        self.register_buffer("_wd", torch.zeros(experts, hidden, d, dtype=torch.int8))
+        self.register_buffer("_wd_s", torch.zeros(experts, d, dtype=torch.bfloat16))
+        self._gate_key = None
+        self._gate_w = None
+
+    def _gate_weight(self):
+        w = self.gate.weight
+        key = (w.data_ptr(), w._version, w.device, w.dtype)
+        if key != self._gate_key:
+            self._gate_w = _bf16_exact(w.detach(), "gate.weight").contiguous()
+            self._gate_key = key
+        return self._gate_w
+
+    @torch.no_grad()
+    def forward(self, x):
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1]).contiguous()
+        if x2.dtype != torch.bfloat16:
+            raise TypeError(f"hmoe PoziomkaMoE runs bf16 activations (got {x2.dtype})")
+        T, k, E = x2.shape[0], self.top_k, self._wgu.shape[0]
+        _, ids, w = ops.route_sigmoid_group(x2, self._gate_weight(), k, self.n_group, self.topk_group,
+                                            expert_bias=self.gate.expert_bias, scaling=self.scaling)
+        disp = ops.dispatch(ids, E, topk_w=w, want_inv=False)
+        M = T * k
+        act, _ = ops.gate_up_swiglu(x2, self._wgu, disp.counts, M, a_idx=disp.a_idx, wgu_s=self._wgu_s)
+        y, _ = ops.down_scatter(act, self._wd, disp.counts, M, disp.w_sorted, disp.order, wd_s=self._wd_s)
+        wgu_sh, wd_sh = self.shared_experts._stack.get(self.shared_experts)
+        shared = _dense_swiglu(x2, wgu_sh, wd_sh)
+        return ops.combine(y, T, k, add=shared).view(shape)
