@@ -5,6 +5,8 @@ A step is one pass of the layer over one batch of seeded synthetic tokens, input
   c3            forward only at the same shape
   c4            forward only, Zipf(1.2)-biased router logits, 2 experts never routed
   c2            forward only, 2048 tokens, d=1024, 8 experts, top-2, h=2048
+  bailing       forward of the BailingMoeV2 block at its real shape (PoziomkaMoE: 8192 tokens, d=2048, 128 int8
+                experts, sigmoid group-limited top-8 of 8 groups keeping 2, h=320, one shared expert h=320)
 value = algorithmic grouped-GEMM TFLOP/s of the layer step (routed rows only: 6*M*d*h forward, 18*M*d*h forward +
 backward) / measured step time; ms_per_step is the layer time.  One JSON line is printed.
 """
@@ -37,12 +39,20 @@ WORKLOADS = {
     "c5": dict(T=16384, d=1536, E=16, k=2, h=4096, backward=True, zipf=False,
                desc="C5: MoE layer training step (forward + backward) at the C3 shape: 16384 tokens, d_model=1536, "
                     "16 experts, top-2, SwiGLU hidden=4096"),
+    "bailing": dict(T=8192, d=2048, E=128, k=8, h=320, backward=False, zipf=False, poziomka=True, shared_h=320,
+                    n_group=8, topk_group=2, scaling=2.5,
+                    desc="BailingMoeV2 block forward (PoziomkaMoE, aurora/hf_pipeline.py:332-370): 8192 tokens, "
+                         "d_model=2048, 128 int8 experts, sigmoid router with expert bias, top-8 within the best 2 "
+                         "of 8 groups, SwiGLU hidden=320, one shared expert hidden=320"),
 }
 
 
 def gemm_flops(w):
     M = w["T"] * w["k"]
-    return (18 if w["backward"] else 6) * M * w["d"] * w["h"]
+    f = (18 if w["backward"] else 6) * M * w["d"] * w["h"]
+    if w.get("poziomka"):
+        f += 6 * w["T"] * w["d"] * w["shared_h"]  # the shared expert: every token
+    return f
 
 
 def zipf_bias(E, seed=0, s=1.2, n_empty=2):
@@ -126,6 +136,110 @@ def run_gpu(w, steps, warmup, probe_kernel="gate_up_swiglu"):
     return ms, statistics.mean(dom), kern
 
 
+def _poziomka_block(w, g):
+    """PoziomkaMoE with seeded N(0, 0.02) weights (experts quantised to int8 with per-column scales), bf16, on GPU."""
+    import torch
+
+    from trenowanie_generatora_obrazkow_amd.hf_compat import _quant_int8
+    from trenowanie_generatora_obrazkow_amd.poziomka import PoziomkaMoE
+    d, E, h, sh = w["d"], w["E"], w["h"], w["shared_h"]
+    m = PoziomkaMoE(d, h, E, w["k"], w["n_group"], w["topk_group"], w["scaling"], sh)
+    with torch.no_grad():
+        m.gate.weight.copy_(torch.randn(E, d, generator=g) * 0.02)
+        m.gate.expert_bias.copy_(torch.randn(E, generator=g) * 0.01)
+        for lin in (m.shared_experts.gate_proj, m.shared_experts.up_proj, m.shared_experts.down_proj):
+            lin.weight.copy_(torch.randn(lin.weight.shape, generator=g) * 0.02)
+        for name, shape in (("_wgu", (E, d, 2 * h)), ("_wd", (E, h, d))):
+            q, s = _quant_int8(torch.randn(shape, generator=g) * 0.02)
+            getattr(m, name).copy_(q)
+            getattr(m, name + "_s").copy_(s)
+    return m.to(torch.bfloat16)
+
+
+def run_gpu_poziomka(w, steps, warmup):
+    """Forward of the BailingMoeV2 block; the dominant kernel is the routed gate/up GEMM (int8 experts), the first
+    of the two gate/up launches of a step (the second is the shared expert)."""
+    import torch
+
+    from trenowanie_generatora_obrazkow_amd import ops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    g = torch.Generator().manual_seed(0)
+    m = _poziomka_block(w, g).to(dev)
+    x = torch.randn(w["T"], w["d"], generator=g).bfloat16().to(dev)
+
+    def step():
+        m(x)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ops.probe = {"gate_up_swiglu": []}
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    dom = [a.elapsed_time(b) for a, b in ops.probe["gate_up_swiglu"][0::2]]
+    ops.probe = None
+    ms = (t1 - t0) * 1e3 / steps
+    names = ["route_topk", "dispatch", "gate_up_swiglu", "down_scatter", "combine"]
+    ops.probe = {n: [] for n in names}
+    nb = max(3, min(steps, 10))
+    for _ in range(nb):
+        step()
+    torch.cuda.synchronize()
+    kern = {}
+    for n in names:
+        ts = [a.elapsed_time(b) * 1e3 for a, b in ops.probe[n]]
+        if n in ("gate_up_swiglu", "down_scatter"):  # routed experts, then the shared expert
+            kern[n] = statistics.median(ts[0::2])
+            kern[n + "_shared"] = statistics.median(ts[1::2])
+        else:
+            kern[n] = statistics.median(ts)
+    ops.probe = None
+    return ms, statistics.mean(dom), kern
+
+
+def cpu_baseline_poziomka(w, budget_s=15.0):
+    """The reference block's own forward (oracle/cpu_path.py: aurora/hf_pipeline.py:348-370) on CPU, on a bounded
+    sample of the same workload: the full d, E, k, h with fewer tokens."""
+    import torch
+
+    from oracle import cpu_path
+
+    threads = torch.get_num_threads()
+    T = 512
+    g = torch.Generator().manual_seed(0)
+    m = _poziomka_block(w, g)
+    x = torch.randn(T, w["d"], generator=g).bfloat16()
+    sh = m.shared_experts
+    args = (x, m.gate.weight, m.gate.expert_bias, m._wgu, m._wgu_s, m._wd, m._wd_s, sh.gate_proj.weight,
+            sh.up_proj.weight, sh.down_proj.weight, w["k"], w["n_group"], w["topk_group"], w["scaling"])
+
+    def step():
+        with torch.no_grad():
+            cpu_path.poziomka_forward(*args)
+
+    t0 = time.perf_counter()
+    step()
+    one = time.perf_counter() - t0
+    reps = int(max(3, min(10, budget_s / max(one, 1e-3))))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    flops = gemm_flops(dict(w, T=T))
+    return {"value": flops / med / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{T} tokens of the same block shape (d={w['d']}, E={w['E']}, top-{w['k']}, h={w['h']}, shared "
+                      f"h={w['shared_h']}), bf16 activations, int8 experts, torch CPU forward; median of {reps} runs "
+                      f"after 1 warm-up; {med * 1e3:.1f} ms per sample step"}
+
+
 def cpu_baseline(w, budget_s=15.0):
     """The reference's PyTorch CPU path (oracle/cpu_path.py: router + _fused_moe_infer's `grouped` branch, autograd
     for the backward) on a bounded sample of the same workload: the full d, E, k, h with fewer tokens."""
@@ -202,7 +316,8 @@ def main():
               f"multi-GPU path here", file=sys.stderr)
         sys.exit(2)
     w = WORKLOADS[args.workload]
-    ms, dom_ms, kern = run_gpu(w, args.steps, args.warmup)
+    pz = bool(w.get("poziomka"))
+    ms, dom_ms, kern = (run_gpu_poziomka if pz else run_gpu)(w, args.steps, args.warmup)
     flops = gemm_flops(w)
     tflops = flops / (ms * 1e-3) / 1e12
     M = w["T"] * w["k"]
@@ -222,22 +337,26 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic: seeded N(0,1) tokens and upstream gradient, N(0,0.02) router and expert weights "
-                "(torch CPU generator, seed 0, fp32 then bf16)",
+                "(torch CPU generator, seed 0, fp32 then bf16" + ("; experts quantised to int8 with per-column bf16 "
+                                                                  "scales)" if pz else ")"),
         "config": {"workload": w["desc"], "tokens": w["T"], "d_model": w["d"], "experts": w["E"], "top_k": w["k"],
                    "hidden": w["h"], "pass": "forward+backward" if w["backward"] else "forward"},
         "layer_us": round(ms * 1e3, 1),
         "pct_bf16_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2),
         "gemm_flops_per_step": flops,
         "roofline": {"bound": "mfma", "kernel": "hmoe gate/up grouped GEMM + fused SwiGLU (grouped_gemm_kernel, "
-                                                "EPI_SWIGLU)",
+                                                "EPI_SWIGLU" + (", int8 weights" if pz else "") + ")",
                      "achieved": round(dom_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(dom_tflops / PEAK_BF16_TFLOPS, 4),
                      "flops_per_launch": dom_flops, "avg_launch_us": round(dom_ms * 1e3, 2),
                      "traffic": traffic.get("bytes_per_launch") if traffic else None},
         "kernels_us": {k_: round(v, 1) for k_, v in kern.items()},
     }
+    if pz:
+        res["config"].update(shared_hidden=w["shared_h"], n_group=w["n_group"], topk_group=w["topk_group"],
+                             weights="int8 experts, bf16 router and shared expert")
     if not args.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline(w)
+        res["cpu_baseline"] = (cpu_baseline_poziomka if pz else cpu_baseline)(w)
     print(json.dumps(res), flush=True)
 
 

@@ -51,3 +51,31 @@ def training_step(x, wr, wgu, wd, k, dout, bias=None, renorm=True):
     out = layer_forward(x, wr, wgu, wd, k, bias, renorm)
     out.backward(dout)
     return out
+
+
+def poziomka_forward(x, gate_w, expert_bias, wgu, wgu_s, wd, wd_s, shared_g, shared_u, shared_d, k, n_group,
+                     topk_group, scaling):
+    """The BailingMoeV2 block's own forward, aurora/hf_pipeline.py:348-370 (PoziomkaMoE): sigmoid scores in fp32,
+    expert bias for selection, group-limited top-k, renormalised and scaled weights rounded to x.dtype; a loop over
+    the experts in use with the int8 weights widened to fp32 and the scale after the sum; index_add_ into an fp32
+    output; plus the shared expert (:314-322, bf16 F.linear)."""
+    n, d = x.shape
+    scores = torch.sigmoid(F.linear(x.float(), gate_w.float()))
+    routing = scores + expert_bias.float()
+    group = routing.view(n, n_group, -1).topk(2, dim=-1)[0].sum(-1)
+    keep = torch.zeros_like(group).scatter_(1, group.topk(topk_group, dim=-1, sorted=False)[1], 1)
+    keep = keep.bool().unsqueeze(-1).expand(n, n_group, routing.shape[1] // n_group).reshape(n, -1)
+    idx = routing.masked_fill(~keep, float("-inf")).topk(k, dim=-1)[1]
+    w = scores.gather(1, idx)
+    w = w / (w.sum(-1, keepdim=True) + 1e-20) * scaling
+    out = torch.zeros(n, d, dtype=torch.float32)
+    wq = w.to(x.dtype).float()
+    for e in idx.unique().tolist():
+        rows, slot = (idx == e).nonzero(as_tuple=True)
+        gu = ((x[rows].float() @ wgu[e].float()) * wgu_s[e].float()).to(x.dtype)
+        g, u = gu.chunk(2, dim=-1)
+        y = ((F.silu(g) * u).float() @ wd[e].float()) * wd_s[e].float()
+        out.index_add_(0, rows, (y * wq[rows, slot, None]).to(x.dtype).float())
+    lin = lambda a, m: F.linear(a, m.to(a.dtype))  # noqa: E731
+    shared = lin(F.silu(lin(x, shared_g)) * lin(x, shared_u), shared_d)
+    return out.to(x.dtype) + shared

@@ -527,3 +527,30 @@ def test_sigmoid_group_router_ties(oracle):
     assert list(ids[0]) == [2, 3]  # ties between groups 1 and 3 go to group 1
     ids, _, _ = oracle.sigmoid_group_from_logits(logits, 3, n_group, 2, bias, 1.0)
     assert list(ids[0]) == [6, 2, 3]
+
+
+def test_poziomka_cpu_path_vs_oracle(oracle):
+    """The transcribed reference block forward (oracle/cpu_path.py, aurora/hf_pipeline.py:348-370) against the oracle
+    pieces: the C router (ids equal), the int8 expert forward and the shared expert, within the bf16 tolerance."""
+    from oracle import cpu_path
+    from tests.util import assert_close_bf16, bits
+    T, d, h, E, k, ng, tg = 64, 128, 32, 16, 4, 4, 2
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(T, d, generator=g).bfloat16()
+    gw = (torch.randn(E, d, generator=g) * 0.05).bfloat16()
+    eb = (torch.randn(E, generator=g) * 0.05).bfloat16()
+    qgu, sgu = oracle.quant_int8((torch.randn(E, d, 2 * h, generator=g) * 0.05).numpy())
+    qd, sd = oracle.quant_int8((torch.randn(E, h, d, generator=g) * 0.05).numpy())
+    shg, shu = ((torch.randn(h, d, generator=g) * 0.05).bfloat16() for _ in range(2))
+    shd = (torch.randn(d, h, generator=g) * 0.05).bfloat16()
+    out = cpu_path.poziomka_forward(x, gw, eb, torch.from_numpy(qgu), torch.from_numpy(sgu).bfloat16(),
+                                    torch.from_numpy(qd), torch.from_numpy(sd).bfloat16(), shg, shu, shd, k, ng, tg, 2.5)
+    _, ids, w, _ = oracle.route_sigmoid_group(bits(x), bits(gw), k, ng, tg, eb.float().numpy(), 2.5)
+    xf = x.float().numpy()
+    moe = oracle.moe_forward(xf, ids, w, qgu.astype(np.float32), qd.astype(np.float32), wgu_s=sgu.astype(np.float64),
+                             wd_s=sd.astype(np.float64))
+    wsh = np.concatenate([shg.float().numpy(), shu.float().numpy()]).T[None]
+    sh = oracle.moe_forward(xf, np.zeros((T, 1), np.int64), np.ones((T, 1), np.float32), wsh,
+                            shd.float().numpy().T[None])
+    ref = oracle.round_bf16(moe["out"].astype(np.float64) + sh["out"].astype(np.float64))
+    assert_close_bf16(out.float().numpy(), ref, "poziomka cpu path")
