@@ -97,3 +97,48 @@ def test_poziomka_moe_forward(oracle, T, d, h, E, k, n_group, topk_group):
     np.testing.assert_array_equal(gids.cpu().numpy(), ids)
     assert_close_bf16(f32(y).reshape(T, d), ref, "PoziomkaMoE")
     assert_close_bf16(f32(mc.shared_experts(x.cuda())).reshape(T, d), shared_ref, "shared expert")
+
+
+def test_poziomka_varying_tokens(oracle):
+    """Packed-caption calls (aurora/slayer.py:383-432): one block called with token counts that change call by call,
+    no host synchronisation, each checked against the oracle; at 8192 tokens (the LM server's max_tokens) a sample
+    of tokens is checked."""
+    m = _make_block(oracle, 512, 320, 32, 4, 4, 2, 320, seed=11).cuda()
+    g = torch.Generator().manual_seed(12)
+    for T in (1, 17, 300, 2049):
+        print(f"PoziomkaMoE T={T}", flush=True)
+        x = torch.randn(T, 512, generator=g).bfloat16()
+        y = m(x.cuda())
+        _, ref, _ = _oracle_forward(oracle, m, x, 4, 4, 2)
+        assert_close_bf16(f32(y), ref, f"T={T}")
+    big = _make_block(oracle, 2048, 320, 128, 8, 8, 2, 320, seed=13).cuda()
+    x = torch.randn(8192, 2048, generator=g).bfloat16()
+    y = f32(big(x.cuda()))
+    sample = np.array([0, 1, 2, 777, 4095, 4096, 6000, 8190, 8191] + list(range(100, 8192, 97)))
+    _, ref, _ = _oracle_forward(oracle, big, x[sample], 8, 8, 2)
+    assert_close_bf16(y[sample], ref, "T=8192 sample")
+
+
+def test_poziomka_graph_replay(oracle):
+    """The forward at a fixed token count captured in a HIP graph (no host synchronisation, no allocation outside the
+    graph's pool) and replayed on new inputs: every replay equals the eager forward bit for bit."""
+    m = _make_block(oracle, 512, 320, 32, 4, 4, 2, 320, seed=21).cuda()
+    g = torch.Generator().manual_seed(22)
+    T = 1024
+    xs = [torch.randn(T, 512, generator=g).bfloat16().cuda() for _ in range(4)]
+    static_x = xs[0].clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        m(static_x)  # warm-up on the capture stream's device (first-use attributes set outside the capture)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_y = m(static_x)
+    for i, x in enumerate(xs):
+        eager = m(x)
+        torch.cuda.synchronize()
+        static_x.copy_(x)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static_y, eager), f"replay {i}"

@@ -148,3 +148,89 @@ def test_poziomka_module_layout():
         mb(torch.zeros(3, d, dtype=torch.bfloat16))
     with pytest.raises(RuntimeError, match="GPU"):
         PoziomkaMLP(d, sh).bfloat16()(torch.zeros(2, d, dtype=torch.bfloat16))
+
+
+def _rand_block(d, h, E, sh, seed):
+    from trenowanie_generatora_obrazkow_amd.poziomka import PoziomkaMoE
+    g = torch.Generator().manual_seed(seed)
+    m = PoziomkaMoE(d, h, E, 4, 4, 2, 2.5, sh)
+    with torch.no_grad():
+        for name, t in list(m.named_parameters()) + list(m.named_buffers()):
+            if t.dtype == torch.int8:
+                t.copy_(torch.randint(-127, 128, t.shape, generator=g, dtype=torch.int8))
+            else:
+                t.copy_(torch.randn(t.shape, generator=g) * 0.02)
+    return m.to(torch.bfloat16)
+
+
+def test_poziomka_export_round_trip(tmp_path):
+    """load_export reads the layout export.py:62-102 writes (config.json lm_* fields; the fused trunk under "lm.",
+    layer i's block under "lm.layers.{i}.mlp."), skips dense layers and other tensors, and export_state writes the same
+    keys back."""
+    import json
+
+    from safetensors.torch import save_file
+
+    from trenowanie_generatora_obrazkow_amd.poziomka import export_state, load_export
+    d, h, E, sh = 64, 32, 16, 48
+    blocks = {i: _rand_block(d, h, E, sh, seed=i) for i in (1, 2)}
+    sd = export_state(blocks)
+    assert "lm.layers.1.mlp._wgu" in sd and "lm.layers.2.mlp.shared_experts.down_proj.weight" in sd
+    sd["lm.layers.0.mlp.gate_proj.weight"] = torch.zeros(128, d, dtype=torch.bfloat16)  # the dense first layer
+    sd["lm.word_embeddings.weight"] = torch.zeros(10, d, dtype=torch.bfloat16)
+    sd["blocks.0.attn.qkv.weight"] = torch.zeros(8, 8)  # refiner tensors
+    te = tmp_path / "text_encoder"
+    te.mkdir()
+    save_file(sd, str(te / "diffusion_pytorch_model.safetensors"))
+    cfg = {"lm_arch": "poziomka", "lm_blocks": 3, "lm_dense_layers": 1, "lm_dim": d, "lm_moe_intermediate": h,
+           "lm_experts": E, "lm_top_k": 4, "lm_n_group": 4, "lm_topk_group": 2, "lm_routed_scaling": 2.5,
+           "lm_shared_intermediate": sh}
+    (te / "config.json").write_text(json.dumps(cfg))
+    for p in (tmp_path, te, te / "diffusion_pytorch_model.safetensors"):
+        got = load_export(str(p))
+        assert sorted(got) == [1, 2]
+        for i, m in got.items():
+            ref = blocks[i].state_dict()
+            for k, v in m.state_dict().items():
+                assert v.dtype == ref[k].dtype and torch.equal(v, ref[k]), (i, k)
+            assert (m.top_k, m.n_group, m.topk_group, m.scaling) == (4, 4, 2, 2.5)
+    cfg["lm_arch"] = "gollem"
+    (te / "config.json").write_text(json.dumps(cfg))
+    with pytest.raises(ValueError):
+        load_export(str(tmp_path))
+
+
+def test_swap_moe_replaces_reference_blocks():
+    """swap_moe finds blocks with the reference PoziomkaMoE's attributes (a stand-in class here) and replaces them by
+    this package's PoziomkaMoE with identical tensors."""
+    from trenowanie_generatora_obrazkow_amd.poziomka import PoziomkaMoE, swap_moe
+    d, h, E, sh = 64, 32, 16, 48
+    src = _rand_block(d, h, E, sh, seed=7)
+
+    class RefBlock(nn.Module):  # same attributes and state layout as aurora/hf_pipeline.py:332-346
+        def __init__(self):
+            super().__init__()
+            self.top_k, self.n_group, self.topk_group, self.scaling = 4, 4, 2, 2.5
+            self.gate = nn.Module()
+            self.gate.weight = nn.Parameter(src.gate.weight.detach().clone())
+            self.gate.register_buffer("expert_bias", src.gate.expert_bias.clone())
+            self.shared_experts = nn.Module()
+            for n in ("gate_proj", "up_proj", "down_proj"):
+                lin = nn.Linear(1, 1, bias=False)
+                lin.weight = nn.Parameter(getattr(src.shared_experts, n).weight.detach().clone())
+                setattr(self.shared_experts, n, lin)
+            for n in ("_wgu", "_wgu_s", "_wd", "_wd_s"):
+                self.register_buffer(n, getattr(src, n).clone())
+
+    class Layer(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.mlp = RefBlock()
+
+    model = nn.Sequential(Layer(), Layer())
+    assert swap_moe(model) == 2
+    for layer in model:
+        assert isinstance(layer.mlp, PoziomkaMoE)
+        for k, v in layer.mlp.state_dict().items():
+            assert torch.equal(v, src.state_dict()[k]), k
+    assert swap_moe(model) == 0

@@ -15,6 +15,11 @@ Forward, inference only (the reference block is frozen), served by the hmoe kern
   4. the shared expert (a dense SwiGLU MLP, :342 / :322) as the same two GEMMs over one "expert" holding every token;
   5. combine: the k slots summed in fp32, rounded, plus the shared expert's output (:369-370).
 
+`load_export` reads the exported text encoder (export.py:62-102) into these blocks, `export_state` writes them back
+in that format, and `swap_moe` replaces the reference's blocks inside a loaded trunk.  Calls take any token count
+(packed captions of varying total length, aurora/slayer.py:383-432) without a host synchronisation, so a forward of
+a fixed token count can be captured in a HIP graph and replayed.
+
 The reference adds the k slot outputs with `index_add_` in expert order; here they are summed in slot order (same
 terms, fp32 accumulation; the bf16 results can differ in the last place).  There is no CPU path: tensors must live
 on a ROCm GPU.
@@ -136,3 +141,82 @@ class PoziomkaMoE(nn.Module):
         wgu_sh, wd_sh = self.shared_experts._stack.get(self.shared_experts)
         shared = _dense_swiglu(x2, wgu_sh, wd_sh)
         return ops.combine(y, T, k, add=shared).view(shape)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# On-disk format: the exported text encoder (export.py:62-102) and swapping the reference's blocks
+# ---------------------------------------------------------------------------------------------------------------
+_MOE_KEYS = ("gate.weight", "gate.expert_bias", "shared_experts.gate_proj.weight", "shared_experts.up_proj.weight",
+             "shared_experts.down_proj.weight", "_wgu", "_wgu_s", "_wd", "_wd_s")
+
+
+def _export_paths(path):
+    import os
+    if os.path.isdir(path):
+        d = os.path.join(path, "text_encoder") if os.path.isdir(os.path.join(path, "text_encoder")) else path
+        return os.path.join(d, "config.json"), os.path.join(d, "diffusion_pytorch_model.safetensors")
+    return os.path.join(os.path.dirname(path), "config.json"), path
+
+
+def load_export(path, device=None, dtype=torch.bfloat16) -> dict:
+    """The MoE blocks of an exported Poziomka text encoder, as export.py:62-102 writes it: `text_encoder/config.json`
+    (lm_* fields) and `diffusion_pytorch_model.safetensors` holding the fused trunk under "lm." (layer i's block
+    under "lm.layers.{i}.mlp.": gate.weight, gate.expert_bias, shared_experts.{gate,up,down}_proj.weight, and the
+    int8 stacks _wgu / _wgu_s / _wd / _wd_s of aurora/hf_compat.py:154-162).  `path` is the export root, its
+    text_encoder directory, or the safetensors file.  Returns {layer index: PoziomkaMoE} for the MoE layers
+    (index >= lm_dense_layers), floating tensors in `dtype` (the trunk runs bf16), on `device`."""
+    import json
+
+    from safetensors import safe_open
+    cfg_path, st_path = _export_paths(path)
+    with open(cfg_path) as f:
+        cfg = json.load(f)
+    if cfg.get("lm_arch") != "poziomka":
+        raise ValueError(f"{cfg_path}: not a Poziomka text encoder export (lm_arch={cfg.get('lm_arch')!r})")
+    blocks = {}
+    with safe_open(st_path, framework="pt", device="cpu") as f:
+        keys = set(f.keys())
+        for i in range(cfg["lm_dense_layers"], cfg["lm_blocks"]):
+            pre = f"lm.layers.{i}.mlp."
+            missing = [k for k in _MOE_KEYS if pre + k not in keys]
+            if missing:
+                raise KeyError(f"{st_path}: layer {i} lacks {missing}")
+            m = PoziomkaMoE(cfg["lm_dim"], cfg["lm_moe_intermediate"], cfg["lm_experts"], cfg["lm_top_k"],
+                            cfg["lm_n_group"], cfg["lm_topk_group"], cfg["lm_routed_scaling"],
+                            cfg["lm_shared_intermediate"])
+            m.load_state_dict({k: f.get_tensor(pre + k) for k in _MOE_KEYS}, strict=True)
+            blocks[i] = m.to(dtype=dtype).to(device=device) if device is not None else m.to(dtype=dtype)
+    return blocks
+
+
+def export_state(blocks: dict) -> dict:
+    """{layer index: PoziomkaMoE} -> the "lm.layers.{i}.mlp." tensors of the export format (load_export's keys)."""
+    return {f"lm.layers.{i}.mlp.{k}": v.detach().cpu().contiguous()
+            for i, m in blocks.items() for k, v in m.state_dict().items()}
+
+
+def from_reference(mod) -> PoziomkaMoE:
+    """A PoziomkaMoE with the configuration and tensors of the reference's block (aurora/hf_pipeline.py:332-346, or
+    any module with the same attributes and state dict), on the same device and dtypes."""
+    E, d, h2 = mod._wgu.shape
+    sh = mod.shared_experts.gate_proj.weight.shape[0]
+    m = PoziomkaMoE(d, h2 // 2, E, mod.top_k, mod.n_group, mod.topk_group, mod.scaling, sh)
+    m = m.to(device=mod._wgu.device, dtype=mod.gate.weight.dtype)
+    m.load_state_dict(mod.state_dict(), strict=True)
+    return m
+
+
+def swap_moe(model) -> int:
+    """Replace every reference PoziomkaMoE block inside `model` (recognised by its attributes: _wgu, gate,
+    shared_experts, top_k, n_group, topk_group, scaling) by this module's PoziomkaMoE with the same tensors.
+    Returns the number of blocks replaced."""
+    n = 0
+    for parent in list(model.modules()):
+        for name, child in list(parent.named_children()):
+            if isinstance(child, PoziomkaMoE):
+                continue
+            if all(hasattr(child, a) for a in ("_wgu", "gate", "shared_experts", "top_k", "n_group", "topk_group",
+                                                "scaling")):
+                setattr(parent, name, from_reference(child))
+                n += 1
+    return n
