@@ -117,11 +117,13 @@ class PoziomkaMoE(nn.Module):
         self._gate_key = None
         self._gate_w = None
 
-    def _gate_weight(self):
-        w = self.gate.weight
-        key = (w.data_ptr(), w._version, w.device, w.dtype)
+    def _gate_tensors(self):
+        """bf16 router weight and fp32 expert bias as the kernel takes them, converted once per weight version."""
+        w, b = self.gate.weight, self.gate.expert_bias
+        key = (w.data_ptr(), w._version, w.device, w.dtype, b.data_ptr(), b._version, b.dtype)
         if key != self._gate_key:
-            self._gate_w = _bf16_exact(w.detach(), "gate.weight").contiguous()
+            self._gate_w = (_bf16_exact(w.detach(), "gate.weight").contiguous(),
+                            b.detach().to(torch.float32).contiguous())
             self._gate_key = key
         return self._gate_w
 
@@ -132,8 +134,9 @@ class PoziomkaMoE(nn.Module):
         if x2.dtype != torch.bfloat16:
             raise TypeError(f"hmoe PoziomkaMoE runs bf16 activations (got {x2.dtype})")
         T, k, E = x2.shape[0], self.top_k, self._wgu.shape[0]
-        _, ids, w = ops.route_sigmoid_group(x2, self._gate_weight(), k, self.n_group, self.topk_group,
-                                            expert_bias=self.gate.expert_bias, scaling=self.scaling)
+        gw, gb = self._gate_tensors()
+        _, ids, w = ops.route_sigmoid_group(x2, gw, k, self.n_group, self.topk_group, expert_bias=gb,
+                                            scaling=self.scaling)
         disp = ops.dispatch(ids, E, topk_w=w, want_inv=False)
         M = T * k
         act, _ = ops.gate_up_swiglu(x2, self._wgu, disp.counts, M, a_idx=disp.a_idx, wgu_s=self._wgu_s)
