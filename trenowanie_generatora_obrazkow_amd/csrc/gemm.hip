@@ -413,8 +413,21 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
   int slot = blockIdx.x;
   if ((G & 7) == 0) slot = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
 
+  // Work units.  Every workgroup takes units slot, slot + G, ...; when the tiles leave a final round at most half
+  // full (MGROUP), each tile of that round becomes two units of BM/2 rows, so the round takes about half a tile's
+  // time instead of a whole one (the half-row units run the main loop on their live fragment rows only).
+  const int full_units = total / G * G;
+  const int rem = total - full_units;
+  const bool split_last = MODE == MGROUP && rem > 0 && 2 * rem <= G;
+  const int units = split_last ? full_units + 2 * rem : total;
+
   int tile_iter = 0;
-  for (int tile = slot; tile < total; tile += G, ++tile_iter) {
+  for (int unit = slot; unit < units; unit += G, ++tile_iter) {
+    int tile = unit, half = -1;  // half >= 0: rows [half * BM/2, (half + 1) * BM/2) of the tile
+    if (unit >= full_units && split_last) {
+      tile = full_units + (unit - full_units) % rem;
+      half = (unit - full_units) / rem;
+    }
     // ---- tile decode ----
     int mt, nb;
     {
@@ -443,6 +456,14 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
       e = lo;
       row0 = s_rstart[e] + (int64_t)(mt - s_tstart[e]) * C::BM;
       row_end = min(s_rstart[e + 1], p.M);
+      if (half >= 0) {
+        row0 += half * (C::BM / 2);
+        row_end = min(row_end, row0 + C::BM / 2);
+        if (row0 >= row_end) {  // no rows in this half (uniform over the workgroup): nothing to do, and the
+          --tile_iter;          // LDS buffer parity of the next unit must still alternate with the previous one's
+          continue;
+        }
+      }
     } else {
       e = mt / nb_i;
       i0 = (mt - e * nb_i) * C::BM;
