@@ -18,8 +18,9 @@
  *         torch.topk's order wherever two probabilities are not rounded to the same float);
  *       * weights: w_j = p_{e_j}; renorm: s = w_0 + w_1 + ... (in j order), w_j = w_j / (s + 1e-20f) * scaling;
  *         otherwise w_j = w_j * scaling.
- *   - the sigmoid, group-limited router of BailingMoeV2 (aurora/hf_pipeline.py:352-359), from the same logits
- *     (orc_sigmoid_group_from_logits below states its orders);
+ *   - the sigmoid, group-limited router of BailingMoeV2 (aurora/hf_pipeline.py:352-359): its logits are the
+ *     sequential fma sums of orc_router_logits_seq (element order); orc_sigmoid_group_from_logits below states the
+ *     orders of the selection;
  *   - hexp: exp by Cody-Waite range reduction (Cephes split ln2 = 0.693359375 - 2.12194440e-4), a degree-7 Taylor
  *     polynomial in Horner form with fmaf, and exponent scaling by ldexpf; arguments below -87 give 0, above 88
  *     infinity.  The softmax uses it for x <= 0; the sigmoid 1 / (1 + hexp(-x)) for any x.
@@ -98,6 +99,21 @@ void orc_router_logits(const uint16_t* x, int64_t ldx, const uint16_t* wr, const
             }
             float dot = butterfly64(v);
             logits[t * E + e] = bias ? dot + bias[e] : dot;
+        }
+    }
+}
+
+/* logits (T, E) of the sigmoid router: for each (token, expert) the sequential fma sum over the row in element
+ * order, acc = fmaf(x[i], w[e][i], acc) from +0.0f (the order of route_sigmoid_kernel). */
+void orc_router_logits_seq(const uint16_t* x, int64_t ldx, const uint16_t* wr, int64_t T, int64_t d, int E,
+                           float* logits) {
+    for (int64_t t = 0; t < T; ++t) {
+        const uint16_t* xr = x + t * ldx;
+        for (int e = 0; e < E; ++e) {
+            const uint16_t* wrow = wr + (int64_t)e * d;
+            float acc = 0.0f;
+            for (int64_t i = 0; i < d; ++i) acc = fmaf(bf16_to_f32(xr[i]), bf16_to_f32(wrow[i]), acc);
+            logits[t * E + e] = acc;
         }
     }
 }

@@ -554,3 +554,22 @@ def test_poziomka_cpu_path_vs_oracle(oracle):
                             shd.float().numpy().T[None])
     ref = oracle.round_bf16(moe["out"].astype(np.float64) + sh["out"].astype(np.float64))
     assert_close_bf16(out.float().numpy(), ref, "poziomka cpu path")
+
+
+def test_router_logits_seq_vs_float64(oracle):
+    """The sigmoid router's sequential fma logits against float64: within the fp32 accumulation bound d * 2^-24 *
+    sum|x w| (a transposed operand or a dropped term would be far outside it)."""
+    rng = np.random.default_rng(21)
+    T, d, E = 40, 520, 24
+    x = oracle.round_bf16(rng.standard_normal((T, d)))
+    w = oracle.round_bf16(rng.standard_normal((E, d)) * 0.05)
+    lg = oracle.router_logits_seq(oracle.f32_to_bf16_bits(x), oracle.f32_to_bf16_bits(w))
+    ref = x.astype(np.float64) @ w.astype(np.float64).T
+    bound = d * 2.0 ** -24 * (np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64).T)
+    assert (np.abs(lg - ref) <= bound).all()
+    # a single term by hand: the first element's product leads the sum
+    x1 = np.zeros((1, 8), np.float32)
+    x1[0, 0] = 3.0
+    w1 = np.zeros((1, 8), np.float32)
+    w1[0, 0] = 0.5
+    assert oracle.router_logits_seq(oracle.f32_to_bf16_bits(x1), oracle.f32_to_bf16_bits(w1))[0, 0] == 1.5

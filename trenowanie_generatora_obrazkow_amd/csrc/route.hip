@@ -77,88 +77,20 @@ __device__ __forceinline__ void wave_argmax(float& bv, int& be) {
   argmax_take(bv, be, lane_xor<1>(bv), lane_xor_i<1>(be));
 }
 
-// Logits in the fixed order: lane l's partial is the sequential sum over chunks c and elements i of
-// x[c*512 + 8l + i] * w[c*512 + 8l + i]; the 64 partials are summed by the xor butterfly (s = 32, 16, ..., 1); the
-// bias is added last.  A bf16 x bf16 product has at most 16 significant bits, so it is exact in fp32 and the fused
-// multiply-add rounds exactly once, like a separate multiply and add (barring products below the fp32 normal range,
-// |x w| < 2^-126, which round differently).
-//
-// Experts are processed in groups of G (a power of two <= 64) with a "transposed" butterfly: at step s the lanes
-// with bit s set keep the upper half of the group's partials and send the lower half, so each step halves the values
-// per lane instead of reducing every expert separately; each value still meets exactly the partner the plain
-// butterfly would give it (fp addition is commutative), so the sums are bit-identical.  After log2(G) steps lane l
-// holds expert l >> (6 - log2 G) of the group, and the remaining steps are the plain butterfly.
-//
-// SIG = false: softmax router (bias added to the logits, selection on the logits, weights = softmax probabilities).
-// SIG = true: the sigmoid, group-limited router of BailingMoeV2 (aurora/hf_pipeline.py:352-359): score =
-// 1 / (1 + exp(-logit)); routing = score + bias (selection only); experts in n_group consecutive groups of
+// Selection for one token from its E logits held lane-wise (lane l: experts l, l + 64, ...), for both routers.
+// SIG = false: softmax router (the bias is already in the logits; selection on the logits; weights = softmax
+// probabilities).  SIG = true: the sigmoid, group-limited router of BailingMoeV2 (aurora/hf_pipeline.py:352-359):
+// score = 1 / (1 + exp(-logit)); routing = score + bias (selection only); experts in n_group consecutive groups of
 // E / n_group, a group's value is the sum of its two largest routing values, the topk_group best groups are kept
 // (ties to the lower group) and the k experts with the largest routing values among them selected (ties to the
 // lower expert); weights = the selected scores, renormalised (w / (sum + 1e-20)) and scaled.  `logits` then
 // receives the scores.
-template <int NCH, int G, bool SIG>
-__global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restrict__ x, int64_t ldx,
-                                                         const uint16_t* __restrict__ wr,
-                                                         const float* __restrict__ bias, int T, int d, int E, int k,
-                                                         int renorm, float scaling, float* __restrict__ logits,
-                                                         int32_t* __restrict__ ids, float* __restrict__ wout,
-                                                         int n_group, int topk_group) {
+template <bool SIG>
+__device__ __forceinline__ void route_select(const float (&lg)[kRouteEPL], int t, int lane, int E, int k, int renorm,
+                                             float scaling, const float* __restrict__ bias, float* __restrict__ logits,
+                                             int32_t* __restrict__ ids, float* __restrict__ wout, int n_group,
+                                             int topk_group) {
 #pragma clang fp contract(off)
-  const int lane = threadIdx.x & 63;
-  const int nwaves = blockDim.x >> 6;
-  const int wave = threadIdx.x >> 6;
-  for (int t = blockIdx.x * nwaves + wave; t < T; t += gridDim.x * nwaves) {
-    uint4 xr[NCH];
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      int idx = c * 512 + lane * 8;
-      if (idx < d)
-        xr[c] = *reinterpret_cast<const uint4*>(x + (int64_t)t * ldx + idx);
-      else
-        xr[c] = make_uint4(0, 0, 0, 0);
-    }
-    float lg[kRouteEPL];
-#pragma unroll
-    for (int i = 0; i < kRouteEPL; ++i) lg[i] = -__builtin_inff();
-    for (int g0 = 0; g0 < E; g0 += G) {
-      // lane partials of the G experts of this group; rows past E repeat row E-1 and columns past d read column
-      // d-8 against zero x (both only feed lanes / values that are discarded), so the loads carry no branches
-      float p[G];
-#pragma unroll
-      for (int e = 0; e < G; ++e) {
-        p[e] = 0.0f;
-        const uint16_t* wrow = wr + (int64_t)min(g0 + e, E - 1) * d;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-          const int idx = min(c * 512 + lane * 8, d - 8);
-          const uint4 wv = *reinterpret_cast<const uint4*>(wrow + idx);
-          const uint32_t xw[4] = {xr[c].x, xr[c].y, xr[c].z, xr[c].w};
-          const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            p[e] = __builtin_fmaf(bf_lo(xw[j]), bf_lo(ww[j]), p[e]);
-            p[e] = __builtin_fmaf(bf_hi(xw[j]), bf_hi(ww[j]), p[e]);
-          }
-        }
-      }
-      transposed_butterfly<G>(p, lane);
-      constexpr int H = G == 8 ? 3 : G == 16 ? 4 : G == 32 ? 5 : 6;
-      float v = p[0];
-      if constexpr (H < 4) v = bfly_add<4>(v);  // the plain butterfly finishes in descending s
-      if constexpr (H < 5) v = bfly_add<2>(v);
-      if constexpr (H < 6) v = bfly_add<1>(v);
-      const int my_e = g0 + (lane >> (6 - H));
-      if (!SIG && bias && my_e < E) v = __fadd_rn(v, bias[my_e]);
-      // lane l collects expert i*64 + l from the lanes of its group slot
-#pragma unroll
-      for (int i = 0; i < kRouteEPL; ++i) {
-        if (i * 64 < E && i * 64 + 63 >= g0 && i * 64 < g0 + G) {
-          const int e = i * 64 + lane;
-          const float val = __shfl(v, ((e - g0) << (6 - H)) & 63, 64);
-          if (e >= g0 && e < g0 + G && e < E) lg[i] = val;
-        }
-      }
-    }
     // key[i]: the selection key of expert i*64 + lane; num[i]: the value its weight is made of (divided by S)
     float key[kRouteEPL], num[kRouteEPL];
     float S = 1.0f;
@@ -290,6 +222,193 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restr
           ids[(int64_t)t * k + j] = sele[j];
           wout[(int64_t)t * k + j] = wj;
         }
+    }
+}
+
+// Logits in the fixed order: lane l's partial is the sequential sum over chunks c and elements i of
+// x[c*512 + 8l + i] * w[c*512 + 8l + i]; the 64 partials are summed by the xor butterfly (s = 32, 16, ..., 1); the
+// bias is added last.  A bf16 x bf16 product has at most 16 significant bits, so it is exact in fp32 and the fused
+// multiply-add rounds exactly once, like a separate multiply and add (barring products below the fp32 normal range,
+// |x w| < 2^-126, which round differently).
+//
+// Experts are processed in groups of G (a power of two <= 64) with a "transposed" butterfly: at step s the lanes
+// with bit s set keep the upper half of the group's partials and send the lower half, so each step halves the values
+// per lane instead of reducing every expert separately; each value still meets exactly the partner the plain
+// butterfly would give it (fp addition is commutative), so the sums are bit-identical.  After log2(G) steps lane l
+// holds expert l >> (6 - log2 G) of the group, and the remaining steps are the plain butterfly.
+template <int NCH, int G>
+__global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                         const uint16_t* __restrict__ wr,
+                                                         const float* __restrict__ bias, int T, int d, int E, int k,
+                                                         int renorm, float scaling, float* __restrict__ logits,
+                                                         int32_t* __restrict__ ids, float* __restrict__ wout) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int nwaves = blockDim.x >> 6;
+  const int wave = threadIdx.x >> 6;
+  for (int t = blockIdx.x * nwaves + wave; t < T; t += gridDim.x * nwaves) {
+    uint4 xr[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      int idx = c * 512 + lane * 8;
+      if (idx < d)
+        xr[c] = *reinterpret_cast<const uint4*>(x + (int64_t)t * ldx + idx);
+      else
+        xr[c] = make_uint4(0, 0, 0, 0);
+    }
+    float lg[kRouteEPL];
+#pragma unroll
+    for (int i = 0; i < kRouteEPL; ++i) lg[i] = -__builtin_inff();
+    for (int g0 = 0; g0 < E; g0 += G) {
+      // lane partials of the G experts of this group; rows past E repeat row E-1 and columns past d read column
+      // d-8 against zero x (both only feed lanes / values that are discarded), so the loads carry no branches
+      float p[G];
+#pragma unroll
+      for (int e = 0; e < G; ++e) {
+        p[e] = 0.0f;
+        const uint16_t* wrow = wr + (int64_t)min(g0 + e, E - 1) * d;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+          const int idx = min(c * 512 + lane * 8, d - 8);
+          const uint4 wv = *reinterpret_cast<const uint4*>(wrow + idx);
+          const uint32_t xw[4] = {xr[c].x, xr[c].y, xr[c].z, xr[c].w};
+          const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            p[e] = __builtin_fmaf(bf_lo(xw[j]), bf_lo(ww[j]), p[e]);
+            p[e] = __builtin_fmaf(bf_hi(xw[j]), bf_hi(ww[j]), p[e]);
+          }
+        }
+      }
+      transposed_butterfly<G>(p, lane);
+      constexpr int H = G == 8 ? 3 : G == 16 ? 4 : G == 32 ? 5 : 6;
+      float v = p[0];
+      if constexpr (H < 4) v = bfly_add<4>(v);  // the plain butterfly finishes in descending s
+      if constexpr (H < 5) v = bfly_add<2>(v);
+      if constexpr (H < 6) v = bfly_add<1>(v);
+      const int my_e = g0 + (lane >> (6 - H));
+      if (bias && my_e < E) v = __fadd_rn(v, bias[my_e]);
+      // lane l collects expert i*64 + l from the lanes of its group slot
+#pragma unroll
+      for (int i = 0; i < kRouteEPL; ++i) {
+        if (i * 64 < E && i * 64 + 63 >= g0 && i * 64 < g0 + G) {
+          const int e = i * 64 + lane;
+          const float val = __shfl(v, ((e - g0) << (6 - H)) & 63, 64);
+          if (e >= g0 && e < g0 + G && e < E) lg[i] = val;
+        }
+      }
+    }
+    route_select<false>(lg, t, lane, E, k, renorm, scaling, bias, logits, ids, wout, 1, 1);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// BailingMoeV2 (sigmoid, group-limited) router.  A workgroup of 4 waves routes 4 x kSgTW tokens.  The router weight
+// and the workgroup's token values stream through LDS in chunks of 64 elements (double-buffered): weight rows as
+// bf16 with a row pitch of kSgPitch bytes (the lanes' 16-byte reads of 64 consecutive rows fall on distinct banks),
+// token values widened to fp32 once when staged and read back as wave-uniform broadcasts.  Lane l owns experts l,
+// l + 64, ...; each logit is the sequential fma sum over the row in element order (x[0]*w[0] first), and each
+// 8-element piece of weight widened to fp32 once serves the wave's kSgTW tokens.
+// ---------------------------------------------------------------------------------------------------------------
+constexpr int kSgTW = 4, kSgChunk = 64, kSgPitch = 144;
+constexpr int kSgTok = 4 * kSgTW;                    // tokens per workgroup
+constexpr int kSgXBytes = kSgTok * kSgChunk * 4;     // fp32 token values per chunk buffer
+
+template <int EPL>
+__global__ __launch_bounds__(256) void route_sigmoid_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                            const uint16_t* __restrict__ wr,
+                                                            const float* __restrict__ bias, int T, int d, int E,
+                                                            int k, float scaling, float* __restrict__ scores,
+                                                            int32_t* __restrict__ ids, float* __restrict__ wout,
+                                                            int n_group, int topk_group) {
+#pragma clang fp contract(off)
+  // [2][EPL * 64][kSgPitch] bf16 weight rows, then [2][kSgTok][kSgChunk] fp32 token values
+  extern __shared__ __attribute__((aligned(16))) char s_w[];
+  constexpr int ER = EPL * 64;       // expert rows staged (rows past E are zero)
+  constexpr int PIECES = ER * 8;     // 16-byte weight pieces per chunk
+  constexpr int PPT = PIECES / 256;  // weight pieces per thread
+  char* const s_x = s_w + 2 * ER * kSgPitch;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tblk = blockIdx.x * kSgTok;  // the workgroup's first token
+  const int nch = (d + kSgChunk - 1) / kSgChunk;
+  uint4 stage[PPT];
+  uint4 xstage;  // threads 0..127: 8 token values (token tid / 8, elements 8 * (tid % 8) + 0..7 of the chunk)
+  auto load_chunk = [&](int c) {
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      const int pc = tid + 256 * j, e = pc >> 3, el = c * kSgChunk + (pc & 7) * 8;
+      stage[j] = (e < E && el < d) ? *reinterpret_cast<const uint4*>(wr + (int64_t)e * d + el) : make_uint4(0, 0, 0, 0);
+    }
+    if (tid < kSgTok * 8) {
+      const int t = min(tblk + (tid >> 3), T - 1), el = c * kSgChunk + (tid & 7) * 8;
+      xstage = el < d ? *reinterpret_cast<const uint4*>(x + (int64_t)t * ldx + el) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store_chunk = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      const int pc = tid + 256 * j;
+      *reinterpret_cast<uint4*>(s_w + (buf * ER + (pc >> 3)) * kSgPitch + (pc & 7) * 16) = stage[j];
+    }
+    if (tid < kSgTok * 8) {
+      float* xd = reinterpret_cast<float*>(s_x + buf * kSgXBytes) + (tid >> 3) * kSgChunk + (tid & 7) * 8;
+      *reinterpret_cast<float4*>(xd) = make_float4(bf_lo(xstage.x), bf_hi(xstage.x), bf_lo(xstage.y), bf_hi(xstage.y));
+      *reinterpret_cast<float4*>(xd + 4) =
+          make_float4(bf_lo(xstage.z), bf_hi(xstage.z), bf_lo(xstage.w), bf_hi(xstage.w));
+    }
+  };
+  float acc[kSgTW][EPL];
+#pragma unroll
+  for (int q = 0; q < kSgTW; ++q)
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) acc[q][i] = 0.0f;
+  load_chunk(0);
+  store_chunk(0);
+  __syncthreads();
+  for (int c = 0; c < nch; ++c) {
+    if (c + 1 < nch) load_chunk(c + 1);
+    const char* wbuf = s_w + (c & 1) * ER * kSgPitch;
+    const float* xbuf = reinterpret_cast<const float*>(s_x + (c & 1) * kSgXBytes) + wave * kSgTW * kSgChunk;
+    const int npc = min(8, (d - c * kSgChunk) / 8);  // 8-element pieces of this chunk (the last may be short)
+#pragma unroll 2
+    for (int pcs = 0; pcs < npc; ++pcs) {
+      float xv[kSgTW][8];
+#pragma unroll
+      for (int q = 0; q < kSgTW; ++q) {
+        const float4 a = *reinterpret_cast<const float4*>(xbuf + q * kSgChunk + pcs * 8);
+        const float4 b = *reinterpret_cast<const float4*>(xbuf + q * kSgChunk + pcs * 8 + 4);
+        xv[q][0] = a.x; xv[q][1] = a.y; xv[q][2] = a.z; xv[q][3] = a.w;
+        xv[q][4] = b.x; xv[q][5] = b.y; xv[q][6] = b.z; xv[q][7] = b.w;
+      }
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) {
+        const uint4 wv = *reinterpret_cast<const uint4*>(wbuf + (i * 64 + lane) * kSgPitch + pcs * 16);
+        const uint32_t w4[4] = {wv.x, wv.y, wv.z, wv.w};
+        float wf[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          wf[2 * j] = bf_lo(w4[j]);
+          wf[2 * j + 1] = bf_hi(w4[j]);
+        }
+#pragma unroll
+        for (int q = 0; q < kSgTW; ++q)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[q][i] = __builtin_fmaf(xv[q][j], wf[j], acc[q][i]);
+      }
+    }
+    if (c + 1 < nch) store_chunk((c + 1) & 1);  // the other buffers: last read before the previous barrier
+    __syncthreads();
+  }
+  const int t0 = tblk + wave * kSgTW;
+#pragma unroll
+  for (int q = 0; q < kSgTW; ++q) {
+    const int t = t0 + q;
+    if (t < T) {
+      float lg[kRouteEPL];
+#pragma unroll
+      for (int i = 0; i < kRouteEPL; ++i) lg[i] = i < EPL ? acc[q][i] : -__builtin_inff();
+      route_select<true>(lg, t, lane, E, k, 1, scaling, bias, scores, ids, wout, n_group, topk_group);
     }
   }
 }
@@ -841,10 +960,9 @@ static inline int grid_for(int64_t work, int per_block, int cap = 8192) {
 
 static inline bool al16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-template <bool SIG>
 static int route_launch(const void* x, int64_t ldx, const void* wr, const float* bias, int64_t T, int64_t d, int E,
                         int k, int renorm, float scaling, float* logits, int32_t* topk_ids, float* topk_w,
-                        int n_group, int topk_group, hipStream_t s) {
+                        hipStream_t s) {
   const int grid = grid_for(T, 4, 4096);
   const int nch = (int)((d + 511) / 512);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
@@ -853,8 +971,8 @@ static int route_launch(const void* x, int64_t ldx, const void* wr, const float*
   int group = E <= 8 ? 8 : E <= 16 ? 16 : E <= 32 ? 32 : 64;
   if (nch > 4 && group > 16) group = 16;
 #define HMOE_ROUTE(NC, GR)                                                                                        \
-  hipLaunchKernelGGL((route_topk_kernel<NC, GR, SIG>), dim3(grid), dim3(256), 0, s, xp, ldx, wp, bias, (int)T,    \
-                     (int)d, E, k, renorm, scaling, logits, topk_ids, topk_w, n_group, topk_group)
+  hipLaunchKernelGGL((route_topk_kernel<NC, GR>), dim3(grid), dim3(256), 0, s, xp, ldx, wp, bias, (int)T, (int)d, \
+                     E, k, renorm, scaling, logits, topk_ids, topk_w)
 #define HMOE_ROUTE_G(NC)        \
   if (group == 8)               \
     HMOE_ROUTE(NC, 8);          \
@@ -927,8 +1045,8 @@ int hmoe_route_topk(const void* x, int64_t ldx, const void* wr, const float* bia
                     hmoe_stream_t stream) {
   const int rc = route_check(x, ldx, wr, T, d, E, k, topk_ids, topk_w);
   if (rc || T == 0) return rc;
-  return route_launch<false>(x, ldx, wr, bias, T, d, E, k, renorm, scaling, logits, topk_ids, topk_w, 1, 1,
-                             reinterpret_cast<hipStream_t>(stream));
+  return route_launch(x, ldx, wr, bias, T, d, E, k, renorm, scaling, logits, topk_ids, topk_w,
+                      reinterpret_cast<hipStream_t>(stream));
 }
 
 int hmoe_route_sigmoid_group(const void* x, int64_t ldx, const void* wr, const float* expert_bias, int64_t T,
@@ -942,8 +1060,26 @@ int hmoe_route_sigmoid_group(const void* x, int64_t ldx, const void* wr, const f
     if (eg < 2 || eg > 64 || (eg & (eg - 1))) return HMOE_ERR_SHAPE;
     if (k > topk_group * eg) return HMOE_ERR_SHAPE;  // the kept groups must hold k experts
   }
-  return route_launch<true>(x, ldx, wr, expert_bias, T, d, E, k, 1, scaling, scores, topk_ids, topk_w, n_group,
-                            topk_group, reinterpret_cast<hipStream_t>(stream));
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int epl = (E + 63) / 64;
+  const size_t lds = (size_t)2 * epl * 64 * kSgPitch + 2 * kSgXBytes;
+  const int grid = (int)((T + kSgTok - 1) / kSgTok);
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  const uint16_t* wp = static_cast<const uint16_t*>(wr);
+#define HMOE_SG(EP)                                                                                             \
+  hipLaunchKernelGGL(route_sigmoid_kernel<EP>, dim3(grid), dim3(256), lds, s, xp, ldx, wp, expert_bias, (int)T, \
+                     (int)d, E, k, scaling, scores, topk_ids, topk_w, n_group, topk_group)
+  if (epl == 1)
+    HMOE_SG(1);
+  else if (epl == 2)
+    HMOE_SG(2);
+  else if (epl == 3)
+    HMOE_SG(3);
+  else
+    HMOE_SG(4);
+#undef HMOE_SG
+  HMOE_CHECK_LAUNCH();
+  return HMOE_OK;
 }
 
 size_t hmoe_dispatch_workspace_size(int64_t T, int k, int E) {
