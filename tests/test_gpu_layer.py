@@ -106,3 +106,33 @@ def test_fuse_moe_infer(oracle):
     assert model[0]._mode == "hip"
     ref = oracle.moe_forward(f32(x), ids.numpy(), w.numpy(), f32(wgu_ref), f32(wd_ref))
     assert_close_bf16(f32(y), ref["out"], "moe_infer")
+
+
+def test_fuse_moe_matches_expert_loop():
+    """The claim of aurora/hf_compat.py:64-65: the fused path equals the per-expert loop it replaces up to bf16
+    rounding and routing ties ("cos 0.9999 to the loop").  The loop here is the unfused moe_infer of DeepSeek-style
+    blocks restated with torch on the CPU: each expert's bf16 Linear layers on its tokens, times the routing weight,
+    summed over the k slots."""
+    from trenowanie_generatora_obrazkow_amd.hf_compat import fuse_moe
+    T, d, h, E, k = 600, 256, 192, 8, 2
+    torch.manual_seed(5)
+    model = nn.Sequential(_MoEBlock(d, h, E)).bfloat16()
+    experts = [(e.gate_proj.weight.detach().clone(), e.up_proj.weight.detach().clone(),
+                e.down_proj.weight.detach().clone()) for e in model[0].experts]
+    assert fuse_moe(model) == 1
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(T, d, generator=g).bfloat16()
+    ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)])
+    w = torch.rand(T, k, generator=g).softmax(-1)
+    y = model.cuda()[0].moe_infer(x.cuda(), ids.cuda(), w.cuda()).float().cpu()
+    ref = torch.zeros(T, d)
+    for e, (wg, wu, wdn) in enumerate(experts):
+        rows, slot = (ids == e).nonzero(as_tuple=True)
+        if rows.numel() == 0:
+            continue
+        xe = x[rows]
+        out = torch.nn.functional.linear(torch.nn.functional.silu(torch.nn.functional.linear(xe, wg)) *
+                                         torch.nn.functional.linear(xe, wu), wdn)
+        ref.index_add_(0, rows, out.float() * w[rows, slot, None])
+    cos = torch.nn.functional.cosine_similarity(y.flatten(), ref.flatten(), dim=0).item()
+    assert cos > 0.9999, cos
