@@ -120,3 +120,31 @@ def test_grouped_wgrad(oracle, tile, M, P, N, E, skew):
             st += c
         assert_close_bf16(f32(dw), oracle.round_bf16(ref) if dt == torch.bfloat16 else ref, f"wgrad {dt}")
         assert (f32(dw)[counts.numpy() == 0] == 0).all()
+
+
+def test_ops_reject_bad_inputs():
+    """The tensor wrappers stop wrong shapes, dtypes and layouts before the C entry points (whose kernels trust the
+    sizes they are given)."""
+    from trenowanie_generatora_obrazkow_amd import ops
+    dev = torch.device("cuda")
+    E, d, h, M = 4, 64, 32, 40
+    wgu = torch.zeros(E, d, 2 * h, dtype=torch.bfloat16, device=dev)
+    wd = torch.zeros(E, h, d, dtype=torch.bfloat16, device=dev)
+    counts = torch.tensor([10, 10, 10, 10], dtype=torch.int32, device=dev)
+    x = torch.zeros(M, d, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(TypeError):
+        ops.gate_up_swiglu(x.float(), wgu, counts, M)
+    with pytest.raises(ValueError):
+        ops.gate_up_swiglu(x[:, :32], wgu, counts, M)                       # wrong d
+    with pytest.raises(ValueError):
+        ops.gate_up_swiglu(x[:20], wgu, counts, M)                          # too few rows, no gather
+    with pytest.raises(ValueError):
+        ops.gate_up_swiglu(x, wgu, counts, M, a_idx=torch.zeros(M - 1, dtype=torch.int32, device=dev))
+    act = torch.zeros(M, h, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError):
+        ops.down_scatter(act[:, :16], wd, counts, M, None, None)
+    with pytest.raises(ValueError):
+        ops.combine(torch.zeros(M - 2, d, dtype=torch.bfloat16, device=dev), M // 2, 2)
+    with pytest.raises(ValueError):
+        ops.unpermute_bwd(torch.zeros(M, d, device=dev), torch.zeros(M, dtype=torch.int32, device=dev), M // 2, 2,
+                          dlogits=torch.zeros(M // 2, E, device=dev))

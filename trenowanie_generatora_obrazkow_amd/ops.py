@@ -43,6 +43,36 @@ def _contig(t, name):
     return t
 
 
+def _need(t, name, shape=None, dtypes=None, contig=True, min_rows=None):
+    """Validate a tensor handed to a C entry point: the kernels trust the sizes they are given, so a wrong shape,
+    dtype or layout must stop here rather than become an out-of-range access on the device.  shape entries of None
+    are not checked; min_rows: at least that many rows (a gathered operand); a row-strided 2-D tensor passes when
+    contig=False as long as its rows are contiguous."""
+    if t is None:
+        raise ValueError(f"{name} is required")
+    L.require_gpu(t, name)
+    if dtypes is not None and t.dtype not in dtypes:
+        raise TypeError(f"{name}: dtype {t.dtype} not in {dtypes}")
+    if shape is not None:
+        if t.dim() != len(shape) or any(want is not None and got != want for got, want in zip(t.shape, shape)):
+            raise ValueError(f"{name}: shape {tuple(t.shape)} does not match {shape}")
+    if min_rows is not None and t.shape[0] < min_rows:
+        raise ValueError(f"{name}: {t.shape[0]} rows, at least {min_rows} needed")
+    if contig and not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if not contig and t.dim() == 2 and t.stride(1) != 1:
+        raise ValueError(f"{name} rows must be contiguous")
+    return t
+
+
+_BF16 = (torch.bfloat16,)
+_I32 = (torch.int32,)
+
+
+def _rows_index(idx, name, M):
+    return None if idx is None else _need(idx, name, (M,), _I32)
+
+
 def route_topk(x: torch.Tensor, wr: torch.Tensor, k: int, bias=None, renorm=True, scaling=1.0, want_logits=True):
     """Softmax top-k router -> (logits (T, E) fp32 or None, topk_ids (T, k) int32, topk_w (T, k) fp32)."""
     T, d = x.shape
@@ -204,6 +234,8 @@ def gate_up_swiglu(x, wgu, counts, M, a_idx=None, keep_gu=False, wgu_s=None):
     wgu = _contig(wgu, "wgu")
     counts = _counts(counts)
     wgu_s = _w_scale(wgu, wgu_s, h2)
+    a_idx = _rows_index(a_idx, "a_idx", M)
+    _need(x, "x", (None, d), _BF16, contig=False, min_rows=1 if a_idx is not None else M)
     act = torch.empty(M, h, device=x.device, dtype=torch.bfloat16)
     if wgu_s is not None:
         if keep_gu:
@@ -226,6 +258,10 @@ def down_scatter(act, wd, counts, M, w_sorted, y_idx, keep_yhat=False, wd_s=None
     wd = _contig(wd, "wd")
     counts = _counts(counts)
     wd_s = _w_scale(wd, wd_s, d)
+    _need(act, "act", (M, h), _BF16)
+    y_idx = _rows_index(y_idx, "y_idx", M)
+    if w_sorted is not None:
+        _need(w_sorted, "w_sorted", (M,), _BF16)
     y = torch.empty(M, d, device=act.device, dtype=torch.bfloat16)
     if wd_s is not None:
         if keep_yhat:
@@ -244,6 +280,7 @@ def down_scatter(act, wd, counts, M, w_sorted, y_idx, keep_yhat=False, wd_s=None
 def combine(y, T, k, add=None):
     """out[t] = bf16(sum_j y[t*k + j]) (+ add[t], rounded once more: bf16 + bf16)."""
     d = y.shape[1]
+    _need(y, "y", (T * k, d), _BF16)
     out = torch.empty(T, d, device=y.device, dtype=y.dtype)
     with _Probe("combine"):
         if add is None:
@@ -260,6 +297,11 @@ def combine_bwd(dout, yhat, disp: Dispatch, k):
     M, d = yhat.shape
     T = M // k
     dout = dout.contiguous()
+    _need(yhat, "yhat", (T * k, d), _BF16)
+    _need(dout, "dout", (T, d), _BF16)
+    for t_, n_ in ((disp.order, "order"), (disp.a_idx, "a_idx")):
+        _need(t_, n_, (M,), _I32)
+    _need(disp.w_sorted, "w_sorted", (M,), _BF16)
     dys = torch.empty(M, d, device=dout.device, dtype=torch.bfloat16)
     dtw = torch.empty(T, k, device=dout.device, dtype=torch.float32)
     with _Probe("combine_bwd"):
@@ -272,6 +314,13 @@ def down_dgrad_swiglu(dy, wd, counts, M, gu, a_idx=None, w_sorted=None):
     """dgu (M, 2h) from the upstream gradient dy (T, d) gathered through a_idx (or sorted rows (M, d) when a_idx is
     None) and scaled by w_sorted in fp32."""
     E, h, d = wd.shape
+    wd = _contig(wd, "wd")
+    counts = _counts(counts)
+    a_idx = _rows_index(a_idx, "a_idx", M)
+    _need(dy, "dy", (None, d), _BF16, min_rows=1 if a_idx is not None else M)
+    _need(gu, "gu", (M, 2 * h), _BF16)
+    if w_sorted is not None:
+        _need(w_sorted, "w_sorted", (M,), _BF16)
     dgu = torch.empty(M, 2 * h, device=dy.device, dtype=torch.bfloat16)
     with _Probe("down_dgrad_swiglu"):
         L.call("hmoe_down_dgrad_swiglu", L.ptr(dy), L.ptr(a_idx), L.ptr(w_sorted), L.ptr(wd), E, h, d, L.ptr(counts),
@@ -281,6 +330,9 @@ def down_dgrad_swiglu(dy, wd, counts, M, gu, a_idx=None, w_sorted=None):
 
 def gate_up_dgrad(dgu, wgu, counts, M, dtype=torch.float32):
     E, d, h2 = wgu.shape
+    wgu = _contig(wgu, "wgu")
+    counts = _counts(counts)
+    _need(dgu, "dgu", (M, h2), _BF16)
     dxs = torch.empty(M, d, device=dgu.device, dtype=dtype)
     with _Probe("gate_up_dgrad"):
         L.call("hmoe_gate_up_dgrad", L.ptr(dgu), L.ptr(wgu), E, d, h2 // 2, L.ptr(counts), L.dt(counts), M, L.ptr(dxs),
@@ -291,6 +343,10 @@ def gate_up_dgrad(dgu, wgu, counts, M, dtype=torch.float32):
 def grouped_wgrad(a, b, counts, E, dtype=torch.bfloat16):
     M, P = a.shape
     N = b.shape[1]
+    counts = _counts(counts)
+    _need(a, "a", (M, P), _BF16, contig=False)
+    _need(b, "b", (M, N), _BF16, contig=False)
+    _need(counts, "counts", (E,), (torch.int32, torch.int64))
     dw = torch.empty(E, P, N, device=a.device, dtype=dtype)
     with _Probe("grouped_wgrad"):
         L.call("hmoe_grouped_wgrad", L.ptr(a), a.stride(0), L.ptr(b), b.stride(0), E, P, N, L.ptr(counts), L.dt(counts), M,
@@ -302,6 +358,10 @@ def router_bwd(logits, ids, dtw, x, renorm=True, scaling=1.0, dwr_dtype=torch.fl
     T, E = logits.shape
     k = ids.shape[1]
     d = x.shape[1]
+    _need(logits, "logits", (T, E), (torch.float32,))
+    _need(ids, "topk_ids", (T, k), _I32)
+    _need(dtw, "dtopk_w", (T, k), (torch.float32,))
+    _need(x, "x", (T, d), _BF16, contig=False)
     dl = torch.empty(T, E, device=logits.device, dtype=torch.float32)
     dwr = torch.empty(E, d, device=logits.device, dtype=dwr_dtype) if want_dwr else None
     ws_bytes = L.lib().hmoe_router_bwd_workspace_size(T, E, d) if want_dwr else 0
@@ -316,6 +376,13 @@ def router_bwd(logits, ids, dtw, x, renorm=True, scaling=1.0, dwr_dtype=torch.fl
 def unpermute_bwd(dxs, inv_pos, T, k, dlogits=None, wr=None):
     d = dxs.shape[1]
     E = wr.shape[0] if wr is not None else 0
+    _need(dxs, "dxs", (T * k, d), (torch.float32, torch.bfloat16))
+    _need(inv_pos, "inv_pos", (T * k,), _I32)
+    if (dlogits is None) != (wr is None):
+        raise ValueError("dlogits and wr come together")
+    if wr is not None:
+        _need(wr, "wr", (E, d), _BF16)
+        _need(dlogits, "dlogits", (T, E), (torch.float32,))
     dx = torch.empty(T, d, device=dxs.device, dtype=torch.bfloat16)
     with _Probe("unpermute_bwd"):
         L.call("hmoe_unpermute_bwd", L.ptr(dxs), L.dt(dxs), L.ptr(inv_pos), L.ptr(dlogits), L.ptr(wr), T, k, d, E,
