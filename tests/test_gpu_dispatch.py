@@ -18,7 +18,8 @@ def _ref_dispatch(ids_cpu, E, k):
 
 
 @pytest.mark.parametrize("T,E,k,skew", [(512, 8, 2, 0), (16384, 16, 2, 0), (16384, 16, 2, 1), (8192, 128, 8, 0),
-                                        (1, 4, 2, 0), (1000, 3, 3, 1), (5000, 1024, 1, 0)])
+                                        (1, 4, 2, 0), (1000, 3, 3, 1), (5000, 1024, 1, 0),
+                                        (100000, 48, 2, 1)])
 def test_dispatch_bitexact(oracle, T, E, k, skew):
     from trenowanie_generatora_obrazkow_amd import ops
     print(f"dispatch T={T} E={E} k={k} skew={skew}", flush=True)

@@ -461,34 +461,74 @@ __global__ __launch_bounds__(64) void dispatch_hist_kernel(const void* __restric
   for (int e = lane; e < E; e += 64) hist[(int64_t)blockIdx.x * E + e] = run[e];
 }
 
-__global__ __launch_bounds__(256) void dispatch_scan_kernel(int32_t* __restrict__ hist, int nblk, int E,
-                                                            int32_t* __restrict__ counts,
-                                                            int64_t* __restrict__ counts64,
-                                                            int32_t* __restrict__ starts) {
-  __shared__ int cnt[kMaxEDispatch + 1];
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    int s = 0;
-    for (int b = 0; b < nblk; ++b) s += hist[(int64_t)b * E + e];
-    cnt[e] = s;
-    counts[e] = s;
-    if (counts64) counts64[e] = s;
+// Per-expert totals, expert starts and per-(block, expert) first sorted row, in one workgroup of 1024 threads.
+// Thread (g, e) of the G x E grid (G = the largest power of two with G * E <= 1024) owns the histogram blocks
+// [g * C, (g + 1) * C) of expert e (C = ceil(nblk / G)): it sums them, the group sums are scanned per expert, the
+// totals are scanned over the experts by wave prefix sums, and each thread then rewrites its blocks' counts as
+// running first rows.  All integer, so the order of the sums does not matter.
+__global__ __launch_bounds__(1024) void dispatch_scan_kernel(int32_t* __restrict__ hist, int nblk, int E,
+                                                             int32_t* __restrict__ counts,
+                                                             int64_t* __restrict__ counts64,
+                                                             int32_t* __restrict__ starts) {
+  __shared__ int part[1024];              // [G][E] group sums, then their exclusive prefix per expert
+  __shared__ int tot[kMaxEDispatch + 1];  // totals, then exclusive starts
+  __shared__ int wsum[16];
+  const int tid = threadIdx.x;
+  int G = 1;
+  while (G * 2 * E <= 1024) G *= 2;
+  const int C = (nblk + G - 1) / G;
+  const int g = tid / E, e = tid - g * E;
+  const bool mine = g < G;
+  int b0 = 0, b1 = 0;
+  if (mine) {
+    b0 = min(nblk, g * C);
+    b1 = min(nblk, b0 + C);
+    int sum = 0;
+    for (int b = b0; b < b1; ++b) sum += hist[(int64_t)b * E + e];
+    part[tid] = sum;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
+  // exclusive prefix over the groups of each expert, and the expert totals
+  for (int ee = tid; ee < E; ee += 1024) {
     int run = 0;
-    for (int e = 0; e < E; ++e) {
-      int c = cnt[e];
-      cnt[e] = run;
-      starts[e] = run;
-      run += c;
+    for (int gg = 0; gg < G; ++gg) {
+      const int v = part[gg * E + ee];
+      part[gg * E + ee] = run;
+      run += v;
     }
-    starts[E] = run;
+    tot[ee] = run;
+    counts[ee] = run;
+    if (counts64) counts64[ee] = run;
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    int run = cnt[e];
-    for (int b = 0; b < nblk; ++b) {
-      int c = hist[(int64_t)b * E + e];
+  // exclusive scan of the totals over the experts: a wave prefix per 64 experts, then the wave totals
+  const int lane = tid & 63, w = tid >> 6;
+  const int v = tid < E ? tot[tid] : 0;
+  int incl = v;
+#pragma unroll
+  for (int sft = 1; sft < 64; sft <<= 1) {
+    const int o = __shfl_up(incl, sft, 64);
+    if (lane >= sft) incl += o;
+  }
+  if (lane == 63) wsum[w] = incl;
+  __syncthreads();
+  int wbase = 0;
+  for (int ww = 0; ww < w; ++ww) wbase += wsum[ww];
+  __syncthreads();
+  if (tid < E) {
+    tot[tid] = wbase + incl - v;
+    starts[tid] = wbase + incl - v;
+  }
+  if (tid == 0) {
+    int all = 0;
+    for (int ww = 0; ww < 16; ++ww) all += wsum[ww];
+    starts[E] = all;
+  }
+  __syncthreads();
+  if (mine) {
+    int run = tot[e] + part[tid];
+    for (int b = b0; b < b1; ++b) {
+      const int c = hist[(int64_t)b * E + e];
       hist[(int64_t)b * E + e] = run;
       run += c;
     }
@@ -1117,7 +1157,7 @@ int hmoe_dispatch(const void* topk_ids, int ids_dtype, const void* topk_w, int w
                        hist, rank);
     HMOE_CHECK_LAUNCH();
   }
-  hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(256), 0, s, hist, (int)nblk, E, counts, counts64, starts);
+  hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, s, hist, (int)nblk, E, counts, counts64, starts);
   HMOE_CHECK_LAUNCH();
   if (M > 0) {
     if (!order) return HMOE_ERR_ARG;
