@@ -623,6 +623,10 @@ __global__ __launch_bounds__(256) void make_schedule_kernel(const void* __restri
 // ---------------------------------------------------------------------------------------------------------------
 // out[t] = bf16(sum_j y[t*k + j]) (fp32 sum in slot order), or with `add`: bf16(that + add[t]) (bf16 + bf16
 // computed in fp32 and rounded once, as torch adds two bf16 tensors)
+// out[t] = bf16(sum_j y[t*k + j]) (+ add[t], rounded again), one thread per 8 columns of a token.  KT > 0 is the
+// slot count at compile time: the thread issues its KT row loads before the first sum (KT = 0: a runtime loop).
+// Either way the slots are summed in order j = 0, 1, ..., so the result does not depend on KT.
+template <int KT>
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ y, int64_t T, int k, int64_t d,
                                                       const uint16_t* __restrict__ add, uint16_t* __restrict__ out) {
   const int64_t nvec = d / 8;
@@ -631,23 +635,33 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
     const int64_t t = i / nvec, c = i - t * nvec;
     const uint4* src = reinterpret_cast<const uint4*>(y + t * k * d) + c;
     float s[8];
-    {
-      const uint4 v = src[0];
+    auto first = [&](const uint4 v) {
       const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         s[2 * q] = bf_lo(w[q]);
         s[2 * q + 1] = bf_hi(w[q]);
       }
-    }
-    for (int j = 1; j < k; ++j) {
-      const uint4 v = src[j * nvec];
+    };
+    auto accum = [&](const uint4 v) {
       const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         s[2 * q] += bf_lo(w[q]);
         s[2 * q + 1] += bf_hi(w[q]);
       }
+    };
+    const uint4 a = add ? reinterpret_cast<const uint4*>(add + t * d)[c] : make_uint4(0, 0, 0, 0);
+    if constexpr (KT > 0) {
+      uint4 v[KT];
+#pragma unroll
+      for (int j = 0; j < KT; ++j) v[j] = src[j * nvec];
+      first(v[0]);
+#pragma unroll
+      for (int j = 1; j < KT; ++j) accum(v[j]);
+    } else {
+      first(src[0]);
+      for (int j = 1; j < k; ++j) accum(src[j * nvec]);
     }
     uint4 o;
     o.x = pack_bf2(s[0], s[1]);
@@ -655,7 +669,6 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
     o.z = pack_bf2(s[4], s[5]);
     o.w = pack_bf2(s[6], s[7]);
     if (add) {
-      const uint4 a = reinterpret_cast<const uint4*>(add + t * d)[c];
       const uint32_t av[4] = {a.x, a.y, a.z, a.w};
       uint32_t ov[4] = {o.x, o.y, o.z, o.w};
 #pragma unroll
@@ -1000,6 +1013,21 @@ static inline int grid_for(int64_t work, int per_block, int cap = 8192) {
 
 static inline bool al16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+static void combine_launch(const uint16_t* y, int64_t T, int k, int64_t d, const uint16_t* add, uint16_t* out,
+                           int64_t work, hipStream_t s) {
+  const dim3 grid(grid_for(work, 256, 65536));
+#define HMOE_COMBINE(KT) hipLaunchKernelGGL((combine_kernel<KT>), grid, dim3(256), 0, s, y, T, k, d, add, out)
+  switch (k) {
+    case 1: HMOE_COMBINE(1); break;
+    case 2: HMOE_COMBINE(2); break;
+    case 4: HMOE_COMBINE(4); break;
+    case 6: HMOE_COMBINE(6); break;
+    case 8: HMOE_COMBINE(8); break;
+    default: HMOE_COMBINE(0); break;
+  }
+#undef HMOE_COMBINE
+}
+
 static int route_launch(const void* x, int64_t ldx, const void* wr, const float* bias, int64_t T, int64_t d, int E,
                         int k, int renorm, float scaling, float* logits, int32_t* topk_ids, float* topk_w,
                         hipStream_t s) {
@@ -1189,8 +1217,7 @@ int hmoe_combine(const void* y, int64_t T, int k, int64_t d, void* out, hmoe_str
   if (!y || !out || d % 8 || !al16(y) || !al16(out)) return HMOE_ERR_ARG;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int64_t work = T * (d / 8);
-  hipLaunchKernelGGL(combine_kernel, dim3(grid_for(work, 256, 65536)), dim3(256), 0, s,
-                     static_cast<const uint16_t*>(y), T, k, d, nullptr, static_cast<uint16_t*>(out));
+  combine_launch(static_cast<const uint16_t*>(y), T, k, d, nullptr, static_cast<uint16_t*>(out), work, s);
   HMOE_CHECK_LAUNCH();
   return HMOE_OK;
 }
@@ -1201,9 +1228,8 @@ int hmoe_combine_add(const void* y, int64_t T, int k, int64_t d, const void* add
   if (!y || !add || !out || d % 8 || !al16(y) || !al16(add) || !al16(out)) return HMOE_ERR_ARG;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int64_t work = T * (d / 8);
-  hipLaunchKernelGGL(combine_kernel, dim3(grid_for(work, 256, 65536)), dim3(256), 0, s,
-                     static_cast<const uint16_t*>(y), T, k, d, static_cast<const uint16_t*>(add),
-                     static_cast<uint16_t*>(out));
+  combine_launch(static_cast<const uint16_t*>(y), T, k, d, static_cast<const uint16_t*>(add),
+                 static_cast<uint16_t*>(out), work, s);
   HMOE_CHECK_LAUNCH();
   return HMOE_OK;
 }
