@@ -48,10 +48,15 @@ def test_layer_forward_c3_sampled(oracle):
     assert_close_bf16(f32(out)[tok], ref["out"], "out C3 sampled")
 
 
+@pytest.mark.parametrize("tile", ["auto", "L", "S"])
 @pytest.mark.parametrize("T,d,E,k,h,zipf", [(512, 256, 8, 2, 512, 0), (1024, 512, 16, 2, 1024, 1),
                                             (300, 520, 5, 3, 264, 0)])
-def test_layer_backward(oracle, T, d, E, k, h, zipf):
-    print(f"layer bwd T={T} d={d} E={E} k={k} h={h} zipf={zipf}", flush=True)
+def test_layer_backward(oracle, monkeypatch, tile, T, d, E, k, h, zipf):
+    """Forward and backward against the float64 oracle, with the GEMM tile size chosen by the library or forced to
+    256x256 / 128x128 (the partial m-tiles, N tails and row masks of every epilogue on both tile sizes)."""
+    if tile != "auto":
+        monkeypatch.setenv("HMOE_GEMM_TILE", tile)
+    print(f"layer bwd T={T} d={d} E={E} k={k} h={h} zipf={zipf} tile={tile}", flush=True)
     x, wr, wgu, wd = make_inputs(T, d, E, h, seed=T + 1)
     g = torch.Generator().manual_seed(5)
     dout = torch.randn(T, d, generator=g).bfloat16()
