@@ -436,10 +436,20 @@ __global__ __launch_bounds__(64) void dispatch_hist_kernel(const void* __restric
   const int64_t start = (int64_t)blockIdx.x * kFPB;
   const int64_t end = min(M, start + kFPB);
   const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int64_t base = start; base < end; base += 64) {
+  // all of the block's ids are loaded up front (one memory round trip instead of one per 64 ids)
+  constexpr int kSteps = kFPB / 64;
+  int ev[kSteps];
+#pragma unroll
+  for (int i = 0; i < kSteps; ++i) {
+    const int64_t f = start + i * 64 + lane;
+    ev[i] = f < end ? load_id(ids, ids64, f) : -1;
+  }
+#pragma unroll
+  for (int i = 0; i < kSteps; ++i) {
+    const int64_t base = start + i * 64;
+    if (base >= end) break;
     const int64_t f = base + lane;
-    int e = -1;
-    if (f < end) e = load_id(ids, ids64, f);
+    const int e = ev[i];
     const bool valid = e >= 0 && e < E;
     uint64_t peers = __ballot(valid);
     for (int b = 0; b < nbits; ++b) {

@@ -3,7 +3,8 @@
 backward pass -- neither exists in the reference (its MoE path is inference-only, aurora/hf_compat.py:62).
 
 Forward (all hmoe HIP kernels, one stream, no host sync):
-  route_topk -> dispatch (stable counting sort + row permutation) -> gate/up GEMM with fused SwiGLU ->
+  route_topk -> dispatch (stable counting sort; with a backward to follow, also the permuted copy of x) ->
+  gate/up GEMM with fused SwiGLU (rows of x gathered by the GEMM when there is no copy) ->
   down GEMM x routing weight, scattered to (token, slot) order -> combine over the k slots.
 Backward:
   combine_bwd (weighted dY for the down wgrad, routing-weight grads) -> down dgrad (dY rows gathered, routing
@@ -27,8 +28,13 @@ class _MoEFunction(torch.autograd.Function):
         M = T * k
         need_grad = any(ctx.needs_input_grad[:4])
         logits, ids, tw = ops.route_topk(x, wr, k, bias=bias, renorm=renorm)
-        disp = ops.dispatch(ids, E, topk_w=tw, x=x)
-        act, gu = ops.gate_up_swiglu(disp.xs, wgu, disp.counts, M, keep_gu=need_grad)
+        # With a backward to follow, the dispatch writes the permuted copy xs of x (the gate/up weight gradient
+        # reads it again); a forward alone gathers the rows of x inside the gate/up GEMM instead.
+        disp = ops.dispatch(ids, E, topk_w=tw, x=x if need_grad else None, want_inv=need_grad)
+        if need_grad:
+            act, gu = ops.gate_up_swiglu(disp.xs, wgu, disp.counts, M, keep_gu=True)
+        else:
+            act, gu = ops.gate_up_swiglu(x, wgu, disp.counts, M, a_idx=disp.a_idx)
         y, yhat = ops.down_scatter(act, wd, disp.counts, M, disp.w_sorted, disp.order, keep_yhat=need_grad)
         out = ops.combine(y, T, k)
         if need_grad:
