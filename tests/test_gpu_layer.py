@@ -48,6 +48,32 @@ def test_layer_forward_c3_sampled(oracle):
     assert_close_bf16(f32(out)[tok], ref["out"], "out C3 sampled")
 
 
+def test_layer_backward_c5_expert_slice(oracle):
+    """C5 (the C3 shape, forward + backward) at full size.  The weight gradients of an expert depend only on the
+    rows routed to it, and a token's input gradient only on its own slots, so the float64 oracle runs on the tokens
+    that use expert e* (with their other slots): dWd[e*], dWgu[e*] and dx of those tokens from the full-size GPU
+    backward are checked against it; routing is bit-exact for every token."""
+    T, d, E, k, h = 16384, 1536, 16, 2, 4096
+    e_star = 5
+    x, wr, wgu, wd = make_inputs(T, d, E, h, seed=3)
+    g = torch.Generator().manual_seed(4)
+    dout = torch.randn(T, d, generator=g).bfloat16()
+    out, ids, tw, (xg, wrg, wgug, wdg) = _run_layer(x, wr, wgu, wd, k, dout=dout)
+    logits, rids, rw = oracle.route(bits(x), bits(wr), k)
+    np.testing.assert_array_equal(ids.cpu().numpy(), rids)
+    toks = np.nonzero((rids == e_star).any(axis=1))[0]
+    print(f"C5 backward slice: expert {e_star}, {toks.size} tokens", flush=True)
+    xw, dw = f32(wgu), f32(wd)
+    fwd = oracle.moe_forward(f32(x)[toks], rids[toks], rw[toks], xw, dw)
+    ref = oracle.layer_backward(f32(x)[toks], f32(wr), rids[toks], rw[toks], logits[toks], xw, dw, f32(dout)[toks],
+                                fwd=fwd)
+    R = oracle.round_bf16
+    assert_close_bf16(f32(out)[toks], fwd["out"], "out (tokens of e*)")
+    assert_close_bf16(f32(xg.grad)[toks], R(ref["dx"]), "dx (tokens of e*)")
+    assert_close_bf16(f32(wdg.grad)[e_star], R(ref["dwd"][e_star]), "dWd[e*]")
+    assert_close_bf16(f32(wgug.grad)[e_star], R(ref["dwgu"][e_star]), "dWgu[e*]")
+
+
 @pytest.mark.parametrize("tile", ["auto", "L", "S"])
 @pytest.mark.parametrize("T,d,E,k,h,zipf", [(512, 256, 8, 2, 512, 0), (1024, 512, 16, 2, 1024, 1),
                                             (300, 520, 5, 3, 264, 0)])
