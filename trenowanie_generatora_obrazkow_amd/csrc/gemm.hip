@@ -118,6 +118,10 @@ struct KTile {
     const uint32_t vo = (k0 + kBK <= K || k0 + chunk[i] * 8 < K) ? voff[i] : kOOB;
     buf2lds(vo, rsrc, (uint32_t)k0 * 2u, lds_tile + (wave * PER_WAVE + i) * 1024);
   }
+  // the same for a slice known to lie inside K (no tail test)
+  __device__ __forceinline__ void issue_one_full(char* lds_tile, int wave, int i, int k0) const {
+    buf2lds(voff[i], rsrc, (uint32_t)k0 * 2u, lds_tile + (wave * PER_WAVE + i) * 1024);
+  }
   // Lane part of a fragment read address: row w32*32 + lane%32, k-chunk lane/32 (ks = 0), swizzled.  The
   // swizzle of row grp64 + w32*32 + lane%32 is that of lane%32, and chunk 2 + c stored at (2 + c) ^ s = (c ^ s) ^ 2,
   // so the 64-row group and ks parts are compile-time offsets.
@@ -158,6 +162,9 @@ struct MNTile {
   __device__ __forceinline__ void issue_one(char* lds_tile, int wave, int i, int k0) const {
     const uint32_t vo = (k0 + kBK <= Kvalid || k0 + krow[i] < Kvalid) ? voff[i] : kOOB;
     buf2lds(vo, rsrc, (uint32_t)k0 * kstep, lds_tile + (wave * PER_WAVE + i) * 1024);
+  }
+  __device__ __forceinline__ void issue_one_full(char* lds_tile, int wave, int i, int k0) const {
+    buf2lds(voff[i], rsrc, (uint32_t)k0 * kstep, lds_tile + (wave * PER_WAVE + i) * 1024);
   }
   // lane l of instruction (wave w, i): k-row (w*PER_WAVE + i)*KPI + l / CPR, physical chunk l % CPR
   __device__ __forceinline__ static void slot(int wave, int lane, int i, int& k, int& col) {
@@ -212,6 +219,9 @@ struct MNTile8 {
   __device__ __forceinline__ void issue_one(char* lds_tile, int wave, int i, int k0) const {
     const uint32_t vo = (k0 + kBK <= Kvalid || k0 + krow[i] < Kvalid) ? voff[i] : kOOB;
     buf2lds(vo, rsrc, (uint32_t)k0 * kstep, lds_tile + (wave * PER_WAVE + i) * 1024);
+  }
+  __device__ __forceinline__ void issue_one_full(char* lds_tile, int wave, int i, int k0) const {
+    buf2lds(voff[i], rsrc, (uint32_t)k0 * kstep, lds_tile + (wave * PER_WAVE + i) * 1024);
   }
   // lane l of instruction (wave w, i): k-row (w*PER_WAVE + i)*KPI + l / CPR, physical chunk l % CPR; col = the first
   // logical column the slot holds
@@ -687,31 +697,39 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
       }
       // The two MFMA blocks are unconditional (a conditional copy would split the accumulators' live ranges); on
       // the last slice the ks0 read of the "next" slot reads stale LDS that is never used.
-      for (int kt = 0; kt < nk; ++kt) {
+      // FAST iterations (all but the last kNStage, and not the one that refills a partial last slice) refill a
+      // whole slice with two slices issued after slice kt+1: no per-copy tail test, no refill test and no
+      // wait-count selection inside the MFMA stream.
+      auto iter = [&](int kt, auto fast_tag) {
+        constexpr bool FAST = decltype(fast_tag)::value;
         f1 = read(cons, 1);
         mfmas(f0);
         interleave();
-        const int ahead = min(nk - 1, kt + kNStage - 1) - (kt + 1);  // slices issued after slice kt+1
-        if (ahead >= 2)
+        if constexpr (FAST) {
           wait_vm<2 * LOADS>();
-        else if (ahead == 1)
-          wait_vm<LOADS>();
-        else
-          wait_vm<0>();
+        } else {
+          const int ahead = min(nk - 1, kt + kNStage - 1) - (kt + 1);  // slices issued after slice kt+1
+          if (ahead >= 2)
+            wait_vm<2 * LOADS>();
+          else if (ahead == 1)
+            wait_vm<LOADS>();
+          else
+            wait_vm<0>();
+        }
         lds_barrier();
         if constexpr (MODE == KGROUP) {  // (measured: weight gradients run faster with the copies issued together)
-          if (kt + kNStage < nk) issue(kt + kNStage);  // into the slot of slice kt (fill == cons here)
+          if (FAST || kt + kNStage < nk) issue(kt + kNStage);  // into the slot of slice kt (fill == cons here)
           cons += C::STAGE_BYTES;
           if (cons == ring_end) cons = smem;
           f0 = read(cons, 0);
           mfmas(f1);
           interleave();
-          continue;
+          return;
         }
         // Second half: MFMAs on the ks1 fragments, the next slice's ks0 fragment reads and the refill of slice
         // kt's slot with slice kt+4 (fill == cons here), one step per MFMA so the reads and copies issue in its
         // shadow.
-        const bool refill = kt + kNStage < nk;
+        const bool refill = FAST || kt + kNStage < nk;
         const int kr = (kt + kNStage) * kBK;
         char* const dst = fill;
         cons += C::STAGE_BYTES;
@@ -720,6 +738,19 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
           fill += C::STAGE_BYTES;
           if (fill == ring_end) fill = smem;
         }
+        auto copy = [&](int l) {  // copy number l: A's first, then B's
+          if constexpr (FAST) {
+            if (l < TA::PER_WAVE)
+              ta.issue_one_full(dst, wave, l, kr);
+            else if (l < LOADS)
+              tb.issue_one_full(dst + C::A_BYTES, wave, l - TA::PER_WAVE, kr);
+          } else {
+            if (l < TA::PER_WAVE)
+              ta.issue_one(dst, wave, l, kr);
+            else if (l < LOADS)
+              tb.issue_one(dst + C::A_BYTES, wave, l - TA::PER_WAVE, kr);
+          }
+        };
 #pragma unroll
         for (int a = 0; a < FE; ++a)
 #pragma unroll
@@ -730,13 +761,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
               f0.xa[i] = TA::frag(cons, i * C::FSM, loff_a, 0);
             else if (i < FE + C::FN)
               f0.wb[i - FE] = TB::frag(cons + C::A_BYTES, (i - FE) * C::FSN, loff_b, 0);
-            if ((i & 1) && refill) {
-              const int l = i >> 1;  // copy number: A's first, then B's
-              if (l < TA::PER_WAVE)
-                ta.issue_one(dst, wave, l, kr);
-              else if (l < LOADS)
-                tb.issue_one(dst + C::A_BYTES, wave, l - TA::PER_WAVE, kr);
-            }
+            if ((i & 1) && refill) copy(i >> 1);
             __builtin_amdgcn_sched_barrier(0);
           }
         // fragment reads and copies left over when there are fewer MFMAs than reads or copy pairs
@@ -750,12 +775,14 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int l = FE * C::FN / 2; l < LOADS; ++l) {
           if (!refill) break;
-          if (l < TA::PER_WAVE)
-            ta.issue_one(dst, wave, l, kr);
-          else
-            tb.issue_one(dst + C::A_BYTES, wave, l - TA::PER_WAVE, kr);
+          copy(l);
         }
-      }
+      };
+      // iterations whose refill slice kt + kNStage is whole: (kt + kNStage + 1) * kBK <= kvalid
+      const int nfast = max(0, min(nk - kNStage, kvalid / kBK - kNStage));
+      int kt = 0;
+      for (; kt < nfast; ++kt) iter(kt, std::true_type{});
+      for (; kt < nk; ++kt) iter(kt, std::false_type{});
     };
     if constexpr (MODE == MGROUP) {
       const int64_t rows = row_end - row0;
