@@ -705,6 +705,9 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
         f1 = read(cons, 1);
         mfmas(f0);
         interleave();
+        // every MFMA of this half stays ahead of the wait and barrier below: the trailing ones then run while the
+        // last fragment reads complete (the barrier waits for those reads)
+        __builtin_amdgcn_sched_barrier(0);
         if constexpr (FAST) {
           wait_vm<2 * LOADS>();
         } else {
