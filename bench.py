@@ -283,6 +283,31 @@ def cpu_baseline(w, budget_s=15.0):
                       f"{med * 1e3:.1f} ms per sample step"}
 
 
+def library_ceiling(M, N, K, reps=10):
+    """Dense bf16 (M, K) @ (K, N) through torch.matmul (the vendor BLAS, hipBLASLt on gfx950) on the same GPU: the
+    practical ceiling the grouped GEMM is compared with (same M, N, K; no gather, no expert boundaries, no fused
+    epilogue)."""
+    import torch
+
+    g = torch.Generator(device="cuda").manual_seed(1)
+    a = torch.randn(M, K, device="cuda", dtype=torch.bfloat16, generator=g)
+    b = torch.randn(K, N, device="cuda", dtype=torch.bfloat16, generator=g)
+    for _ in range(3):
+        c = a @ b
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        c = a @ b
+    e.record()
+    torch.cuda.synchronize()
+    us = s.elapsed_time(e) * 1e3 / reps
+    del a, b, c
+    blas = str(torch.backends.cuda.preferred_blas_library()).split(".")[-1]
+    blas = {"Cublaslt": "hipBLASLt", "Cublas": "rocBLAS"}.get(blas, blas)  # torch's enum names on ROCm
+    return {"kernel": f"torch.matmul bf16, dense ({M} x {K}) @ ({K} x {N}), BLAS backend {blas}",
+            "M": M, "N": N, "K": K, "avg_launch_us": round(us, 2), "tflops": round(2 * M * N * K / us / 1e6, 2)}
+
+
 def load_traffic(workload):
     p = os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
     if os.path.exists(p):
@@ -324,6 +349,8 @@ def main():
     dom_flops = 4 * M * w["d"] * w["h"]  # gate/up: 2 * M * d * (2h)
     dom_tflops = dom_flops / (dom_ms * 1e-3) / 1e12
     traffic = load_traffic(args.workload)
+    lib = library_ceiling(M, 2 * w["h"], w["d"])
+    lib["achieved_over_library"] = round(dom_tflops / lib["tflops"], 4)
     res = {
         "metric": METRIC,
         "value": round(tflops, 2),
@@ -349,7 +376,8 @@ def main():
                      "achieved": round(dom_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(dom_tflops / PEAK_BF16_TFLOPS, 4),
                      "flops_per_launch": dom_flops, "avg_launch_us": round(dom_ms * 1e3, 2),
-                     "traffic": traffic.get("bytes_per_launch") if traffic else None},
+                     "traffic": traffic.get("bytes_per_launch") if traffic else None,
+                     "library_ceiling": lib},
         "kernels_us": {k_: round(v, 1) for k_, v in kern.items()},
     }
     if pz:
