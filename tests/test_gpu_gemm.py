@@ -96,6 +96,36 @@ def test_grouped_mm_partial_tiles(oracle, tile, counts):
     assert_close_bf16(f32(y), ref, "partial int8")
 
 
+@pytest.mark.parametrize("h", [320, 192, 208, 64])
+@pytest.mark.parametrize("wdt", ["bf16", "int8"])
+def test_gate_up_swiglu_partial_n(oracle, tile, h, wdt):
+    """gate/up + SwiGLU where the last n-tile holds at most 64 of its 128 gate columns (h = 320, 192, 64: the large
+    tile runs that n-tile on its live fragments only) or more (h = 208), bf16 and int8 weights, against the oracle's
+    act rows."""
+    from trenowanie_generatora_obrazkow_amd import ops
+    print(f"gate_up partial n h={h} w={wdt} tile={tile}", flush=True)
+    T, d, E, k = 600, 256, 6, 2
+    g = torch.Generator().manual_seed(h)
+    x = torch.randn(T, d, generator=g).bfloat16()
+    wgu = (torch.randn(E, d, 2 * h, generator=g) * 0.05).bfloat16()
+    wd = (torch.randn(E, h, d, generator=g) * 0.05).bfloat16()
+    ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)])
+    tw = torch.rand(T, k, generator=g).softmax(-1)
+    dev = torch.device("cuda")
+    disp = ops.dispatch(ids.int().to(dev), E, topk_w=tw.to(dev), want_inv=False)
+    if wdt == "int8":
+        q, s = oracle.quant_int8(f32(wgu))
+        act, _ = ops.gate_up_swiglu(x.to(dev), torch.from_numpy(q).to(dev), disp.counts, T * k, a_idx=disp.a_idx,
+                                    wgu_s=torch.from_numpy(s).bfloat16().to(dev))
+        ref = oracle.moe_forward(f32(x), ids.numpy(), tw.numpy(), q.astype(np.float32), f32(wd),
+                                 wgu_s=s.astype(np.float64))
+    else:
+        act, _ = ops.gate_up_swiglu(x.to(dev), wgu.to(dev), disp.counts, T * k, a_idx=disp.a_idx)
+        ref = oracle.moe_forward(f32(x), ids.numpy(), tw.numpy(), f32(wgu), f32(wd))
+    order = disp.order.cpu().numpy().astype(np.int64)
+    assert_close_bf16(f32(act), ref["act"][order], f"act h={h} {wdt}")
+
+
 @pytest.mark.parametrize("M,P,N,E,skew", [(4096, 256, 512, 8, 0), (3000, 520, 264, 5, 1), (777, 128, 1024, 16, 1)])
 def test_grouped_wgrad(oracle, tile, M, P, N, E, skew):
     from trenowanie_generatora_obrazkow_amd import ops

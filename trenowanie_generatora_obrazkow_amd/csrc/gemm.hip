@@ -648,25 +648,30 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
       bf16x8 xa[C::FM], wb[C::FN];
     };
     static_assert(kNStage == 4 && kBK == 32, "pipeline written for a 4-deep ring of two-step slices");
-    auto main_loop = [&](auto fe_tag) {
+    // NL = live B fragments: all FN, or, for a SwiGLU n-tile whose gate (and up) columns fill at most half of
+    // their 128, the first fragment of each half (the other half's columns are past N: their copies are zeros).
+    auto main_loop = [&](auto fe_tag, auto nl_tag) {
       constexpr int FE = decltype(fe_tag)::value;
-      constexpr int RD = FE * (A_MN ? 2 : 1) + C::FN * (B_MN ? 2 : 1);  // LDS reads per k16 step
-      constexpr int NMF = FE * C::FN;                                      // MFMAs per k16 step
+      constexpr int NL = decltype(nl_tag)::value;
+      static_assert(NL == C::FN || (NL == 2 && C::FN == 4), "live B fragments: all, or one per SwiGLU half");
+      auto bf = [](int j) { return NL == C::FN ? j : j * (C::FN / 2); };  // fragment of live fragment j
+      constexpr int RD = FE * (A_MN ? 2 : 1) + NL * (B_MN ? 2 : 1);  // LDS reads per k16 step
+      constexpr int NMF = FE * NL;                                     // MFMAs per k16 step
       constexpr int PAIRS = RD < NMF ? RD : NMF;
       auto read = [&](const char* slot, int ks) {
         Frags f;
 #pragma unroll
         for (int a = 0; a < FE; ++a) f.xa[a] = TA::frag(slot, a * C::FSM, loff_a, ks);
 #pragma unroll
-        for (int b = 0; b < C::FN; ++b) f.wb[b] = TB::frag(slot + C::A_BYTES, b * C::FSN, loff_b, ks);
+        for (int j = 0; j < NL; ++j) f.wb[bf(j)] = TB::frag(slot + C::A_BYTES, bf(j) * C::FSN, loff_b, ks);
         return f;
       };
       auto mfmas = [&](const Frags f) {
 #pragma unroll
         for (int a = 0; a < FE; ++a)
 #pragma unroll
-          for (int b = 0; b < C::FN; ++b)
-            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.wb[b], f.xa[a], acc[a][b], 0, 0, 0);
+          for (int j = 0; j < NL; ++j)
+            acc[a][bf(j)] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.wb[bf(j)], f.xa[a], acc[a][bf(j)], 0, 0, 0);
       };
       // one LDS read after each MFMA while both last, then whichever is left
       auto interleave = [&]() {
@@ -757,26 +762,26 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int a = 0; a < FE; ++a)
 #pragma unroll
-          for (int b = 0; b < C::FN; ++b) {
-            const int i = a * C::FN + b;
+          for (int j = 0; j < NL; ++j) {
+            const int i = a * NL + j, b = bf(j);
             acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f1.wb[b], f1.xa[a], acc[a][b], 0, 0, 0);
             if (i < FE)
               f0.xa[i] = TA::frag(cons, i * C::FSM, loff_a, 0);
-            else if (i < FE + C::FN)
-              f0.wb[i - FE] = TB::frag(cons + C::A_BYTES, (i - FE) * C::FSN, loff_b, 0);
+            else if (i < FE + NL)
+              f0.wb[bf(i - FE)] = TB::frag(cons + C::A_BYTES, bf(i - FE) * C::FSN, loff_b, 0);
             if ((i & 1) && refill) copy(i >> 1);
             __builtin_amdgcn_sched_barrier(0);
           }
         // fragment reads and copies left over when there are fewer MFMAs than reads or copy pairs
 #pragma unroll
-        for (int i = FE * C::FN; i < FE + C::FN; ++i) {
+        for (int i = FE * NL; i < FE + NL; ++i) {
           if (i < FE)
             f0.xa[i] = TA::frag(cons, i * C::FSM, loff_a, 0);
           else
-            f0.wb[i - FE] = TB::frag(cons + C::A_BYTES, (i - FE) * C::FSN, loff_b, 0);
+            f0.wb[bf(i - FE)] = TB::frag(cons + C::A_BYTES, bf(i - FE) * C::FSN, loff_b, 0);
         }
 #pragma unroll
-        for (int l = FE * C::FN / 2; l < LOADS; ++l) {
+        for (int l = FE * NL / 2; l < LOADS; ++l) {
           if (!refill) break;
           copy(l);
         }
@@ -787,16 +792,28 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
       for (; kt < nfast; ++kt) iter(kt, std::true_type{});
       for (; kt < nk; ++kt) iter(kt, std::false_type{});
     };
+    // a SwiGLU n-tile whose gate columns end within the first 64 of its 128 (e.g. the last n-tile at h = 320)
+    // runs with the live B fragments only
+    constexpr bool NHALF = EPI == EPI_SWIGLU && C::FN == 4;
+    auto run_loop = [&](auto fe_tag) {
+      if constexpr (NHALF) {
+        if (p.N - n0 <= C::BN / 4) {
+          main_loop(fe_tag, std::integral_constant<int, 2>{});
+          return;
+        }
+      }
+      main_loop(fe_tag, std::integral_constant<int, C::FN>{});
+    };
     if constexpr (MODE == MGROUP) {
       const int64_t rows = row_end - row0;
       if (C::FM >= 4 && rows <= C::FSM)
-        main_loop(std::integral_constant<int, 1>{});
+        run_loop(std::integral_constant<int, 1>{});
       else if (C::FM >= 4 && rows <= 2 * C::FSM)
-        main_loop(std::integral_constant<int, 2>{});
+        run_loop(std::integral_constant<int, 2>{});
       else
-        main_loop(std::integral_constant<int, C::FM>{});
+        run_loop(std::integral_constant<int, C::FM>{});
     } else {
-      main_loop(std::integral_constant<int, C::FM>{});
+      run_loop(std::integral_constant<int, C::FM>{});
     }
     // fragment rows holding tile rows (the epilogue passes to run)
     const int fe_rows = MODE == MGROUP ? (int)min((row_end - row0 + C::FSM - 1) / C::FSM, (int64_t)C::FM) : C::FM;
@@ -1134,16 +1151,18 @@ static inline bool pick_large(int64_t tiles_large) {
 }
 
 // Row-grouped launches take the small tiles also when the large ones would pad the output columns noticeably more
-// (e.g. 320 SwiGLU columns: 384 in 128-column tiles, 320 in 64-column ones) or when K is short (fewer than 16
-// slices: a tile's fixed cost, prologue and epilogue, then outweighs its main loop).  Measured on MI355X: the
-// BailingMoeV2 block (h = 320, K = 320 for down) runs 5% faster on small tiles; the C3/C5 shapes 30% slower.
+// (a SwiGLU n-tile with at most 64 live columns of 128 counts as 64: its main loop skips the dead half) or when K is
+// short (fewer than 16 slices: a tile's fixed cost, prologue and epilogue, then outweighs its main loop).  Measured
+// on MI355X: the C3/C5 shapes run 30% slower on small tiles; the BailingMoeV2 down GEMM (K = 320) 4% faster.
 template <int EPI>
 static bool pick_large_mgroup(int64_t tiles_large, int64_t ncols, int64_t K) {
   const int f = env_force();
   if (f) return f == 1;
   if (!pick_large(tiles_large)) return false;
   const int64_t bl = EPI == EPI_SWIGLU ? CfgL::BN / 2 : CfgL::BN, bs = EPI == EPI_SWIGLU ? CfgS::BN / 2 : CfgS::BN;
-  const int64_t padl = (ncols + bl - 1) / bl * bl, pads = (ncols + bs - 1) / bs * bs;
+  int64_t padl = (ncols + bl - 1) / bl * bl;
+  const int64_t pads = (ncols + bs - 1) / bs * bs;
+  if (EPI == EPI_SWIGLU && ncols % bl && ncols % bl <= bl / 2) padl -= bl / 2;  // a half-live last n-tile runs at half width
   if (padl * 10 > pads * 11) return false;  // > 10% more padded columns on large tiles
   return K >= 16 * kBK;
 }
