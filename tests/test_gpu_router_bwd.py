@@ -12,7 +12,8 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("T,d,E,k,renorm", [(1000, 1536, 16, 2, True), (777, 520, 40, 4, True),
-                                            (300, 1024, 8, 2, False), (129, 2056, 128, 8, True)])
+                                            (300, 1024, 8, 2, False), (129, 2056, 128, 8, True),
+                                            (333, 1024, 16, 4, True), (5, 264, 12, 3, True)])
 def test_router_bwd_and_unpermute(oracle, T, d, E, k, renorm):
     from trenowanie_generatora_obrazkow_amd import ops
     print(f"router bwd T={T} d={d} E={E} k={k} renorm={renorm}", flush=True)

@@ -21,6 +21,8 @@
 // accumulator holds one output row and 4 consecutive output columns per group -> 8-byte bf16 / 16-byte fp32 stores.
 #include "hmoe_common.h"
 
+#include <atomic>
+
 namespace hmoe {
 
 constexpr int kBK = 32;      // k per LDS slice
@@ -1080,30 +1082,30 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
 // ----------------------------------------------------------------------------------------------------------------
 // Launch helpers
 // ----------------------------------------------------------------------------------------------------------------
-static int g_num_cus[64];
+static std::atomic<int> g_num_cus[64];  // per-device CU count (0 = not yet read); host threads may race to fill it
 
 static int num_cus() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return -1;
-  if (g_num_cus[dev] == 0) {
-    int n = 0;
+  int n = g_num_cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return -1;
-    g_num_cus[dev] = n;
+    g_num_cus[dev].store(n, std::memory_order_relaxed);
   }
-  return g_num_cus[dev];
+  return n;
 }
 
 template <class C, int MODE, bool A_MN, bool B_MN, int EPI>
 static int launch(const GemmParams& p, int64_t tiles_upper, hipStream_t s) {
   auto kern = grouped_gemm_kernel<C, MODE, A_MN, B_MN, EPI>;
-  static bool attr_set[64] = {};
+  static std::atomic<bool> attr_set[64];  // per device: the (idempotent) attribute call is done
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return HMOE_ERR_DEVICE;
-  if (!attr_set[dev]) {
+  if (!attr_set[dev].load(std::memory_order_acquire)) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                             C::LDS_BYTES) != hipSuccess)
       return HMOE_ERR_LAUNCH;
-    attr_set[dev] = true;
+    attr_set[dev].store(true, std::memory_order_release);
   }
   const int cus = num_cus();
   if (cus <= 0) return HMOE_ERR_DEVICE;

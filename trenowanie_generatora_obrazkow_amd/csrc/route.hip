@@ -810,6 +810,72 @@ __global__ __launch_bounds__(256) void router_dlogits_kernel(const float* __rest
   }
 }
 
+// The same for E <= 16: four tokens per wave, 16 lanes each (lane l: token l / 16, expert l % 16).  The 16-lane
+// butterflies give the 64-lane ones' values bit for bit (those only add exact zeros / take maxima with -inf from
+// the lanes past E).
+__global__ __launch_bounds__(256) void router_dlogits16_kernel(const float* __restrict__ logits,
+                                                               const int32_t* __restrict__ ids,
+                                                               const float* __restrict__ dtw, int64_t T, int E, int k,
+                                                               int renorm, float scaling,
+                                                               float* __restrict__ dlogits) {
+  const int lane = threadIdx.x & 63;
+  const int e = lane & 15, seg = lane & ~15;
+  const int nwaves = blockDim.x >> 6;
+  for (int64_t t0 = ((int64_t)blockIdx.x * nwaves + (threadIdx.x >> 6)) * 4; t0 < T;
+       t0 += (int64_t)gridDim.x * nwaves * 4) {
+    const int64_t t = t0 + (lane >> 4);
+    const bool live = t < T;
+    const int64_t tc = live ? t : T - 1;  // rows past T read the last row and write nothing
+    const float lg = e < E ? logits[tc * E + e] : -__builtin_inff();
+    float m = lg;
+    m = bfly_max<8>(m);
+    m = bfly_max<4>(m);
+    m = bfly_max<2>(m);
+    m = bfly_max<1>(m);
+    const float ex = e < E ? hexp(__fsub_rn(lg, m)) : 0.0f;
+    float S = ex;
+    S = bfly_add<8>(S);
+    S = bfly_add<4>(S);
+    S = bfly_add<2>(S);
+    S = bfly_add<1>(S);
+    const float p = __fdiv_rn(ex, S);
+    float sp[kMaxK], dw[kMaxK];
+    int se[kMaxK];
+    float ssum = 0.0f, sdot = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) {
+      sp[j] = 0.0f;
+      dw[j] = 0.0f;
+      se[j] = -1;
+      if (j < k) {
+        se[j] = ids[tc * k + j];
+        sp[j] = __shfl(se[j] == e ? p : 0.0f, seg | (se[j] & 15), 64);
+        dw[j] = dtw[tc * k + j] * scaling;
+        ssum += sp[j];
+        sdot += dw[j] * sp[j];
+      }
+    }
+    const float den = ssum + 1e-20f;
+    float dsel[kMaxK];
+    float pdp = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) {
+      dsel[j] = 0.0f;
+      if (j < k) {
+        dsel[j] = renorm ? dw[j] / den - sdot / (den * den) : dw[j];
+        pdp += sp[j] * dsel[j];
+      }
+    }
+    if (live && e < E) {
+      float dp = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kMaxK; ++j)
+        if (j < k && se[j] == e) dp += dsel[j];
+      dlogits[t * E + e] = p * (dp - pdp);
+    }
+  }
+}
+
 // dwr = dlogits^T x.  A chunk of kDwrWaves * kDwrTok tokens per workgroup; wave w sums its kDwrTok tokens in token
 // order for 8 columns per lane and up to kDwrEG experts per pass (dlogits of a token are wave-uniform scalar loads);
 // the four waves' sums are added in wave order through LDS and stored as the chunk's partial.  The chunk partials
@@ -898,28 +964,42 @@ __global__ __launch_bounds__(256) void router_dwr_partial_kernel(const float* __
   }
 }
 
-// out[i] = sum over chunks c (in order) of part[c][i]; block 256 = 64 outputs x 4 chunk quarters, the quarter sums
-// added in quarter order.
-__global__ __launch_bounds__(256) void router_dwr_reduce_kernel(const float* __restrict__ part, int nchunk, int E,
-                                                                int64_t d, void* __restrict__ dwr, int dwr_bf16) {
-  __shared__ float red[3][64];
+// out[i] = sum over chunks c of part[c][i]: block 1024 = 64 outputs x kRedGroups chunk groups; each group adds its
+// chunks in order (eight loads in flight), then the group sums are added in group order, so the result does not
+// depend on the launch.
+constexpr int kRedGroups = 16;
+
+__global__ __launch_bounds__(1024) void router_dwr_reduce_kernel(const float* __restrict__ part, int nchunk, int E,
+                                                                 int64_t d, void* __restrict__ dwr, int dwr_bf16) {
+  __shared__ float red[kRedGroups][64];
   const int64_t total = (int64_t)E * d;
   const int j = threadIdx.x & 63, q = threadIdx.x >> 6;
-  const int per = (nchunk + 3) / 4;
-  const int c0 = q * per, c1 = min(nchunk, c0 + per);
+  const int per = (nchunk + kRedGroups - 1) / kRedGroups;
+  const int c0 = min(nchunk, q * per), c1 = min(nchunk, c0 + per);
   for (int64_t base = (int64_t)blockIdx.x * 64; base < total; base += (int64_t)gridDim.x * 64) {
     const int64_t i = base + j;
     float s = 0.0f;
-    if (i < total)
-      for (int c = c0; c < c1; ++c) s += part[(int64_t)c * total + i];
-    if (q > 0) red[q - 1][j] = s;
+    if (i < total) {
+      int c = c0;
+      for (; c + 8 <= c1; c += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = part[(int64_t)(c + u) * total + i];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += v[u];
+      }
+      for (; c < c1; ++c) s += part[(int64_t)c * total + i];
+    }
+    red[q][j] = s;
     __syncthreads();
     if (q == 0 && i < total) {
-      s = ((s + red[0][j]) + red[1][j]) + red[2][j];
+      float r = red[0][j];
+#pragma unroll
+      for (int g = 1; g < kRedGroups; ++g) r += red[g][j];
       if (dwr_bf16)
-        reinterpret_cast<uint16_t*>(dwr)[i] = (uint16_t)f2bf(s);
+        reinterpret_cast<uint16_t*>(dwr)[i] = (uint16_t)f2bf(r);
       else
-        reinterpret_cast<float*>(dwr)[i] = s;
+        reinterpret_cast<float*>(dwr)[i] = r;
     }
     __syncthreads();
   }
@@ -1275,8 +1355,12 @@ int hmoe_router_bwd(const float* logits, const int32_t* topk_ids, const float* d
   if (dwr && (!workspace || workspace_bytes < hmoe_router_bwd_workspace_size(T, E, d))) return HMOE_ERR_WORKSPACE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (T > 0) {
-    hipLaunchKernelGGL(router_dlogits_kernel, dim3(grid_for(T, 4, 8192)), dim3(256), 0, s, logits, topk_ids,
-                       dtopk_w, T, E, k, renorm, scaling, dlogits);
+    if (E <= 16)
+      hipLaunchKernelGGL(router_dlogits16_kernel, dim3(grid_for(T, 16, 8192)), dim3(256), 0, s, logits, topk_ids,
+                         dtopk_w, T, E, k, renorm, scaling, dlogits);
+    else
+      hipLaunchKernelGGL(router_dlogits_kernel, dim3(grid_for(T, 4, 8192)), dim3(256), 0, s, logits, topk_ids,
+                         dtopk_w, T, E, k, renorm, scaling, dlogits);
     HMOE_CHECK_LAUNCH();
   }
   if (dwr) {
@@ -1287,7 +1371,7 @@ int hmoe_router_bwd(const float* logits, const int32_t* topk_ids, const float* d
                          dlogits, static_cast<const uint16_t*>(x), ldx, T, E, d, part);
       HMOE_CHECK_LAUNCH();
     }
-    hipLaunchKernelGGL(router_dwr_reduce_kernel, dim3(grid_for((int64_t)E * d, 64, 4096)), dim3(256), 0, s, part,
+    hipLaunchKernelGGL(router_dwr_reduce_kernel, dim3(grid_for((int64_t)E * d, 64, 4096)), dim3(1024), 0, s, part,
                        nchunk, E, d, dwr, dwr_dtype == HMOE_DT_BF16);
     HMOE_CHECK_LAUNCH();
   }
