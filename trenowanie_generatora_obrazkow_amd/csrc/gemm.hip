@@ -246,13 +246,14 @@ struct MNTile8 {
     typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
     const int b = grp64 / 64;
     const i32x2 v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(lds_tile + loff + ks * 16 * ROWS + 16 * b));
-    // signed bytes -> exact floats (|q| <= 127 has at most 7 significant bits) -> bf16
-    const uint32_t lo = (uint32_t)v[0] ^ 0x80808080u, hi = (uint32_t)v[1] ^ 0x80808080u;
+    // signed bytes -> exact floats (|q| <= 128 has at most 8 significant bits) -> bf16; each byte converts in one
+    // instruction (a sign-extending byte select on the int -> float conversion)
+    const uint32_t lo = (uint32_t)v[0], hi = (uint32_t)v[1];
     float f[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      f[j] = (float)((lo >> (8 * j)) & 0xffu) - 128.0f;
-      f[4 + j] = (float)((hi >> (8 * j)) & 0xffu) - 128.0f;
+      f[j] = (float)(int8_t)(lo >> (8 * j));
+      f[4 + j] = (float)(int8_t)(hi >> (8 * j));
     }
     typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
     const u32x4 w = {cvt_bf2(f[0], f[1]), cvt_bf2(f[2], f[3]), cvt_bf2(f[4], f[5]), cvt_bf2(f[6], f[7])};
