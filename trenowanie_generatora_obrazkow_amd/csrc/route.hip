@@ -303,19 +303,21 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restr
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// BailingMoeV2 (sigmoid, group-limited) router.  A workgroup of 4 waves routes 4 x kSgTW tokens.  The router weight
+// BailingMoeV2 (sigmoid, group-limited) router.  A workgroup of 8 waves routes 8 x kSgTW tokens (two per wave: four
+// waves per SIMD at T = 8192, where four tokens per wave left two and measured 25% slower).  The router weight
 // and the workgroup's token values stream through LDS in chunks of 64 elements (double-buffered): weight rows as
 // bf16 with a row pitch of kSgPitch bytes (the lanes' 16-byte reads of 64 consecutive rows fall on distinct banks),
 // token values widened to fp32 once when staged and read back as wave-uniform broadcasts.  Lane l owns experts l,
 // l + 64, ...; each logit is the sequential fma sum over the row in element order (x[0]*w[0] first), and each
 // 8-element piece of weight widened to fp32 once serves the wave's kSgTW tokens.
 // ---------------------------------------------------------------------------------------------------------------
-constexpr int kSgTW = 4, kSgChunk = 64, kSgPitch = 144;
-constexpr int kSgTok = 4 * kSgTW;                    // tokens per workgroup
+constexpr int kSgTW = 2, kSgChunk = 64, kSgPitch = 144;
+constexpr int kSgWaves = 8, kSgThreads = 64 * kSgWaves;
+constexpr int kSgTok = kSgWaves * kSgTW;             // tokens per workgroup
 constexpr int kSgXBytes = kSgTok * kSgChunk * 4;     // fp32 token values per chunk buffer
 
 template <int EPL>
-__global__ __launch_bounds__(256) void route_sigmoid_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+__global__ __launch_bounds__(kSgThreads) void route_sigmoid_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                             const uint16_t* __restrict__ wr,
                                                             const float* __restrict__ bias, int T, int d, int E,
                                                             int k, float scaling, float* __restrict__ scores,
@@ -326,7 +328,7 @@ __global__ __launch_bounds__(256) void route_sigmoid_kernel(const uint16_t* __re
   extern __shared__ __attribute__((aligned(16))) char s_w[];
   constexpr int ER = EPL * 64;       // expert rows staged (rows past E are zero)
   constexpr int PIECES = ER * 8;     // 16-byte weight pieces per chunk
-  constexpr int PPT = PIECES / 256;  // weight pieces per thread
+  constexpr int PPT = PIECES / kSgThreads;  // weight pieces per thread
   char* const s_x = s_w + 2 * ER * kSgPitch;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -337,7 +339,7 @@ __global__ __launch_bounds__(256) void route_sigmoid_kernel(const uint16_t* __re
   auto load_chunk = [&](int c) {
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
-      const int pc = tid + 256 * j, e = pc >> 3, el = c * kSgChunk + (pc & 7) * 8;
+      const int pc = tid + kSgThreads * j, e = pc >> 3, el = c * kSgChunk + (pc & 7) * 8;
       stage[j] = (e < E && el < d) ? *reinterpret_cast<const uint4*>(wr + (int64_t)e * d + el) : make_uint4(0, 0, 0, 0);
     }
     if (tid < kSgTok * 8) {
@@ -348,7 +350,7 @@ __global__ __launch_bounds__(256) void route_sigmoid_kernel(const uint16_t* __re
   auto store_chunk = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
-      const int pc = tid + 256 * j;
+      const int pc = tid + kSgThreads * j;
       *reinterpret_cast<uint4*>(s_w + (buf * ER + (pc >> 3)) * kSgPitch + (pc & 7) * 16) = stage[j];
     }
     if (tid < kSgTok * 8) {
@@ -1225,7 +1227,7 @@ int hmoe_route_sigmoid_group(const void* x, int64_t ldx, const void* wr, const f
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* wp = static_cast<const uint16_t*>(wr);
 #define HMOE_SG(EP)                                                                                             \
-  hipLaunchKernelGGL(route_sigmoid_kernel<EP>, dim3(grid), dim3(256), lds, s, xp, ldx, wp, expert_bias, (int)T, \
+  hipLaunchKernelGGL(route_sigmoid_kernel<EP>, dim3(grid), dim3(kSgThreads), lds, s, xp, ldx, wp, expert_bias, (int)T, \
                      (int)d, E, k, scaling, scores, topk_ids, topk_w, n_group, topk_group)
   if (epl == 1)
     HMOE_SG(1);
