@@ -421,7 +421,7 @@ __global__ __launch_bounds__(kSgThreads) void route_sigmoid_kernel(const uint16_
 // ballots: a lane's peers are the lanes whose id agrees on every bit).  Pass 2 (one workgroup): per-expert totals,
 // expert starts, and per-(block, expert) first sorted row.  Pass 3: positions, index arrays and the row copy.
 // ---------------------------------------------------------------------------------------------------------------
-constexpr int kFPB = 1024;       // flat rows per histogram block
+constexpr int kFPB = 256;        // flat rows per histogram block (one wave each: 128 waves at M = 32768)
 constexpr int kMaxEDispatch = 1024;
 
 __device__ __forceinline__ int load_id(const void* ids, int is64, int64_t f) {
@@ -496,7 +496,15 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(int32_t* __restrict
     b0 = min(nblk, g * C);
     b1 = min(nblk, b0 + C);
     int sum = 0;
-    for (int b = b0; b < b1; ++b) sum += hist[(int64_t)b * E + e];
+    int b = b0;
+    for (; b + 8 <= b1; b += 8) {  // eight loads in flight
+      int v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = hist[(int64_t)(b + u) * E + e];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) sum += v[u];
+    }
+    for (; b < b1; ++b) sum += hist[(int64_t)b * E + e];
     part[tid] = sum;
   }
   __syncthreads();
@@ -539,7 +547,18 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(int32_t* __restrict
   __syncthreads();
   if (mine) {
     int run = tot[e] + part[tid];
-    for (int b = b0; b < b1; ++b) {
+    int b = b0;
+    for (; b + 8 <= b1; b += 8) {
+      int v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = hist[(int64_t)(b + u) * E + e];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        hist[(int64_t)(b + u) * E + e] = run;
+        run += v[u];
+      }
+    }
+    for (; b < b1; ++b) {
       const int c = hist[(int64_t)b * E + e];
       hist[(int64_t)b * E + e] = run;
       run += c;
