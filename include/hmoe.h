@@ -178,7 +178,8 @@ int hmoe_gate_up_dgrad(const void* dgu, const void* wgu, int64_t E, int64_t d, i
 
 /* Weight gradients of :79 and :81: dw[e] = a[rows of e]^T @ b[rows of e] (fp32 accumulation over the expert's
  * ragged row range, no split, deterministic); a (M, P) row stride lda, b (M, N) row stride ldb, both bf16 in
- * sorted order; dw (E, P, N) fp32 or bf16 (dw_dtype).  Experts with no rows get zeros.  P, N % 8 == 0. */
+ * sorted order; dw (E, P, N) fp32 or bf16 (dw_dtype).  Experts with no rows get zeros (M = 0: all of dw, and a,
+ * b may be NULL).  P, N % 8 == 0. */
 int hmoe_grouped_wgrad(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t E, int64_t P, int64_t N,
                        const void* counts, int counts_dtype, int64_t M, void* dw, int dw_dtype,
                        hmoe_stream_t stream);
@@ -187,7 +188,8 @@ int hmoe_grouped_wgrad(const void* a, int64_t lda, const void* b, int64_t ldb, i
 size_t hmoe_router_bwd_workspace_size(int64_t T, int E, int64_t d);
 
 /* Router backward (softmax -> top-k gather -> renormalise, as in hmoe_route_topk): dlogits (T, E) fp32 from
- * dtopk_w (T, k) fp32, and dwr (E, d) = dlogits^T @ x (fp32 or bf16 per dwr_dtype; fixed-order reduction). */
+ * dtopk_w (T, k) fp32, and dwr (E, d) = dlogits^T @ x (fp32 or bf16 per dwr_dtype; fixed-order reduction).
+ * T = 0 writes zeros to dwr; the per-token pointers may then be NULL. */
 int hmoe_router_bwd(const float* logits, const int32_t* topk_ids, const float* dtopk_w, int64_t T, int E, int k,
                     int renorm, float scaling, const void* x, int64_t ldx, int64_t d, float* dlogits, void* dwr,
                     int dwr_dtype, void* workspace, size_t workspace_bytes, hmoe_stream_t stream);

@@ -34,6 +34,32 @@ def test_layer_forward(oracle, T, d, E, k, h):
     assert_close_bf16(f32(out), ref["out"], "out")
 
 
+@pytest.mark.parametrize("T", [0, 1])
+def test_layer_empty_and_single_token(oracle, T):
+    """No tokens: forward and backward run and return empty / zero gradients. One token: forward and backward match
+    the oracle (every expert but k empty)."""
+    print(f"layer T={T}", flush=True)
+    d, E, k, h = 256, 8, 2, 512
+    x, wr, wgu, wd = make_inputs(max(T, 1), d, E, h, seed=7)
+    x = x[:T]
+    dout = torch.randn(T, d, generator=torch.Generator().manual_seed(8)).bfloat16()
+    out, ids, tw, (xg, wrg, wgug, wdg) = _run_layer(x, wr, wgu, wd, k, dout=dout)
+    assert out.shape == (T, d) and ids.shape == (T, k) and tw.shape == (T, k)
+    if T == 0:
+        for g in (wrg.grad, wgug.grad, wdg.grad):
+            assert g is not None and not g.float().abs().any()
+        assert xg.grad.shape == (0, d)
+        return
+    logits, rids, rw = oracle.route(bits(x), bits(wr), k)
+    np.testing.assert_array_equal(ids.cpu().numpy(), rids)
+    fwd = oracle.moe_forward(f32(x), rids, rw, f32(wgu), f32(wd))
+    assert_close_bf16(f32(out), fwd["out"], "out")
+    ref = oracle.layer_backward(f32(x), f32(wr), rids, rw, logits, f32(wgu), f32(wd), f32(dout), fwd=fwd)
+    R = oracle.round_bf16
+    for got, name in ((xg.grad, "dx"), (wgug.grad, "dwgu"), (wdg.grad, "dwd"), (wrg.grad, "dwr")):
+        assert_close_bf16(f32(got), R(ref[name]), name)
+
+
 def test_layer_forward_c3_sampled(oracle):
     """C3 shape (16384 tokens, d=1536, E=16, top-2, h=4096): routing bit-exact for every token, output checked on a
     sample of 192 tokens (each row of the layer depends only on its own token)."""

@@ -1436,7 +1436,8 @@ int hmoe_grouped_wgrad(const void* a, int64_t lda, const void* b, int64_t ldb, i
                        hmoe_stream_t stream) {
   int rc = check_common(counts, counts_dtype, E, M);
   if (rc) return rc;
-  if (!a || !b || !dw || P <= 0 || N <= 0) return HMOE_ERR_ARG;
+  // M = 0 still writes dw (zeros); no operand row is read then, so a and b may be NULL
+  if (!dw || P <= 0 || N <= 0 || (M > 0 && (!a || !b))) return HMOE_ERR_ARG;
   if (dw_dtype != HMOE_DT_F32 && dw_dtype != HMOE_DT_BF16) return HMOE_ERR_DTYPE;
   if (P % 8 || N % 8 || lda % 8 || ldb % 8 || lda < P || ldb < N) return HMOE_ERR_SHAPE;
   if (!al16(a) || !al16(b) || !al16(dw)) return HMOE_ERR_ARG;

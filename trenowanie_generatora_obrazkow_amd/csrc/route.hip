@@ -1370,9 +1370,10 @@ int hmoe_router_bwd(const float* logits, const int32_t* topk_ids, const float* d
                     int dwr_dtype, void* workspace, size_t workspace_bytes, hmoe_stream_t stream) {
   if (T < 0 || E <= 0 || k <= 0 || d <= 0) return HMOE_ERR_ARG;
   if (E > kRouteMaxE || k > kMaxK) return HMOE_ERR_SHAPE;
-  if (!logits || !topk_ids || !dtopk_w || !dlogits) return HMOE_ERR_ARG;
+  // T = 0 still writes dwr (zeros); nothing per token is read or written then, so those pointers may be NULL
+  if (T > 0 && (!logits || !topk_ids || !dtopk_w || !dlogits)) return HMOE_ERR_ARG;
   if (dwr && dwr_dtype != HMOE_DT_F32 && dwr_dtype != HMOE_DT_BF16) return HMOE_ERR_DTYPE;
-  if (dwr && (!x || d % 8 || ldx % 8 || !al16(x))) return HMOE_ERR_ARG;
+  if (dwr && ((T > 0 && !x) || d % 8 || ldx % 8 || !al16(x))) return HMOE_ERR_ARG;
   if (dwr && (!workspace || workspace_bytes < hmoe_router_bwd_workspace_size(T, E, d))) return HMOE_ERR_WORKSPACE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (T > 0) {

@@ -235,7 +235,7 @@ def gate_up_swiglu(x, wgu, counts, M, a_idx=None, keep_gu=False, wgu_s=None):
     counts = _counts(counts)
     wgu_s = _w_scale(wgu, wgu_s, h2)
     a_idx = _rows_index(a_idx, "a_idx", M)
-    _need(x, "x", (None, d), _BF16, contig=False, min_rows=1 if a_idx is not None else M)
+    _need(x, "x", (None, d), _BF16, contig=False, min_rows=min(1, M) if a_idx is not None else M)
     act = torch.empty(M, h, device=x.device, dtype=torch.bfloat16)
     if wgu_s is not None:
         if keep_gu:
@@ -317,7 +317,7 @@ def down_dgrad_swiglu(dy, wd, counts, M, gu, a_idx=None, w_sorted=None):
     wd = _contig(wd, "wd")
     counts = _counts(counts)
     a_idx = _rows_index(a_idx, "a_idx", M)
-    _need(dy, "dy", (None, d), _BF16, min_rows=1 if a_idx is not None else M)
+    _need(dy, "dy", (None, d), _BF16, min_rows=min(1, M) if a_idx is not None else M)
     _need(gu, "gu", (M, 2 * h), _BF16)
     if w_sorted is not None:
         _need(w_sorted, "w_sorted", (M,), _BF16)
