@@ -105,6 +105,8 @@ def test_poziomka_varying_tokens(oracle):
     of tokens is checked."""
     m = _make_block(oracle, 512, 320, 32, 4, 4, 2, 320, seed=11).cuda()
     g = torch.Generator().manual_seed(12)
+    y0 = m(torch.empty(0, 512, dtype=torch.bfloat16, device="cuda"))  # an empty call returns an empty batch
+    assert y0.shape == (0, 512)
     for T in (1, 17, 300, 2049):
         print(f"PoziomkaMoE T={T}", flush=True)
         x = torch.randn(T, 512, generator=g).bfloat16()
