@@ -23,7 +23,7 @@ def _check(oracle, x, wr, k, bias=None, renorm=True, scaling=1.0):
 
 @pytest.mark.parametrize("T,d,E,k", [(512, 256, 8, 2), (2048, 1024, 8, 2), (4096, 1536, 16, 2), (300, 2048, 128, 8),
                                      (77, 520, 5, 3), (64, 4096, 256, 16), (500, 768, 32, 4), (200, 1536, 64, 6),
-                                     (100, 3000, 20, 3), (96, 8192, 40, 4)])
+                                     (100, 3000, 20, 3), (96, 8192, 40, 4), (3, 256, 16, 2), (1, 1024, 12, 12)])
 def test_route_bitexact(oracle, T, d, E, k):
     print(f"route T={T} d={d} E={E} k={k}", flush=True)
     x, wr, _, _ = make_inputs(T, d, E, 8, seed=T + d)

@@ -225,6 +225,72 @@ __device__ __forceinline__ void route_select(const float (&lg)[kRouteEPL], int t
     }
 }
 
+// The softmax selection of route_select<false> for E <= 16, four tokens per wave: lane l holds token t0 + l / 16's
+// logit of expert l % 16 (-inf past E).  Segment (16-lane) butterflies give the 64-lane ones' results bit for bit
+// (those only add exact zeros and compare with -inf from the lanes past E; the arg-max with ties to the lower index
+// does not depend on the reduction tree), so ids, weights and logits equal route_select's.
+__device__ __forceinline__ void route_select16(float lg, int t0, int lane, int T, int E, int k, int renorm,
+                                               float scaling, float* __restrict__ logits, int32_t* __restrict__ ids,
+                                               float* __restrict__ wout) {
+#pragma clang fp contract(off)
+  const int e = lane & 15;
+  const int64_t t = (int64_t)t0 + (lane >> 4);
+  const bool live = t < T, valid = e < E;
+  float m = valid ? lg : -__builtin_inff();
+  m = bfly_max<8>(m);
+  m = bfly_max<4>(m);
+  m = bfly_max<2>(m);
+  m = bfly_max<1>(m);
+  const float num = valid ? hexp(__fsub_rn(lg, m)) : 0.0f;
+  float S = num;
+  S = bfly_add<8>(S);
+  S = bfly_add<4>(S);
+  S = bfly_add<2>(S);
+  S = bfly_add<1>(S);
+  if (logits && live && valid) logits[t * E + e] = lg;
+  bool taken = false;
+  float selp[kMaxK];
+  int sele[kMaxK];
+#pragma unroll
+  for (int j = 0; j < kMaxK; ++j) {
+    selp[j] = 0.0f;
+    sele[j] = 0;
+    if (j < k) {
+      float bv = 0.0f;
+      int be = 0x7fffffff;
+      if (valid && !taken) {
+        bv = lg;
+        be = e;
+      }
+      argmax_take(bv, be, lane_xor<8>(bv), lane_xor_i<8>(be));
+      argmax_take(bv, be, lane_xor<4>(bv), lane_xor_i<4>(be));
+      argmax_take(bv, be, lane_xor<2>(bv), lane_xor_i<2>(be));
+      argmax_take(bv, be, lane_xor<1>(bv), lane_xor_i<1>(be));
+      if (be == e) taken = true;
+      const float pnum = __shfl(num, (lane & ~15) | (be & 15), 64);
+      selp[j] = __fdiv_rn(pnum, S);
+      sele[j] = be;
+    }
+  }
+  if (e == 0 && live) {
+    float den = 0.0f;
+    if (renorm) {
+      float s = selp[0];
+#pragma unroll
+      for (int j = 1; j < kMaxK; ++j)
+        if (j < k) s = __fadd_rn(s, selp[j]);
+      den = __fadd_rn(s, 1e-20f);
+    }
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j)
+      if (j < k) {
+        const float wj = renorm ? __fmul_rn(__fdiv_rn(selp[j], den), scaling) : __fmul_rn(selp[j], scaling);
+        ids[t * k + j] = sele[j];
+        wout[t * k + j] = wj;
+      }
+  }
+}
+
 // Logits in the fixed order: lane l's partial is the sequential sum over chunks c and elements i of
 // x[c*512 + 8l + i] * w[c*512 + 8l + i]; the 64 partials are summed by the xor butterfly (s = 32, 16, ..., 1); the
 // bias is added last.  A bf16 x bf16 product has at most 16 significant bits, so it is exact in fp32 and the fused
@@ -236,7 +302,10 @@ __device__ __forceinline__ void route_select(const float (&lg)[kRouteEPL], int t
 // per lane instead of reducing every expert separately; each value still meets exactly the partner the plain
 // butterfly would give it (fp addition is commutative), so the sums are bit-identical.  After log2(G) steps lane l
 // holds expert l >> (6 - log2 G) of the group, and the remaining steps are the plain butterfly.
-template <int NCH, int G>
+//
+// SEG (E <= 16): a wave takes four tokens one after another through the dot products and selects for all four at
+// once in 16-lane segments (route_select16).
+template <int NCH, int G, bool SEG>
 __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                          const uint16_t* __restrict__ wr,
                                                          const float* __restrict__ bias, int T, int d, int E, int k,
@@ -246,59 +315,71 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restr
   const int lane = threadIdx.x & 63;
   const int nwaves = blockDim.x >> 6;
   const int wave = threadIdx.x >> 6;
-  for (int t = blockIdx.x * nwaves + wave; t < T; t += gridDim.x * nwaves) {
-    uint4 xr[NCH];
+  constexpr int TPW = SEG ? 4 : 1;
+  for (int t0 = (blockIdx.x * nwaves + wave) * TPW; t0 < T; t0 += gridDim.x * nwaves * TPW) {
+    [[maybe_unused]] float seglg = -__builtin_inff();  // SEG: token t0 + lane / 16's logit of expert lane % 16
+#pragma unroll 1
+    for (int q = 0; q < TPW; ++q) {
+      const int t = min(t0 + q, T - 1);  // SEG: a token past T repeats row T - 1; its results are not written
+      uint4 xr[NCH];
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      int idx = c * 512 + lane * 8;
-      if (idx < d)
-        xr[c] = *reinterpret_cast<const uint4*>(x + (int64_t)t * ldx + idx);
-      else
-        xr[c] = make_uint4(0, 0, 0, 0);
-    }
-    float lg[kRouteEPL];
+      for (int c = 0; c < NCH; ++c) {
+        int idx = c * 512 + lane * 8;
+        if (idx < d)
+          xr[c] = *reinterpret_cast<const uint4*>(x + (int64_t)t * ldx + idx);
+        else
+          xr[c] = make_uint4(0, 0, 0, 0);
+      }
+      float lg[kRouteEPL];
 #pragma unroll
-    for (int i = 0; i < kRouteEPL; ++i) lg[i] = -__builtin_inff();
-    for (int g0 = 0; g0 < E; g0 += G) {
-      // lane partials of the G experts of this group; rows past E repeat row E-1 and columns past d read column
-      // d-8 against zero x (both only feed lanes / values that are discarded), so the loads carry no branches
-      float p[G];
+      for (int i = 0; i < kRouteEPL; ++i) lg[i] = -__builtin_inff();
+      for (int g0 = 0; g0 < E; g0 += G) {
+        // lane partials of the G experts of this group; rows past E repeat row E-1 and columns past d read column
+        // d-8 against zero x (both only feed lanes / values that are discarded), so the loads carry no branches
+        float p[G];
 #pragma unroll
-      for (int e = 0; e < G; ++e) {
-        p[e] = 0.0f;
-        const uint16_t* wrow = wr + (int64_t)min(g0 + e, E - 1) * d;
+        for (int e = 0; e < G; ++e) {
+          p[e] = 0.0f;
+          const uint16_t* wrow = wr + (int64_t)min(g0 + e, E - 1) * d;
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-          const int idx = min(c * 512 + lane * 8, d - 8);
-          const uint4 wv = *reinterpret_cast<const uint4*>(wrow + idx);
-          const uint32_t xw[4] = {xr[c].x, xr[c].y, xr[c].z, xr[c].w};
-          const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+          for (int c = 0; c < NCH; ++c) {
+            const int idx = min(c * 512 + lane * 8, d - 8);
+            const uint4 wv = *reinterpret_cast<const uint4*>(wrow + idx);
+            const uint32_t xw[4] = {xr[c].x, xr[c].y, xr[c].z, xr[c].w};
+            const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            p[e] = __builtin_fmaf(bf_lo(xw[j]), bf_lo(ww[j]), p[e]);
-            p[e] = __builtin_fmaf(bf_hi(xw[j]), bf_hi(ww[j]), p[e]);
+            for (int j = 0; j < 4; ++j) {
+              p[e] = __builtin_fmaf(bf_lo(xw[j]), bf_lo(ww[j]), p[e]);
+              p[e] = __builtin_fmaf(bf_hi(xw[j]), bf_hi(ww[j]), p[e]);
+            }
+          }
+        }
+        transposed_butterfly<G>(p, lane);
+        constexpr int H = G == 8 ? 3 : G == 16 ? 4 : G == 32 ? 5 : 6;
+        float v = p[0];
+        if constexpr (H < 4) v = bfly_add<4>(v);  // the plain butterfly finishes in descending s
+        if constexpr (H < 5) v = bfly_add<2>(v);
+        if constexpr (H < 6) v = bfly_add<1>(v);
+        const int my_e = g0 + (lane >> (6 - H));
+        if (bias && my_e < E) v = __fadd_rn(v, bias[my_e]);
+        // lane l collects expert i*64 + l from the lanes of its group slot
+#pragma unroll
+        for (int i = 0; i < kRouteEPL; ++i) {
+          if (i * 64 < E && i * 64 + 63 >= g0 && i * 64 < g0 + G) {
+            const int e = i * 64 + lane;
+            const float val = __shfl(v, ((e - g0) << (6 - H)) & 63, 64);
+            if (e >= g0 && e < g0 + G && e < E) lg[i] = val;
           }
         }
       }
-      transposed_butterfly<G>(p, lane);
-      constexpr int H = G == 8 ? 3 : G == 16 ? 4 : G == 32 ? 5 : 6;
-      float v = p[0];
-      if constexpr (H < 4) v = bfly_add<4>(v);  // the plain butterfly finishes in descending s
-      if constexpr (H < 5) v = bfly_add<2>(v);
-      if constexpr (H < 6) v = bfly_add<1>(v);
-      const int my_e = g0 + (lane >> (6 - H));
-      if (bias && my_e < E) v = __fadd_rn(v, bias[my_e]);
-      // lane l collects expert i*64 + l from the lanes of its group slot
-#pragma unroll
-      for (int i = 0; i < kRouteEPL; ++i) {
-        if (i * 64 < E && i * 64 + 63 >= g0 && i * 64 < g0 + G) {
-          const int e = i * 64 + lane;
-          const float val = __shfl(v, ((e - g0) << (6 - H)) & 63, 64);
-          if (e >= g0 && e < g0 + G && e < E) lg[i] = val;
-        }
+      if constexpr (SEG) {
+        const float v = __shfl(lg[0], lane & 15, 64);
+        if ((lane >> 4) == q) seglg = v;
+      } else {
+        route_select<false>(lg, t, lane, E, k, renorm, scaling, bias, logits, ids, wout, 1, 1);
       }
     }
-    route_select<false>(lg, t, lane, E, k, renorm, scaling, bias, logits, ids, wout, 1, 1);
+    if constexpr (SEG) route_select16(seglg, t0, lane, T, E, k, renorm, scaling, logits, ids, wout);
   }
 }
 
@@ -1149,9 +1230,18 @@ static int route_launch(const void* x, int64_t ldx, const void* wr, const float*
   // experts per transposed-butterfly group; rows longer than 2048 hold more of x in registers, so smaller groups
   int group = E <= 8 ? 8 : E <= 16 ? 16 : E <= 32 ? 32 : 64;
   if (nch > 4 && group > 16) group = 16;
+  // four tokens per wave with a segmented selection for E <= 16
+  const bool seg = E <= 16;
+  const int sgrid = grid_for(T, 16, 4096);
 #define HMOE_ROUTE(NC, GR)                                                                                        \
-  hipLaunchKernelGGL((route_topk_kernel<NC, GR>), dim3(grid), dim3(256), 0, s, xp, ldx, wp, bias, (int)T, (int)d, \
-                     E, k, renorm, scaling, logits, topk_ids, topk_w)
+  do {                                                                                                            \
+    if (seg && GR <= 16)                                                                                          \
+      hipLaunchKernelGGL((route_topk_kernel<NC, (GR <= 16 ? GR : 16), true>), dim3(sgrid), dim3(256), 0, s, xp,   \
+                         ldx, wp, bias, (int)T, (int)d, E, k, renorm, scaling, logits, topk_ids, topk_w);         \
+    else                                                                                                          \
+      hipLaunchKernelGGL((route_topk_kernel<NC, GR, false>), dim3(grid), dim3(256), 0, s, xp, ldx, wp, bias,      \
+                         (int)T, (int)d, E, k, renorm, scaling, logits, topk_ids, topk_w);                        \
+  } while (0)
 #define HMOE_ROUTE_G(NC)        \
   if (group == 8)               \
     HMOE_ROUTE(NC, 8);          \
