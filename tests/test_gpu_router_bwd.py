@@ -47,3 +47,27 @@ def test_router_bwd_and_unpermute(oracle, T, d, E, k, renorm):
     dx0 = ops.unpermute_bwd(dxs.to(dev), inv, T, k)
     ref0 = dxs.double().numpy()[disp["inv_pos"].reshape(T, k)].sum(1)
     assert_close_bf16(dx0.float().cpu().numpy(), oracle.round_bf16(ref0), "dx no router")
+
+
+@pytest.mark.parametrize("T,d,E,k,dt", [(4100, 1536, 16, 2, torch.float32), (4096, 1024, 12, 3, torch.bfloat16),
+                                        (5000, 2048, 16, 1, torch.float32)])
+def test_unpermute_many_tokens(oracle, T, d, E, k, dt):
+    """Many tokens (workgroups walk several tokens each): dx = sum_j dxs[inv_pos[t, j]] + dlogits @ Wr, fp32 and
+    bf16 row sums, against float64, and bit-equal to the same sums taken for the first tokens alone."""
+    from trenowanie_generatora_obrazkow_amd import ops
+    print(f"unpermute T={T} d={d} E={E} k={k} {dt}", flush=True)
+    dev = torch.device("cuda")
+    g = torch.Generator().manual_seed(T + d)
+    M = T * k
+    dxs = torch.randn(M, d, generator=g).to(dt)
+    inv = torch.randperm(M, generator=g).int()
+    dl = torch.randn(T, E, generator=g) * 0.1
+    wr = (torch.randn(E, d, generator=g) * 0.02).bfloat16()
+    dx = ops.unpermute_bwd(dxs.to(dev), inv.to(dev), T, k, dlogits=dl.to(dev), wr=wr.to(dev))
+    ref = dxs.double().numpy()[inv.numpy().reshape(T, k)].sum(1) + dl.double().numpy() @ wr.double().numpy()
+    assert_close_bf16(dx.float().cpu().numpy(), oracle.round_bf16(ref), "dx")
+    # the first 1000 tokens alone: the same bits
+    n = 1000
+    part = ops.unpermute_bwd(dxs[inv[: n * k].long()].to(dev), torch.arange(n * k, dtype=torch.int32, device=dev), n,
+                             k, dlogits=dl[:n].to(dev), wr=wr.to(dev))
+    assert torch.equal(part.cpu(), dx[:n].cpu())
