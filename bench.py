@@ -1,6 +1,8 @@
 """Benchmark of the MoE SwiGLU layer on one MI355X (the metric and configs of BASELINE.json).
 
 A step is one pass of the layer over one batch of seeded synthetic tokens, inputs resident in HBM:
+  c1            forward at the tiny C1 shape (512 tokens, d=256, 8 experts, top-2, h=512); its CPU baseline is the
+                reference's fp32 CPU path on the whole workload
   c5 (default)  training step at the C3 shape: forward + backward (16384 tokens, d=1536, 16 experts, top-2, h=4096)
   c3            forward only at the same shape
   c4            forward only, Zipf(1.2)-biased router logits, 2 experts never routed
@@ -27,6 +29,9 @@ PEAK_HBM_GBS = 8000.0
 METRIC = "MoE layer µs + grouped-GEMM TFLOP/s (% bf16 MFMA peak) at 16k tokens, 1 GPU"
 
 WORKLOADS = {
+    "c1": dict(T=512, d=256, E=8, k=2, h=512, backward=False, zipf=False, cpu_dtype="fp32", cpu_tokens=512,
+               desc="C1: tiny MoE layer forward, 512 tokens, d_model=256, 8 experts, top-2, SwiGLU hidden=512 (the "
+                    "reference's CPU path runs it in fp32 at full size; the GPU runs the bf16 layer)"),
     "c2": dict(T=2048, d=1024, E=8, k=2, h=2048, backward=False, zipf=False,
                desc="C2: MoE layer forward, 8 images x 256 tokens = 2048 tokens, d_model=1024, 8 experts, top-2, "
                     "SwiGLU hidden=2048"),
@@ -203,6 +208,31 @@ def run_gpu_poziomka(w, steps, warmup):
     return ms, statistics.mean(dom), kern
 
 
+def cpu_threads():
+    """CPU threads for the baseline: the CPUs this process may run on (len(os.sched_getaffinity(0))), capped by
+    OMP_NUM_THREADS where the host sets it (a GPU box's CPU share); torch is set to that many threads.  Returns
+    (threads used, affinity CPUs)."""
+    import torch
+    aff = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    n = min(aff, int(cap)) if cap.isdigit() and int(cap) > 0 else aff
+    torch.set_num_threads(n)
+    return n, aff
+
+
+def time_cpu(step, budget_s, warmup=3, min_reps=10, max_reps=30):
+    """3 warm-ups, then the median of at least 10 timed runs (more while the budget lasts)."""
+    for _ in range(warmup):
+        step()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < min_reps or (len(times) < max_reps and time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
 def cpu_baseline_poziomka(w, budget_s=15.0):
     """The reference block's own forward (oracle/cpu_path.py: aurora/hf_pipeline.py:348-370) on CPU, on a bounded
     sample of the same workload: the full d, E, k, h with fewer tokens."""
@@ -210,7 +240,7 @@ def cpu_baseline_poziomka(w, budget_s=15.0):
 
     from oracle import cpu_path
 
-    threads = torch.get_num_threads()
+    threads, aff = cpu_threads()
     T = 512
     g = torch.Generator().manual_seed(0)
     m = _poziomka_block(w, g)
@@ -223,21 +253,13 @@ def cpu_baseline_poziomka(w, budget_s=15.0):
         with torch.no_grad():
             cpu_path.poziomka_forward(*args)
 
-    t0 = time.perf_counter()
-    step()
-    one = time.perf_counter() - t0
-    reps = int(max(3, min(10, budget_s / max(one, 1e-3))))
-    times = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
+    med, reps = time_cpu(step, budget_s)
     flops = gemm_flops(dict(w, T=T))
-    return {"value": flops / med / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+    return {"value": flops / med / 1e12, "unit": "TFLOP/s", "cores": threads, "affinity_cpus": aff, "kind": "port",
+            "us_per_layer": round(med * 1e6, 1),
             "sample": f"{T} tokens of the same block shape (d={w['d']}, E={w['E']}, top-{w['k']}, h={w['h']}, shared "
-                      f"h={w['shared_h']}), bf16 activations, int8 experts, torch CPU forward; median of {reps} runs "
-                      f"after 1 warm-up; {med * 1e3:.1f} ms per sample step"}
+                      f"h={w['shared_h']}), bf16 activations, int8 experts, torch CPU forward with {threads} threads; "
+                      f"median of {reps} runs after 3 warm-ups; {med * 1e3:.1f} ms per sample step"}
 
 
 def cpu_baseline(w, budget_s=15.0):
@@ -247,15 +269,17 @@ def cpu_baseline(w, budget_s=15.0):
 
     from oracle import cpu_path
 
-    threads = torch.get_num_threads()
-    T = 512
+    threads, aff = cpu_threads()
+    T = w.get("cpu_tokens", 2048)
+    fp32 = w.get("cpu_dtype") == "fp32"
+    dt = torch.float32 if fp32 else torch.bfloat16
     d, E, h, k = w["d"], w["E"], w["h"], w["k"]
     g = torch.Generator().manual_seed(0)
-    x = torch.randn(T, d, generator=g).bfloat16()
-    wr = (torch.randn(E, d, generator=g) * 0.02).bfloat16()
-    wgu = (torch.randn(E, d, 2 * h, generator=g) * 0.02).bfloat16()
-    wd = (torch.randn(E, h, d, generator=g) * 0.02).bfloat16()
-    dout = torch.randn(T, d, generator=g).bfloat16()
+    x = torch.randn(T, d, generator=g).to(dt)
+    wr = (torch.randn(E, d, generator=g) * 0.02).to(dt)
+    wgu = (torch.randn(E, d, 2 * h, generator=g) * 0.02).to(dt)
+    wd = (torch.randn(E, h, d, generator=g) * 0.02).to(dt)
+    dout = torch.randn(T, d, generator=g).to(dt)
     bias = torch.from_numpy(zipf_bias(E, seed=0)) if w["zipf"] else None
 
     def step():
@@ -266,21 +290,14 @@ def cpu_baseline(w, budget_s=15.0):
             with torch.no_grad():
                 cpu_path.layer_forward(x, wr, wgu, wd, k, bias=bias)
 
-    t0 = time.perf_counter()
-    step()
-    one = time.perf_counter() - t0
-    reps = int(max(3, min(10, budget_s / max(one, 1e-3))))
-    times = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
+    med, reps = time_cpu(step, budget_s)
     flops = (18 if w["backward"] else 6) * T * k * d * h
-    return {"value": flops / med / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"{T} tokens of the same layer shape (d={d}, E={E}, top-{k}, h={h}), bf16, torch CPU "
-                      f"{'forward+backward' if w['backward'] else 'forward'}; median of {reps} runs after 1 warm-up; "
-                      f"{med * 1e3:.1f} ms per sample step"}
+    what = "the whole workload" if T == w["T"] else f"{T} tokens of the same layer shape"
+    return {"value": flops / med / 1e12, "unit": "TFLOP/s", "cores": threads, "affinity_cpus": aff, "kind": "port",
+            "us_per_layer": round(med * 1e6, 1),
+            "sample": f"{what} (d={d}, E={E}, top-{k}, h={h}), {'fp32' if fp32 else 'bf16'}, torch CPU "
+                      f"{'forward+backward' if w['backward'] else 'forward'} with {threads} threads; median of {reps} "
+                      f"runs after 3 warm-ups; {med * 1e3:.1f} ms per sample step"}
 
 
 def library_ceiling(M, N, K, reps=10):

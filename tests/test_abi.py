@@ -76,6 +76,11 @@ def test_argument_validation_codes(lib):
                            None) == -5
     assert L.hmoe_dispatch(P, 4, None, 0, 16, 2, 2000, None, 0, 0, None, P, None, P, P, P, P, None, P, ws,
                            None) == -2
+    # a missing order or topk_ids is refused before the first launch (counts / starts stay untouched)
+    assert L.hmoe_dispatch(P, 4, None, 0, 16, 2, 4, None, 0, 0, None, P, None, P, None, P, P, None, P, ws,
+                           None) == -1
+    assert L.hmoe_dispatch(None, 4, None, 0, 16, 2, 4, None, 0, 0, None, P, None, P, P, P, P, None, P, ws,
+                           None) == -1
     # grouped_mm: K % 8, fp32 input, int8 weights
     assert L.hmoe_grouped_mm(P, 64, 0, P, 0, 3, 60, 32, 60 * 32, 32, P, 4, 48, None, None, None, 0, None, 0, P, 32,
                              None) == -2

@@ -178,3 +178,52 @@ def test_ops_reject_bad_inputs():
     with pytest.raises(ValueError):
         ops.unpermute_bwd(torch.zeros(M, d, device=dev), torch.zeros(M, dtype=torch.int32, device=dev), M // 2, 2,
                           dlogits=torch.zeros(M // 2, E, device=dev))
+
+
+def test_ops_reject_mismatched_stacks():
+    """One expert count and one width across router, expert stacks and bias; weights of the wrong dtype are refused
+    (never reinterpreted as bf16); grouped_mm's scale and out must cover its M rows.  All of it raises before any
+    kernel is launched."""
+    from trenowanie_generatora_obrazkow_amd import moe_swiglu, ops
+    dev = torch.device("cuda")
+    E, d, h, T, k = 4, 64, 32, 20, 2
+    M = T * k
+    bf = dict(dtype=torch.bfloat16, device=dev)
+    x = torch.zeros(T, d, **bf)
+    wr, wgu, wd = torch.zeros(E, d, **bf), torch.zeros(E, d, 2 * h, **bf), torch.zeros(E, h, d, **bf)
+    with pytest.raises(ValueError):
+        moe_swiglu(x, torch.zeros(E + 1, d, **bf), wgu, wd, k)               # router names a 5th expert
+    with pytest.raises(ValueError):
+        moe_swiglu(x, wr, wgu, torch.zeros(E, h, d + 8, **bf), k)            # down stack of another width
+    with pytest.raises(ValueError):
+        moe_swiglu(x, wr, wgu, wd, k, logit_bias=torch.zeros(E + 1, device=dev))
+    with pytest.raises(ValueError):
+        moe_swiglu(x, wr, wgu, wd, E + 1)
+    with pytest.raises(TypeError):
+        moe_swiglu(x, wr, wgu.half(), wd, k)
+    with pytest.raises(ValueError):
+        ops.route_topk(x, torch.zeros(E, d + 8, **bf), k)
+    with pytest.raises(ValueError):
+        ops.route_topk(x, wr, k, bias=torch.zeros(E + 2, device=dev))
+    counts = torch.full((E,), M // E, dtype=torch.int32, device=dev)
+    with pytest.raises(TypeError):
+        ops.gate_up_swiglu(x, wgu.float(), counts, M, a_idx=torch.zeros(M, dtype=torch.int32, device=dev))
+    act = torch.zeros(M, h, **bf)
+    with pytest.raises(TypeError):
+        ops.down_scatter(act, wd.float(), counts, M, None, None)
+    with pytest.raises(TypeError):
+        ops.down_dgrad_swiglu(x, wd.float(), counts, M, torch.zeros(M, 2 * h, **bf),
+                              a_idx=torch.zeros(M, dtype=torch.int32, device=dev))
+    with pytest.raises(TypeError):
+        ops.gate_up_dgrad(torch.zeros(M, 2 * h, **bf), wgu.float(), counts, M)
+    with pytest.raises(ValueError):
+        ops.gate_up_swiglu(x, wgu, counts[:E - 1], M, a_idx=torch.zeros(M, dtype=torch.int32, device=dev))
+    a = torch.zeros(M, d, **bf)
+    with pytest.raises(ValueError):
+        ops.grouped_mm(a, wgu, counts, M, scale=torch.ones(M - 1, device=dev))
+    with pytest.raises(ValueError):
+        ops.grouped_mm(a, wgu, counts, M, out=torch.zeros(M - 1, 2 * h, **bf))
+    with pytest.raises(TypeError):
+        ops.grouped_mm(a, wgu.float(), counts, M)
+    with pytest.raises(ValueError):
+        ops.dispatch(torch.zeros(T, k, dtype=torch.int32, device=dev), E, x=x[:T - 1])

@@ -193,3 +193,134 @@ def test_fuse_moe_matches_expert_loop():
         ref.index_add_(0, rows, out.float() * w[rows, slot, None])
     cos = torch.nn.functional.cosine_similarity(y.flatten(), ref.flatten(), dim=0).item()
     assert cos > 0.9999, cos
+
+
+def test_layer_c4_full_size(oracle):
+    """C4 at full size: 16384 tokens, d=1536, E=16, top-2, h=4096, Zipf(1.2) expert bias with 2 experts never
+    routed (aurora/hf_compat.py:69-82 over skewed groups: one expert gets ~14k of the 32768 rows, the smallest
+    non-empty one a few).
+      - routing ids and weights bit-exact for every token; counts bit-exact against torch.bincount (2 zeros);
+      - output on sampled tokens (all tokens of the smallest non-empty expert, a sample of the largest, random ones);
+      - backward: weight gradients of the largest expert on a subset J of its hidden units (a weight gradient
+        column j of w_gu / row j of w_d depends only on hidden unit j, so the float64 oracle runs the layer
+        restricted to J with the same routing and upstream gradient), the full weight gradients of the smallest
+        non-empty expert, dx of its tokens and of a sample of the largest expert's tokens, and exact zeros for the
+        two empty experts."""
+    from trenowanie_generatora_obrazkow_amd import ops
+    T, d, E, k, h = 16384, 1536, 16, 2, 4096
+    x, wr, wgu, wd = make_inputs(T, d, E, h, seed=0)
+    bias = oracle.zipf_bias(E, seed=0)
+    dout = torch.randn(T, d, generator=torch.Generator().manual_seed(1)).bfloat16()
+    out, ids, tw, (xg, wrg, wgug, wdg) = _run_layer(x, wr, wgu, wd, k, dout=dout, bias=bias)
+    logits, rids, rw = oracle.route(bits(x), bits(wr), k, bias=bias)
+    np.testing.assert_array_equal(ids.cpu().numpy(), rids)
+    np.testing.assert_array_equal(tw.cpu().numpy().view(np.uint32), rw.view(np.uint32))
+    counts = ops.dispatch(ids, E).counts.cpu()
+    ref_counts = torch.bincount(torch.from_numpy(rids).reshape(-1).long(), minlength=E)
+    assert torch.equal(counts.long(), ref_counts)
+    empty = np.nonzero(ref_counts.numpy() == 0)[0]
+    assert empty.size == 2
+    live = np.nonzero(ref_counts.numpy() > 0)[0]
+    e_max = int(live[np.argmax(ref_counts.numpy()[live])])
+    e_min = int(live[np.argmin(ref_counts.numpy()[live])])
+    print(f"C4 counts {ref_counts.tolist()}, largest expert {e_max}, smallest {e_min}", flush=True)
+    assert ref_counts[e_max] > 10000
+    rng = np.random.default_rng(2)
+    toks_max = np.nonzero((rids == e_max).any(axis=1))[0]
+    toks_min = np.nonzero((rids == e_min).any(axis=1))[0]
+    sample = np.unique(np.concatenate([toks_min, rng.choice(toks_max, 64, replace=False),
+                                       rng.choice(T, 128, replace=False)]))
+    xf, wguf, wdf, doutf = f32(x), f32(wgu), f32(wd), f32(dout)
+    fwd = oracle.moe_forward(xf, rids, rw, wguf, wdf, tokens=sample)
+    assert_close_bf16(f32(out)[sample], fwd["out"], "C4 out sampled")
+    R = oracle.round_bf16
+    gwgu, gwd, gdx = f32(wgug.grad), f32(wdg.grad), f32(xg.grad)
+    for e in empty:
+        assert not gwgu[e].any() and not gwd[e].any(), f"empty expert {e} has a weight gradient"
+    # smallest non-empty expert: its full weight gradients and its tokens' dx
+    ref = oracle.layer_backward(xf[toks_min], f32(wr), rids[toks_min], rw[toks_min], logits[toks_min], wguf, wdf,
+                                doutf[toks_min])
+    assert_close_bf16(gwd[e_min], R(ref["dwd"][e_min]), f"dWd[{e_min}]")
+    assert_close_bf16(gwgu[e_min], R(ref["dwgu"][e_min]), f"dWgu[{e_min}]")
+    assert_close_bf16(gdx[toks_min], R(ref["dx"]), "dx (tokens of the smallest expert)")
+    # dx of a sample of the largest expert's tokens
+    tsel = rng.choice(toks_max, 48, replace=False)
+    ref = oracle.layer_backward(xf[tsel], f32(wr), rids[tsel], rw[tsel], logits[tsel], wguf, wdf, doutf[tsel])
+    assert_close_bf16(gdx[tsel], R(ref["dx"]), "dx (sample of the largest expert's tokens)")
+    # largest expert, hidden units J: the layer restricted to J has the same weight gradients there
+    J = np.sort(rng.choice(h, 128, replace=False))
+    cols = np.concatenate([J, h + J])
+    rb = oracle.moe_backward(xf[toks_max], rids[toks_max], rw[toks_max], wguf[:, :, cols], wdf[:, J, :],
+                             doutf[toks_max])
+    assert_close_bf16(gwd[e_max][J], R(rb["dwd"][e_max]), f"dWd[{e_max}] rows J")
+    assert_close_bf16(gwgu[e_max][:, cols], R(rb["dwgu"][e_max]), f"dWgu[{e_max}] columns J")
+
+
+def test_moe_swiglu_module(oracle):
+    """MoESwiGLU as the reference calls its FFN, self.mlp(h) on (B, T, dim) (aurora/model.py:210), after the
+    reference's own init code (init_block, aurora/model.py:393-396, restated): forward and backward against the
+    float64 oracle; a loss on the returned routing weights reaches x and the router (softmax + renormalisation
+    Jacobian); fp32 input gives fp32 output with the same values, autocast(bf16) gives bf16; fp32 master weights
+    give the bf16 model's output bit for bit and fp32 gradients whose bf16 rounding is the bf16 model's."""
+    from trenowanie_generatora_obrazkow_amd import MoESwiGLU
+    B, T, dim, hidden, E, k = 2, 160, 256, 384, 8, 2
+    torch.manual_seed(3)
+    m = MoESwiGLU(dim, hidden, E, top_k=k).cuda()
+    with torch.no_grad():
+        for lin in (m.in_proj, m.out_proj):
+            nn.init.normal_(lin.weight, std=lin.in_features ** -0.5)
+    g = torch.Generator().manual_seed(4)
+    h = torch.randn(B, T, dim, generator=g).bfloat16()
+    dout = torch.randn(B, T, dim, generator=g).bfloat16()
+    c = torch.randn(B * T, k, generator=g)  # weight of the routing-weight term of the loss
+    hg = h.cuda().requires_grad_(True)
+    out = m(hg)
+    assert out.shape == (B, T, dim) and out.dtype == torch.bfloat16
+    loss = (out.float() * dout.cuda().float()).sum() + (m.last_topk_weight * c.cuda()).sum()
+    loss.backward()
+    torch.cuda.synchronize()
+    x2 = h.reshape(-1, dim)
+    wr, wgu, wd = (f32(p) for p in (m.router_weight, m.w_gu, m.w_d))
+    logits, rids, rw = oracle.route(bits(x2), bits(m.router_weight), k)
+    np.testing.assert_array_equal(m.last_topk_ids.cpu().numpy(), rids)
+    fwd = oracle.moe_forward(f32(x2), rids, rw, wgu, wd)
+    assert_close_bf16(f32(out).reshape(-1, dim), fwd["out"], "module out")
+    b = oracle.moe_backward(f32(x2), rids, rw, wgu, wd, f32(dout).reshape(-1, dim), fwd=fwd)
+    dl = oracle.router_backward(logits, rids, b["dtopk_w"] + c.numpy().astype(np.float64))
+    R = oracle.round_bf16
+    assert_close_bf16(f32(hg.grad).reshape(-1, dim), R(b["dx_experts"] + dl @ wr.astype(np.float64)), "dx")
+    assert_close_bf16(f32(m.router_weight.grad), R(dl.T @ f32(x2).astype(np.float64)), "dWr")
+    assert_close_bf16(f32(m.w_gu.grad), R(b["dwgu"]), "dWgu")
+    assert_close_bf16(f32(m.w_d.grad), R(b["dwd"]), "dWd")
+
+    # a loss on the routing weights alone
+    m.zero_grad(set_to_none=True)
+    hg2 = h.cuda().requires_grad_(True)
+    m(hg2)
+    (m.last_topk_weight * c.cuda()).sum().backward()
+    dl0 = oracle.router_backward(logits, rids, c.numpy().astype(np.float64))
+    assert_close_bf16(f32(hg2.grad).reshape(-1, dim), R(dl0 @ wr.astype(np.float64)), "dx (routing-weight loss)")
+    assert not f32(m.w_gu.grad).any() and not f32(m.w_d.grad).any()
+
+    # dtypes: fp32 input -> fp32 output of the same values; autocast -> the autocast dtype
+    with torch.no_grad():
+        o32 = m(h.float().cuda())
+        assert o32.dtype == torch.float32 and torch.equal(o32, out.float())
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            assert m(h.float().cuda()).dtype == torch.bfloat16
+
+    # fp32 master weights: same forward, fp32 gradients
+    m32 = MoESwiGLU(dim, hidden, E, top_k=k, dtype=torch.float32).cuda()
+    with torch.no_grad():
+        for p32, p16 in ((m32.router_weight, m.router_weight), (m32.w_gu, m.w_gu), (m32.w_d, m.w_d)):
+            p32.copy_(p16.float())
+    m.zero_grad(set_to_none=True)
+    for mod in (m, m32):
+        o = mod(h.cuda())
+        (o.float() * dout.cuda().float()).sum().backward()
+        if mod is m:
+            o16 = o
+    torch.cuda.synchronize()
+    assert torch.equal(o, o16)
+    for p32, p16 in ((m32.router_weight, m.router_weight), (m32.w_gu, m.w_gu), (m32.w_d, m.w_d)):
+        assert p32.grad.dtype == torch.float32 and torch.equal(p32.grad.bfloat16(), p16.grad)

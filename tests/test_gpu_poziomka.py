@@ -144,3 +144,55 @@ def test_poziomka_graph_replay(oracle):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(static_y, eager), f"replay {i}"
+
+
+def test_poziomka_export_loaded_on_gpu(oracle, tmp_path):
+    """The exported text encoder format (export.py:62-102): a safetensors file holding the fused trunk under "lm."
+    (layer i's MoE block under "lm.layers.{i}.mlp.", a dense first layer and other tensors beside it) and
+    text_encoder/config.json with the lm_* fields export.py writes.  load_export(..., device="cuda") builds the MoE
+    blocks; each one's forward on the GPU matches the oracle run on the tensors as stored (fp32 expert bias kept
+    unrounded, int8 experts with bf16 scales, bf16 router and shared expert)."""
+    import json
+
+    from safetensors.torch import save_file
+
+    from trenowanie_generatora_obrazkow_amd.poziomka import export_state, load_export
+    d, h, E, k, n_group, topk_group, sh = 512, 320, 32, 4, 4, 2, 320
+    blocks = {}
+    for i in (1, 2):
+        m = _make_block(oracle, d, h, E, k, n_group, topk_group, sh, seed=40 + i)
+        m.gate.expert_bias = torch.randn(E, generator=torch.Generator().manual_seed(50 + i)) * 0.05  # fp32
+        blocks[i] = m
+    sd = export_state(blocks)
+    sd["lm.layers.0.mlp.gate_proj.weight"] = torch.zeros(1024, d, dtype=torch.bfloat16)  # the dense first layer
+    sd["lm.layers.1.attention.query_key_value.weight"] = torch.zeros(64, d, dtype=torch.bfloat16)
+    sd["lm.word_embeddings.weight"] = torch.zeros(100, d, dtype=torch.bfloat16)
+    sd["blocks.0.attn.qkv.weight"] = torch.zeros(8, 8)  # the trained refiner's tensors
+    te = tmp_path / "text_encoder"
+    te.mkdir()
+    save_file(sd, str(te / "diffusion_pytorch_model.safetensors"))
+    cfg = {"_class_name": "AuroraLMTextEncoder", "kind": "lm", "lm_arch": "poziomka", "vocab_size": 100,
+           "lm_blocks": 3, "lm_dim": d, "lm_heads": 8, "lm_kv_heads": 2, "lm_head_dim": 64, "lm_rotary_dim": 32,
+           "lm_rope_theta": 10000.0, "lm_norm_eps": 1e-6, "lm_dense_layers": 1, "lm_intermediate": 1024,
+           "lm_moe_intermediate": h, "lm_experts": E, "lm_top_k": k, "lm_n_group": n_group,
+           "lm_topk_group": topk_group, "lm_routed_scaling": 2.5, "lm_shared_intermediate": sh}
+    (te / "config.json").write_text(json.dumps(cfg))
+    loaded = load_export(str(tmp_path), device="cuda")
+    assert sorted(loaded) == [1, 2]
+    g = torch.Generator().manual_seed(60)
+    for i, m in loaded.items():
+        print(f"export layer {i}", flush=True)
+        assert m._wgu.is_cuda and m.gate.expert_bias.dtype == torch.float32
+        x = torch.randn(2, 150, d, generator=g).bfloat16()
+        y = m(x.cuda())
+        ids, ref, _ = _oracle_forward(oracle, blocks[i], x.reshape(-1, d), k, n_group, topk_group)
+        _, gids, _ = ops_route(m, x.reshape(-1, d), k, n_group, topk_group)
+        np.testing.assert_array_equal(gids, ids)
+        assert_close_bf16(f32(y).reshape(-1, d), ref, f"exported layer {i}")
+
+
+def ops_route(m, x2, k, n_group, topk_group):
+    from trenowanie_generatora_obrazkow_amd import ops
+    sc, ids, w = ops.route_sigmoid_group(x2.cuda(), m.gate.weight, k, n_group, topk_group,
+                                        expert_bias=m.gate.expert_bias, scaling=m.scaling)
+    return sc, ids.cpu().numpy(), w

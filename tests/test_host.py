@@ -118,10 +118,59 @@ def test_moe_swiglu_module_shapes():
     m = MoESwiGLU(64, 96, 8, top_k=2)
     assert m.router_weight.shape == (8, 64) and m.w_gu.shape == (8, 64, 192) and m.w_d.shape == (8, 96, 64)
     assert m.w_gu.dtype == torch.bfloat16
-    assert abs(m.w_gu.float().std().item() - 0.02) < 2e-3
+    # the reference's initialisation convention: N(0, in_features ** -0.5) (aurora/model.py:393-396)
+    for p, fan_in in ((m.router_weight, 64), (m.w_gu, 64), (m.w_d, 96)):
+        assert abs(p.float().std().item() / fan_in ** -0.5 - 1) < 0.1
+    m2 = MoESwiGLU(64, 96, 8, top_k=2, init_std=0.02)
+    assert abs(m2.w_gu.float().std().item() - 0.02) < 2e-3
     assert m.logit_bias.dtype == torch.float32 and (m.logit_bias == 0).all()
     with pytest.raises(RuntimeError, match="GPU"):
         m(torch.randn(2, 5, 64))
+
+
+def test_reference_init_code_runs_on_moe_block():
+    """The reference initialises a block's FFN through nn.Linear attributes: Denoiser.init_block (aurora/model.py:
+    393-396: normal_(lin.weight, std=lin.in_features ** -0.5) for mlp.in_proj and mlp.out_proj), the text encoder's
+    init_weights (:308-312: in_proj the same way, out_proj zeroed) and train_pp --init (train_pp.py:1420-1421:
+    out_proj zeroed in new blocks).  Those loops, restated here on a stand-in block whose mlp is a MoESwiGLU, reach
+    the stacked expert parameters: every expert gets the fan-in std, out_proj zeroes every expert, the state dict
+    keeps only the stacked names."""
+    torch.manual_seed(1)
+    dim, hidden, E = 256, 512, 8
+    block = nn.Module()
+    block.mlp = MoESwiGLU(dim, hidden, E, init_std=0.5)
+    with torch.no_grad():
+        for lin in (block.mlp.in_proj, block.mlp.out_proj):        # init_block
+            nn.init.normal_(lin.weight, std=lin.in_features ** -0.5)
+    assert block.mlp.in_proj.in_features == dim and block.mlp.out_proj.in_features == hidden
+    assert block.mlp.in_proj.out_features == 2 * hidden and block.mlp.out_proj.out_features == dim
+    for w, fan_in in ((block.mlp.w_gu, dim), (block.mlp.w_d, hidden)):
+        per_expert = w.detach().float().reshape(E, -1).std(dim=1)
+        assert torch.allclose(per_expert, torch.full((E,), fan_in ** -0.5), rtol=0.03), per_expert
+    with torch.no_grad():
+        nn.init.normal_(block.mlp.in_proj.weight, std=block.mlp.in_proj.in_features ** -0.5)   # text init_weights
+        nn.init.zeros_(block.mlp.out_proj.weight)
+    assert not block.mlp.w_d.detach().float().abs().any()
+    assert block.mlp.in_proj.weight is block.mlp.w_gu and block.mlp.out_proj.weight is block.mlp.w_d
+    assert set(block.state_dict()) == {"mlp.router_weight", "mlp.w_gu", "mlp.w_d", "mlp.logit_bias"}
+
+
+def test_moe_swiglu_rejects_mismatched_shapes_before_launch():
+    """The functional layer cross-checks router, expert stacks, bias and k on the host, before any kernel call
+    (here on CPU tensors: the shape errors come first)."""
+    from trenowanie_generatora_obrazkow_amd import moe_swiglu
+    E, d, h, T = 4, 64, 32, 10
+    x = torch.zeros(T, d, dtype=torch.bfloat16)
+    wr, wgu, wd = (torch.zeros(s, dtype=torch.bfloat16) for s in ((E, d), (E, d, 2 * h), (E, h, d)))
+    for args, err in (((x, torch.zeros(E + 1, d, dtype=torch.bfloat16), wgu, wd, 2), ValueError),
+                      ((x, wr, torch.zeros(E, d, 2 * h + 2, dtype=torch.bfloat16), wd, 2), ValueError),
+                      ((x, wr, wgu, torch.zeros(E, h, d, dtype=torch.float16), 2), TypeError),
+                      ((x.float(), wr, wgu, wd, 2), TypeError),
+                      ((x, wr, wgu, wd, 0), ValueError)):
+        with pytest.raises(err):
+            moe_swiglu(*args)
+    with pytest.raises(ValueError):
+        moe_swiglu(x, wr, wgu, wd, 2, logit_bias=torch.zeros(E - 1))
 
 
 def test_poziomka_module_layout():
@@ -234,3 +283,32 @@ def test_swap_moe_replaces_reference_blocks():
         for k, v in layer.mlp.state_dict().items():
             assert torch.equal(v, src.state_dict()[k]), k
     assert swap_moe(model) == 0
+
+
+def test_poziomka_expert_bias_keeps_its_precision(tmp_path):
+    """The reference selects experts on scores + expert_bias.float() (aurora/hf_pipeline.py:353), so an fp32 bias
+    must survive from_reference / swap_moe and load_export unrounded even when the block's weights are bf16: a bias
+    that is not bf16-exact comes back bit for bit, in fp32."""
+    import json
+
+    from safetensors.torch import save_file
+
+    from trenowanie_generatora_obrazkow_amd.poziomka import export_state, from_reference, load_export
+    d, h, E, sh = 64, 32, 16, 48
+    src = _rand_block(d, h, E, sh, seed=3)
+    bias = (torch.randn(E, generator=torch.Generator().manual_seed(4)) * 0.01 + 1e-3).float()
+    assert not torch.equal(bias.bfloat16().float(), bias)  # not representable in bf16
+    src.gate.expert_bias = bias.clone()
+    m = from_reference(src)
+    assert m.gate.expert_bias.dtype == torch.float32 and torch.equal(m.gate.expert_bias, bias)
+    assert m.gate.weight.dtype == torch.bfloat16
+    te = tmp_path / "text_encoder"
+    te.mkdir()
+    save_file(export_state({1: src}), str(te / "diffusion_pytorch_model.safetensors"))
+    cfg = {"lm_arch": "poziomka", "lm_blocks": 2, "lm_dense_layers": 1, "lm_dim": d, "lm_moe_intermediate": h,
+           "lm_experts": E, "lm_top_k": 4, "lm_n_group": 4, "lm_topk_group": 2, "lm_routed_scaling": 2.5,
+           "lm_shared_intermediate": sh}
+    (te / "config.json").write_text(json.dumps(cfg))
+    got = load_export(str(tmp_path))[1]
+    assert got.gate.expert_bias.dtype == torch.float32 and torch.equal(got.gate.expert_bias, bias)
+    assert got.gate.weight.dtype == torch.bfloat16 and got._wgu_s.dtype == torch.bfloat16

@@ -1371,6 +1371,8 @@ int hmoe_dispatch(const void* topk_ids, int ids_dtype, const void* topk_w, int w
   if (w_sorted && !topk_w) return HMOE_ERR_ARG;
   const int64_t M = T * k;
   if (M > INT32_MAX) return HMOE_ERR_SHAPE;
+  // every argument is checked before the first launch: an error leaves counts / starts untouched
+  if (M > 0 && (!topk_ids || !order)) return HMOE_ERR_ARG;
   if (xs && (!x || d <= 0 || d % 8 || ldx % 8 || ldx < d || !al16(x) || !al16(xs))) return HMOE_ERR_ARG;
   if (workspace_bytes < hmoe_dispatch_workspace_size(T, k, E) || !workspace) return HMOE_ERR_WORKSPACE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -1389,7 +1391,6 @@ int hmoe_dispatch(const void* topk_ids, int ids_dtype, const void* topk_w, int w
   hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, s, hist, (int)nblk, E, counts, counts64, starts);
   HMOE_CHECK_LAUNCH();
   if (M > 0) {
-    if (!order) return HMOE_ERR_ARG;
     const int grid = grid_for(T, 4, 8192);
     hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(grid), dim3(256), 0, s, topk_ids, ids64, topk_w, w_dtype, T, k,
                        E, hist, rank, static_cast<const uint16_t*>(x), ldx, d, static_cast<uint16_t*>(xs), order,

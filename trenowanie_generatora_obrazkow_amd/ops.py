@@ -73,16 +73,25 @@ def _rows_index(idx, name, M):
     return None if idx is None else _need(idx, name, (M,), _I32)
 
 
+def _router_args(x, wr):
+    if x.dim() != 2 or wr.dim() != 2 or x.dtype != torch.bfloat16 or wr.dtype != torch.bfloat16:
+        raise TypeError("router expects a bf16 (T, d) x and a bf16 (E, d) weight")
+    if wr.shape[1] != x.shape[1]:
+        raise ValueError(f"router weight {tuple(wr.shape)} does not match x of width {x.shape[1]}")
+    if x.stride(1) != 1:
+        raise ValueError("x rows must be contiguous")
+    L.require_gpu(wr, "router weight")
+
+
 def route_topk(x: torch.Tensor, wr: torch.Tensor, k: int, bias=None, renorm=True, scaling=1.0, want_logits=True):
     """Softmax top-k router -> (logits (T, E) fp32 or None, topk_ids (T, k) int32, topk_w (T, k) fp32)."""
     T, d = x.shape
     E = wr.shape[0]
-    if x.dtype != torch.bfloat16 or wr.dtype != torch.bfloat16:
-        raise TypeError("router expects bf16 x and weight")
-    if x.stride(1) != 1:
-        raise ValueError("x rows must be contiguous")
+    _router_args(x, wr)
     wr = _contig(wr, "router weight")
     if bias is not None:
+        if tuple(bias.shape) != (E,):
+            raise ValueError(f"logit bias: shape {tuple(bias.shape)}, expected ({E},)")
         bias = _contig(bias.to(torch.float32), "bias")
     s = _dev_stream(x)
     logits = torch.empty(T, E, device=x.device, dtype=torch.float32) if want_logits else None
@@ -100,12 +109,11 @@ def route_sigmoid_group(x: torch.Tensor, wr: torch.Tensor, k: int, n_group: int,
     topk_w (T, k) fp32)."""
     T, d = x.shape
     E = wr.shape[0]
-    if x.dtype != torch.bfloat16 or wr.dtype != torch.bfloat16:
-        raise TypeError("router expects bf16 x and weight")
-    if x.stride(1) != 1:
-        raise ValueError("x rows must be contiguous")
+    _router_args(x, wr)
     wr = _contig(wr, "router weight")
     if expert_bias is not None:
+        if tuple(expert_bias.shape) != (E,):
+            raise ValueError(f"expert bias: shape {tuple(expert_bias.shape)}, expected ({E},)")
         expert_bias = _contig(expert_bias.to(torch.float32), "expert bias")
     s = _dev_stream(x)
     scores = torch.empty(T, E, device=x.device, dtype=torch.float32) if want_scores else None
@@ -136,8 +144,10 @@ def dispatch(topk_ids: torch.Tensor, E: int, topk_w=None, x=None, want_counts64=
     M = T * k
     dev = topk_ids.device
     s = _dev_stream(topk_ids)
-    ids = _contig(topk_ids, "topk_ids")
+    ids = _need(topk_ids, "topk_ids", (T, k), (torch.int32, torch.int64))
     if topk_w is not None:
+        if tuple(topk_w.shape) != (T, k):
+            raise ValueError(f"topk_weight: shape {tuple(topk_w.shape)}, expected {(T, k)}")
         topk_w = _contig(topk_w, "topk_weight")
         if topk_w.dtype not in (torch.float32, torch.bfloat16):
             topk_w = topk_w.float()
@@ -152,8 +162,7 @@ def dispatch(topk_ids: torch.Tensor, E: int, topk_w=None, x=None, want_counts64=
     d = 0
     ldx = 0
     if x is not None:
-        if x.dtype != torch.bfloat16 or x.stride(1) != 1:
-            raise ValueError("x must be bf16 with contiguous rows")
+        _need(x, "x", (T, None), _BF16, contig=False)  # xs = x[a_idx] reads rows a_idx < T
         d = x.shape[1]
         ldx = x.stride(0)
         xs = torch.empty(M, d, device=dev, dtype=torch.bfloat16)
@@ -179,33 +188,42 @@ def make_schedule(counts: torch.Tensor, M: int, block_m: int = 64):
     return tuple(out)
 
 
-def _counts(counts):
-    counts = _contig(counts, "counts")
+def _counts(counts, E):
+    """Rows per expert, (E,) int32 or int64 on the GPU: the kernels read E entries."""
     if counts.dtype not in (torch.int32, torch.int64):
         counts = counts.to(torch.int64)
-    return counts
+    return _need(counts, "counts", (E,), (torch.int32, torch.int64))
 
 
 def grouped_mm(a, w, counts, M, a_idx=None, y_idx=None, scale=None, w_scale=None, out=None):
+    """y[y_idx[r] or r] = (a[a_idx[r] or r] @ w[e(r)]) * w_scale[e(r)] * scale[r], y (M, N) bf16.  The index
+    values are trusted (in range: a_idx < rows of a, y_idx < M); everything else is checked here."""
+    if w.dim() != 3 or w.dtype not in (torch.bfloat16, torch.int8):
+        raise TypeError(f"w must be an (E, K, N) bf16 or int8 stack (got {tuple(w.shape)} {w.dtype})")
     E, K, N = w.shape
     s = _dev_stream(a)
-    counts = _counts(counts)
+    counts = _counts(counts, E)
     if a.stride(1) != 1:
         a = a.contiguous()
     if w.stride(2) != 1:
         w = w.contiguous()
+    a_idx = _rows_index(a_idx, "a_idx", M)
+    y_idx = _rows_index(y_idx, "y_idx", M)
+    _need(a, "a", (None, K), _BF16, contig=False, min_rows=min(1, M) if a_idx is not None else M)
+    if a_idx is not None and a.shape[0] * a.stride(0) * 2 >= 2 ** 31:
+        raise ValueError("a gathered through a_idx must span less than 2 GiB (32-bit row offsets)")
     if w_scale is not None:
         w_scale = _contig(w_scale, "w_scale")
         if w_scale.shape != (E, N):
             raise ValueError(f"w_scale must be (E, N) = {(E, N)}, got {tuple(w_scale.shape)}")
+    if out is not None:
+        _need(out, "out", (M, N), _BF16, contig=False)
     y = out if out is not None else torch.empty(M, N, device=a.device, dtype=a.dtype)
     if scale is not None:
         scale = _contig(scale, "scale")
         if scale.dtype not in (torch.bfloat16, torch.float32):
             scale = scale.float()
-    for t, n in ((a_idx, "a_idx"), (y_idx, "y_idx")):
-        if t is not None and (t.dtype != torch.int32 or not t.is_contiguous()):
-            raise ValueError(f"{n} must be contiguous int32")
+        _need(scale, "scale", (M,))
     with _Probe("grouped_mm"):
         L.call("hmoe_grouped_mm", L.ptr(a), a.stride(0), L.dt(a), L.ptr(w), L.dt(w), E, K, N, w.stride(0), w.stride(1),
                L.ptr(counts), L.dt(counts), M, L.ptr(a_idx), L.ptr(y_idx), L.ptr(scale),
@@ -228,11 +246,13 @@ def _w_scale(w, w_s, n):
 def gate_up_swiglu(x, wgu, counts, M, a_idx=None, keep_gu=False, wgu_s=None):
     """act = bf16(bf16(silu(g)) * u) for [g | u] = x[a_idx] @ wgu[e]; wgu bf16, or int8 with per-column scales
     wgu_s (E, 2h) (inference only: no gu)."""
+    if wgu.dim() != 3 or wgu.dtype not in (torch.bfloat16, torch.int8) or wgu.shape[2] % 2:
+        raise TypeError(f"wgu must be an (E, d, 2h) bf16 or int8 stack (got {tuple(wgu.shape)} {wgu.dtype})")
     E, d, h2 = wgu.shape
     h = h2 // 2
     s = _dev_stream(x)
     wgu = _contig(wgu, "wgu")
-    counts = _counts(counts)
+    counts = _counts(counts, E)
     wgu_s = _w_scale(wgu, wgu_s, h2)
     a_idx = _rows_index(a_idx, "a_idx", M)
     _need(x, "x", (None, d), _BF16, contig=False, min_rows=min(1, M) if a_idx is not None else M)
@@ -253,10 +273,12 @@ def gate_up_swiglu(x, wgu, counts, M, a_idx=None, keep_gu=False, wgu_s=None):
 
 def down_scatter(act, wd, counts, M, w_sorted, y_idx, keep_yhat=False, wd_s=None):
     """y[y_idx[r]] = bf16(act[r] @ wd[e] * w_sorted[r]); wd bf16, or int8 with per-column scales wd_s (E, d)."""
+    if wd.dim() != 3 or wd.dtype not in (torch.bfloat16, torch.int8):
+        raise TypeError(f"wd must be an (E, h, d) bf16 or int8 stack (got {tuple(wd.shape)} {wd.dtype})")
     E, h, d = wd.shape
     s = _dev_stream(act)
     wd = _contig(wd, "wd")
-    counts = _counts(counts)
+    counts = _counts(counts, E)
     wd_s = _w_scale(wd, wd_s, d)
     _need(act, "act", (M, h), _BF16)
     y_idx = _rows_index(y_idx, "y_idx", M)
@@ -313,9 +335,9 @@ def combine_bwd(dout, yhat, disp: Dispatch, k):
 def down_dgrad_swiglu(dy, wd, counts, M, gu, a_idx=None, w_sorted=None):
     """dgu (M, 2h) from the upstream gradient dy (T, d) gathered through a_idx (or sorted rows (M, d) when a_idx is
     None) and scaled by w_sorted in fp32."""
+    _need(wd, "wd", (None, None, None), _BF16)
     E, h, d = wd.shape
-    wd = _contig(wd, "wd")
-    counts = _counts(counts)
+    counts = _counts(counts, E)
     a_idx = _rows_index(a_idx, "a_idx", M)
     _need(dy, "dy", (None, d), _BF16, min_rows=min(1, M) if a_idx is not None else M)
     _need(gu, "gu", (M, 2 * h), _BF16)
@@ -329,9 +351,9 @@ def down_dgrad_swiglu(dy, wd, counts, M, gu, a_idx=None, w_sorted=None):
 
 
 def gate_up_dgrad(dgu, wgu, counts, M, dtype=torch.float32):
+    _need(wgu, "wgu", (None, None, None), _BF16)
     E, d, h2 = wgu.shape
-    wgu = _contig(wgu, "wgu")
-    counts = _counts(counts)
+    counts = _counts(counts, E)
     _need(dgu, "dgu", (M, h2), _BF16)
     dxs = torch.empty(M, d, device=dgu.device, dtype=dtype)
     with _Probe("gate_up_dgrad"):
@@ -343,10 +365,9 @@ def gate_up_dgrad(dgu, wgu, counts, M, dtype=torch.float32):
 def grouped_wgrad(a, b, counts, E, dtype=torch.bfloat16):
     M, P = a.shape
     N = b.shape[1]
-    counts = _counts(counts)
+    counts = _counts(counts, E)
     _need(a, "a", (M, P), _BF16, contig=False)
     _need(b, "b", (M, N), _BF16, contig=False)
-    _need(counts, "counts", (E,), (torch.int32, torch.int64))
     dw = torch.empty(E, P, N, device=a.device, dtype=dtype)
     with _Probe("grouped_wgrad"):
         L.call("hmoe_grouped_wgrad", L.ptr(a), a.stride(0), L.ptr(b), b.stride(0), E, P, N, L.ptr(counts), L.dt(counts), M,

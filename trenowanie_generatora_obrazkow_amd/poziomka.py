@@ -187,9 +187,21 @@ def load_export(path, device=None, dtype=torch.bfloat16) -> dict:
             m = PoziomkaMoE(cfg["lm_dim"], cfg["lm_moe_intermediate"], cfg["lm_experts"], cfg["lm_top_k"],
                             cfg["lm_n_group"], cfg["lm_topk_group"], cfg["lm_routed_scaling"],
                             cfg["lm_shared_intermediate"])
-            m.load_state_dict({k: f.get_tensor(pre + k) for k in _MOE_KEYS}, strict=True)
-            blocks[i] = m.to(dtype=dtype).to(device=device) if device is not None else m.to(dtype=dtype)
+            sd = {k: f.get_tensor(pre + k) for k in _MOE_KEYS}
+            m.gate.expert_bias = torch.empty_like(sd["gate.expert_bias"])  # loaded in the dtype it was stored in
+            m.load_state_dict(sd, strict=True)
+            blocks[i] = _place(m, dtype, device)
     return blocks
+
+
+def _place(m: PoziomkaMoE, dtype, device) -> PoziomkaMoE:
+    """m's floating tensors in `dtype` on `device`, except the expert bias: it only takes part in the selection,
+    which the reference computes as scores + expert_bias.float() (aurora/hf_pipeline.py:353), so it keeps the
+    precision it has (an fp32 bias rounded to bf16 could select other experts)."""
+    bias = m.gate.expert_bias
+    m = m.to(dtype=dtype)
+    m.gate.expert_bias = bias
+    return m.to(device=device) if device is not None else m
 
 
 def export_state(blocks: dict) -> dict:
@@ -204,7 +216,8 @@ def from_reference(mod) -> PoziomkaMoE:
     E, d, h2 = mod._wgu.shape
     sh = mod.shared_experts.gate_proj.weight.shape[0]
     m = PoziomkaMoE(d, h2 // 2, E, mod.top_k, mod.n_group, mod.topk_group, mod.scaling, sh)
-    m = m.to(device=mod._wgu.device, dtype=mod.gate.weight.dtype)
+    m.gate.expert_bias = torch.empty_like(mod.gate.expert_bias)  # the reference block's bias keeps its dtype
+    m = _place(m, mod.gate.weight.dtype, mod._wgu.device)
     m.load_state_dict(mod.state_dict(), strict=True)
     return m
 
