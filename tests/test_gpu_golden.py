@@ -61,7 +61,7 @@ def test_golden_layer():
     out, ids, tw = moe_swiglu(x, wr, wgu, wd, k)
     out.backward(t_bf16(lz["dout"]).cuda())
     np.testing.assert_array_equal(ids.cpu().numpy(), lz["ids"])
-    np.testing.assert_array_equal(tw.cpu().numpy().view(np.uint32), lz["w"].view(np.uint32))
+    np.testing.assert_array_equal(tw.detach().cpu().numpy().view(np.uint32), lz["w"].view(np.uint32))
     assert_close_bf16(f32(out), f32(t_bf16(lz["out"])), "out")
     from oracle.moe_oracle import round_bf16
     for name, t in (("dx", x), ("dwr", wr), ("dwgu", wgu), ("dwd", wd)):

@@ -68,7 +68,7 @@ def test_layer_forward_c3_sampled(oracle):
     out, ids, tw, _ = _run_layer(x, wr, wgu, wd, k)
     logits, rids, rw = oracle.route(bits(x), bits(wr), k)
     np.testing.assert_array_equal(ids.cpu().numpy(), rids)
-    np.testing.assert_array_equal(tw.cpu().numpy().view(np.uint32), rw.view(np.uint32))
+    np.testing.assert_array_equal(tw.detach().cpu().numpy().view(np.uint32), rw.view(np.uint32))
     tok = np.random.default_rng(0).choice(T, 192, replace=False)
     ref = oracle.moe_forward(f32(x), rids, rw, f32(wgu), f32(wd), tokens=tok)
     assert_close_bf16(f32(out)[tok], ref["out"], "out C3 sampled")
@@ -214,7 +214,7 @@ def test_layer_c4_full_size(oracle):
     out, ids, tw, (xg, wrg, wgug, wdg) = _run_layer(x, wr, wgu, wd, k, dout=dout, bias=bias)
     logits, rids, rw = oracle.route(bits(x), bits(wr), k, bias=bias)
     np.testing.assert_array_equal(ids.cpu().numpy(), rids)
-    np.testing.assert_array_equal(tw.cpu().numpy().view(np.uint32), rw.view(np.uint32))
+    np.testing.assert_array_equal(tw.detach().cpu().numpy().view(np.uint32), rw.view(np.uint32))
     counts = ops.dispatch(ids, E).counts.cpu()
     ref_counts = torch.bincount(torch.from_numpy(rids).reshape(-1).long(), minlength=E)
     assert torch.equal(counts.long(), ref_counts)
