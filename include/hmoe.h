@@ -34,6 +34,7 @@ extern "C" {
 #define HMOE_ERR_LAUNCH (-4)    /* hipGetLastError reported a launch failure */
 #define HMOE_ERR_WORKSPACE (-5) /* workspace missing or smaller than the *_workspace_size query */
 #define HMOE_ERR_DEVICE (-6)    /* device query failed */
+#define HMOE_ERR_TOO_LARGE (-7) /* input beyond the fixed device scratch of an allocation-free entry point */
 
 #define HMOE_DT_BF16 0
 #define HMOE_DT_F16 1
@@ -92,6 +93,19 @@ int hmoe_dispatch(const void* topk_ids, int ids_dtype, const void* topk_w, int w
                   const void* x, int64_t ldx, int64_t d, void* xs, int32_t* counts, int64_t* counts64,
                   int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos, uint16_t* w_sorted,
                   void* workspace, size_t workspace_bytes, hmoe_stream_t stream);
+
+/* Allocation-free form of hmoe_dispatch.  No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same arguments, checks and
+ * outputs as hmoe_dispatch, without the workspace: the kernels use a fixed device array of 8 MiB inside the library
+ * (one per GPU, held until the process ends), so the call allocates nothing.  Inputs whose workspace
+ * (hmoe_dispatch_workspace_size(T, k, E)) exceeds 8 MiB are refused with HMOE_ERR_TOO_LARGE before any launch
+ * (about 1.9 million routed rows T * k at E <= 16; C3 needs 136 KiB).  Every call on a GPU shares that GPU's array: calls
+ * that overlap in time on one GPU (other streams, other host threads) race and must be serialised by the caller.
+ * Each call writes every scratch entry it reads, so no state carries over between calls. */
+int hmoe_dispatch_noalloc(const void* topk_ids, int ids_dtype, const void* topk_w, int w_dtype, int64_t T, int k,
+                          int E, const void* x, int64_t ldx, int64_t d, void* xs, int32_t* counts, int64_t* counts64,
+                          int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos, uint16_t* w_sorted,
+                          hmoe_stream_t stream);
 
 /* make_schedule: replaces aurora/moe_triton.py:93-107.  For each of the ceil(M / block_m) + E blocks: the expert
  * (or -1), the first sorted row and the end row of that expert, int32, computed on the device from counts

@@ -50,7 +50,8 @@ def test_exports_nothing_undeclared(lib):
 def test_version_and_errors(lib):
     L = lib.lib()
     assert L.hmoe_abi_version() == 1
-    for code, word in ((0, "ok"), (-1, "argument"), (-2, "shape"), (-3, "type"), (-4, "launch"), (-5, "workspace")):
+    for code, word in ((0, "ok"), (-1, "argument"), (-2, "shape"), (-3, "type"), (-4, "launch"), (-5, "workspace"),
+                       (-7, "scratch")):
         assert word in L.hmoe_error_string(code).decode()
 
 

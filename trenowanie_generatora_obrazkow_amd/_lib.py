@@ -32,6 +32,8 @@ SIGNATURES = {
     "hmoe_dispatch_workspace_size": (_SZ, [_I64, _I32, _I32]),
     "hmoe_dispatch": (_I32, [_P, _I32, _P, _I32, _I64, _I32, _I32, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P,
                              _P, _SZ, _P]),
+    "hmoe_dispatch_noalloc": (_I32, [_P, _I32, _P, _I32, _I64, _I32, _I32, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P,
+                                     _P, _P]),
     "hmoe_make_schedule": (_I32, [_P, _I32, _I32, _I64, _I32, _P, _P, _P, _P]),
     "hmoe_grouped_mm": (_I32, [_P, _I64, _I32, _P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P,
                                _I32, _P, _I32, _P, _I64, _P]),

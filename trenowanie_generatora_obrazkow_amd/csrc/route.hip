@@ -2,6 +2,8 @@
 // points.  HBM-bound integer/byte work: vectorised 16-byte row copies, wave ballots for the stable ranks.
 #include "hmoe_common.h"
 
+#include <atomic>
+
 namespace hmoe {
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -1288,6 +1290,82 @@ static int route_check(const void* x, int64_t ldx, const void* wr, int64_t T, in
   return HMOE_OK;
 }
 
+static size_t dispatch_ws_bytes(int64_t T, int k, int E) {
+  const int64_t M = T * k;
+  const int64_t nblk = (M + kFPB - 1) / kFPB;
+  const size_t hist = (size_t)(nblk > 0 ? nblk : 1) * (size_t)E * 4;
+  const size_t rank = (size_t)(M > 0 ? M : 1) * 4;
+  return ((hist + 255) / 256) * 256 + ((rank + 255) / 256) * 256;
+}
+
+// hmoe_dispatch with its workspace given: every argument is checked before the first launch, so an error leaves
+// counts / starts untouched.  The workspace holds the per-block histograms (then their exclusive offsets) and the
+// per-row ranks; each call writes every entry it later reads, so nothing in it has to start at zero.
+static int dispatch_impl(const void* topk_ids, int ids_dtype, const void* topk_w, int w_dtype, int64_t T, int k, int E,
+                         const void* x, int64_t ldx, int64_t d, void* xs, int32_t* counts, int64_t* counts64,
+                         int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos, uint16_t* w_sorted,
+                         void* workspace, size_t workspace_bytes, hipStream_t s) {
+  if (T < 0 || k <= 0 || E <= 0) return HMOE_ERR_ARG;
+  if (E > kMaxEDispatch || k > kMaxK) return HMOE_ERR_SHAPE;
+  if (!counts || !starts) return HMOE_ERR_ARG;
+  if (ids_dtype != HMOE_DT_I32 && ids_dtype != HMOE_DT_I64) return HMOE_ERR_DTYPE;
+  if (topk_w && w_dtype != HMOE_DT_F32 && w_dtype != HMOE_DT_BF16) return HMOE_ERR_DTYPE;
+  if (w_sorted && !topk_w) return HMOE_ERR_ARG;
+  const int64_t M = T * k;
+  if (M > INT32_MAX) return HMOE_ERR_SHAPE;
+  if (M > 0 && (!topk_ids || !order)) return HMOE_ERR_ARG;
+  if (xs && (!x || d <= 0 || d % 8 || ldx % 8 || ldx < d || !al16(x) || !al16(xs))) return HMOE_ERR_ARG;
+  if (workspace_bytes < dispatch_ws_bytes(T, k, E) || !workspace) return HMOE_ERR_WORKSPACE;
+  const int64_t nblk = (M + kFPB - 1) / kFPB;
+  int32_t* hist = static_cast<int32_t*>(workspace);
+  const size_t hist_bytes = (((size_t)(nblk > 0 ? nblk : 1) * (size_t)E * 4 + 255) / 256) * 256;
+  int32_t* rank = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + hist_bytes);
+  int nbits = 0;
+  while ((1 << nbits) < E) ++nbits;
+  const int ids64 = ids_dtype == HMOE_DT_I64;
+  if (M > 0) {
+    hipLaunchKernelGGL(dispatch_hist_kernel, dim3((unsigned)nblk), dim3(64), 0, s, topk_ids, ids64, M, E, nbits,
+                       hist, rank);
+    HMOE_CHECK_LAUNCH();
+  }
+  hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, s, hist, (int)nblk, E, counts, counts64, starts);
+  HMOE_CHECK_LAUNCH();
+  if (M > 0) {
+    const int grid = grid_for(T, 4, 8192);
+    hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(grid), dim3(256), 0, s, topk_ids, ids64, topk_w, w_dtype, T, k,
+                       E, hist, rank, static_cast<const uint16_t*>(x), ldx, d, static_cast<uint16_t*>(xs), order,
+                       a_idx, inv_pos, w_sorted);
+    HMOE_CHECK_LAUNCH();
+  }
+  return HMOE_OK;
+}
+
+// Device scratch of hmoe_dispatch_noalloc: the workspace hmoe_dispatch would take, as a file-scope device array (one
+// copy per GPU, held until the process ends).  Host code never uses this name as an address: its device address is
+// looked up once per device with hipGetSymbolAddress and kept in g_scratch_ptr.
+constexpr size_t kDispatchScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) unsigned char scratch[kDispatchScratchBytes];
+static std::atomic<void*> g_scratch_ptr[64];
+
+// The current device's address of `scratch` (nullptr with *rc set when the device or the lookup fails).
+static void* dispatch_scratch(int* rc) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    *rc = HMOE_ERR_DEVICE;
+    return nullptr;
+  }
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+      *rc = HMOE_ERR_DEVICE;
+      return nullptr;
+    }
+    g_scratch_ptr[dev].store(p, std::memory_order_release);  // racing first calls store the same address
+  }
+  *rc = HMOE_OK;
+  return p;
+}
+
 }  // namespace hmoe
 
 using namespace hmoe;
@@ -1305,6 +1383,8 @@ const char* hmoe_error_string(int code) {
     case HMOE_ERR_LAUNCH: return "kernel launch failed";
     case HMOE_ERR_WORKSPACE: return "workspace missing or too small";
     case HMOE_ERR_DEVICE: return "device query failed";
+    case HMOE_ERR_TOO_LARGE:
+      return "input too large for the fixed device scratch of an allocation-free entry point (use the workspace form)";
     default: return "unknown error";
   }
 }
@@ -1351,53 +1431,28 @@ int hmoe_route_sigmoid_group(const void* x, int64_t ldx, const void* wr, const f
   return HMOE_OK;
 }
 
-size_t hmoe_dispatch_workspace_size(int64_t T, int k, int E) {
-  const int64_t M = T * k;
-  const int64_t nblk = (M + kFPB - 1) / kFPB;
-  const size_t hist = (size_t)(nblk > 0 ? nblk : 1) * (size_t)E * 4;
-  const size_t rank = (size_t)(M > 0 ? M : 1) * 4;
-  return ((hist + 255) / 256) * 256 + ((rank + 255) / 256) * 256;
-}
+size_t hmoe_dispatch_workspace_size(int64_t T, int k, int E) { return dispatch_ws_bytes(T, k, E); }
 
 int hmoe_dispatch(const void* topk_ids, int ids_dtype, const void* topk_w, int w_dtype, int64_t T, int k, int E,
                   const void* x, int64_t ldx, int64_t d, void* xs, int32_t* counts, int64_t* counts64,
                   int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos, uint16_t* w_sorted,
                   void* workspace, size_t workspace_bytes, hmoe_stream_t stream) {
+  return dispatch_impl(topk_ids, ids_dtype, topk_w, w_dtype, T, k, E, x, ldx, d, xs, counts, counts64, starts, order,
+                       a_idx, inv_pos, w_sorted, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+int hmoe_dispatch_noalloc(const void* topk_ids, int ids_dtype, const void* topk_w, int w_dtype, int64_t T, int k,
+                          int E, const void* x, int64_t ldx, int64_t d, void* xs, int32_t* counts, int64_t* counts64,
+                          int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos, uint16_t* w_sorted,
+                          hmoe_stream_t stream) {
   if (T < 0 || k <= 0 || E <= 0) return HMOE_ERR_ARG;
   if (E > kMaxEDispatch || k > kMaxK) return HMOE_ERR_SHAPE;
-  if (!counts || !starts) return HMOE_ERR_ARG;
-  if (ids_dtype != HMOE_DT_I32 && ids_dtype != HMOE_DT_I64) return HMOE_ERR_DTYPE;
-  if (topk_w && w_dtype != HMOE_DT_F32 && w_dtype != HMOE_DT_BF16) return HMOE_ERR_DTYPE;
-  if (w_sorted && !topk_w) return HMOE_ERR_ARG;
-  const int64_t M = T * k;
-  if (M > INT32_MAX) return HMOE_ERR_SHAPE;
-  // every argument is checked before the first launch: an error leaves counts / starts untouched
-  if (M > 0 && (!topk_ids || !order)) return HMOE_ERR_ARG;
-  if (xs && (!x || d <= 0 || d % 8 || ldx % 8 || ldx < d || !al16(x) || !al16(xs))) return HMOE_ERR_ARG;
-  if (workspace_bytes < hmoe_dispatch_workspace_size(T, k, E) || !workspace) return HMOE_ERR_WORKSPACE;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int64_t nblk = (M + kFPB - 1) / kFPB;
-  int32_t* hist = static_cast<int32_t*>(workspace);
-  const size_t hist_bytes = (((size_t)(nblk > 0 ? nblk : 1) * (size_t)E * 4 + 255) / 256) * 256;
-  int32_t* rank = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + hist_bytes);
-  int nbits = 0;
-  while ((1 << nbits) < E) ++nbits;
-  const int ids64 = ids_dtype == HMOE_DT_I64;
-  if (M > 0) {
-    hipLaunchKernelGGL(dispatch_hist_kernel, dim3((unsigned)nblk), dim3(64), 0, s, topk_ids, ids64, M, E, nbits,
-                       hist, rank);
-    HMOE_CHECK_LAUNCH();
-  }
-  hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, s, hist, (int)nblk, E, counts, counts64, starts);
-  HMOE_CHECK_LAUNCH();
-  if (M > 0) {
-    const int grid = grid_for(T, 4, 8192);
-    hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(grid), dim3(256), 0, s, topk_ids, ids64, topk_w, w_dtype, T, k,
-                       E, hist, rank, static_cast<const uint16_t*>(x), ldx, d, static_cast<uint16_t*>(xs), order,
-                       a_idx, inv_pos, w_sorted);
-    HMOE_CHECK_LAUNCH();
-  }
-  return HMOE_OK;
+  if (T > INT32_MAX / k || dispatch_ws_bytes(T, k, E) > kDispatchScratchBytes) return HMOE_ERR_TOO_LARGE;
+  int rc = HMOE_OK;
+  void* ws = dispatch_scratch(&rc);
+  if (rc) return rc;
+  return dispatch_impl(topk_ids, ids_dtype, topk_w, w_dtype, T, k, E, x, ldx, d, xs, counts, counts64, starts, order,
+                       a_idx, inv_pos, w_sorted, ws, kDispatchScratchBytes, reinterpret_cast<hipStream_t>(stream));
 }
 
 int hmoe_make_schedule(const void* counts, int counts_dtype, int E, int64_t M, int block_m, int32_t* block_e,
