@@ -32,10 +32,13 @@ constexpr int kMaxEGemm = 1024;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-template <int BM_, int BN_, int WM_, int WN_, int GM_, int BE_ = 2>
+template <int BM_, int BN_, int WM_, int WN_, int GM_, int BE_ = 2, bool PP_ = false>
 struct Cfg {
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, GM = GM_;
   static constexpr int BE = BE_;  // bytes per B element: 2 (bf16) or 1 (int8 weights)
+  // PP: two groups of four waves (one wave of each group per SIMD) alternate between an MFMA phase and a phase of
+  // fragment reads and ring copies (see the kernel's ping-pong loop)
+  static constexpr bool PP = PP_;
   static constexpr int NWAVES = WM * WN, NT = NWAVES * 64;
   static constexpr int TM = BM / WM, TN = BN / WN;
   static constexpr int FM = TM / 32, FN = TN / 32;
@@ -85,9 +88,13 @@ __device__ __forceinline__ i32x4 make_rsrc(const void* base) {
 // 16 bytes per lane from base + voff + soff into LDS at lds + 16 * lane (lds is wave-uniform; it goes to M0).
 // Issued as inline asm so the compiler does not guard every later LDS read with a vmcnt(0) wait for it: completion
 // of these copies is tracked explicitly (wait_vm + barrier before a slice is read).
+// Wait states: a vector memory instruction that reads an SGPR written by a VALU instruction (v_readfirstlane of a
+// descriptor word, the reload of a spilled SGPR) needs 5 wait states after that write, and a write of M0 needs 1
+// before the LDS-bound load reads it.  The compiler provides neither for inline asm, so the s_nop 4 after the M0
+// write covers both.
 __device__ __forceinline__ void buf2lds(uint32_t voff, i32x4 rsrc, uint32_t soff, char* lds) {
   const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(lds);
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :: "s"(m0), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
 }
 
@@ -416,9 +423,12 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
 
   typename TileSel<A_MN, C::BM, C::NWAVES>::type ta;
   typename TileSel<B_MN, C::BN, C::NWAVES, C::BE, C::FN>::type tb;
-  static_assert(C::FSM == 64 && C::FSN == 64, "fragment reads assume two waves along each tile dimension");
-  const int loff_a = decltype(ta)::lane_off(wm, lane);
-  const int loff_b = decltype(tb)::lane_off(wn, lane);
+  // A wave's fragment f along a dimension covers 32 rows / columns from f * FS + 32 w: the lane part of the read
+  // address is that of wave (w & 1) inside a 64-wide group, and 64 * (w >> 1) selects the group.
+  static_assert(C::FSM % 64 == 0 && C::FSN % 64 == 0, "fragment reads work on 64-wide groups");
+  const int loff_a = decltype(ta)::lane_off(wm & 1, lane);
+  const int loff_b = decltype(tb)::lane_off(wn & 1, lane);
+  const int wgrp_a = 64 * (wm >> 1), wgrp_b = 64 * (wn >> 1);
 
   // XCD-aware slot: consecutive workgroup ids are dealt round-robin over the 8 XCDs; give each XCD a contiguous
   // range of tile ids so the tiles it runs share A rows and B columns in its L2.
@@ -664,9 +674,10 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
       auto read = [&](const char* slot, int ks) {
         Frags f;
 #pragma unroll
-        for (int a = 0; a < FE; ++a) f.xa[a] = TA::frag(slot, a * C::FSM, loff_a, ks);
+        for (int a = 0; a < FE; ++a) f.xa[a] = TA::frag(slot, a * C::FSM + wgrp_a, loff_a, ks);
 #pragma unroll
-        for (int j = 0; j < NL; ++j) f.wb[bf(j)] = TB::frag(slot + C::A_BYTES, bf(j) * C::FSN, loff_b, ks);
+        for (int j = 0; j < NL; ++j)
+          f.wb[bf(j)] = TB::frag(slot + C::A_BYTES, bf(j) * C::FSN + wgrp_b, loff_b, ks);
         return f;
       };
       auto mfmas = [&](const Frags f) {
@@ -760,9 +771,9 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
             const int i = a * NL + j, b = bf(j);
             acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f1.wb[b], f1.xa[a], acc[a][b], 0, 0, 0);
             if (i < FE)
-              f0.xa[i] = TA::frag(cons, i * C::FSM, loff_a, 0);
+              f0.xa[i] = TA::frag(cons, i * C::FSM + wgrp_a, loff_a, 0);
             else if (i < FE + NL)
-              f0.wb[bf(i - FE)] = TB::frag(cons + C::A_BYTES, bf(i - FE) * C::FSN, loff_b, 0);
+              f0.wb[bf(i - FE)] = TB::frag(cons + C::A_BYTES, bf(i - FE) * C::FSN + wgrp_b, loff_b, 0);
             if ((i & 1) && refill) copy(i >> 1);
             __builtin_amdgcn_sched_barrier(0);
           }
@@ -770,9 +781,9 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int i = FE * NL; i < FE + NL; ++i) {
           if (i < FE)
-            f0.xa[i] = TA::frag(cons, i * C::FSM, loff_a, 0);
+            f0.xa[i] = TA::frag(cons, i * C::FSM + wgrp_a, loff_a, 0);
           else
-            f0.wb[bf(i - FE)] = TB::frag(cons + C::A_BYTES, bf(i - FE) * C::FSN, loff_b, 0);
+            f0.wb[bf(i - FE)] = TB::frag(cons + C::A_BYTES, bf(i - FE) * C::FSN + wgrp_b, loff_b, 0);
         }
 #pragma unroll
         for (int l = FE * NL / 2; l < LOADS; ++l) {
@@ -786,10 +797,89 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
       for (; kt < nfast; ++kt) iter(kt, std::true_type{});
       for (; kt < nk; ++kt) iter(kt, std::false_type{});
     };
+    // Ping-pong loop (C::PP): the two groups of four waves (G = wave / 4; one wave of each group per SIMD) run a
+    // sequence of 2 nk + 1 phases separated by workgroup barriers, G1 one phase behind G0:
+    //   phase p, rel = p - G:  rel even -> memory phase of slice rel / 2: read this wave's fragments of the slice (both
+    //                          k16 steps) into registers and issue its copies of slice + 3 into the ring slot of
+    //                          slice - 1 (both groups have read that slot by now);
+    //                          rel odd  -> MFMA phase of slice rel / 2 on the fragments read in the previous phase.
+    // So in every phase one wave of each SIMD issues only MFMAs while the other reads LDS and issues copies; the LDS
+    // read rate of two waves per SIMD is about twice that of one.  Before the barrier that ends an odd phase 2q + 1
+    // every wave waits for its copies of slice q + 1, which G0 reads in the next phase.
+    auto pp_loop = [&](auto fe_tag) {
+      constexpr int FE = decltype(fe_tag)::value;
+      static_assert(C::NWAVES == 8 && kNStage == 4, "ping-pong: two groups of four waves over a 4-deep ring");
+      const int G = __builtin_amdgcn_readfirstlane(wave >> 2);
+      auto slot_of = [&](int s) -> char* { return smem + (s & (kNStage - 1)) * C::STAGE_BYTES; };
+      auto issue_at = [&](int s) {
+        char* dst = slot_of(s);
+        ta.issue(dst, wave, lane, s * kBK);
+        tb.issue(dst + C::A_BYTES, wave, lane, s * kBK);
+      };
+      Frags fr[2];
+#pragma unroll
+      for (int s = 0; s < kNStage; ++s)
+        if (s < nk) issue_at(s);
+      if (nk > 0) {
+        const int ahead = min(nk - 1, kNStage - 1);
+        if (ahead >= 3)
+          wait_vm<3 * LOADS>();
+        else if (ahead == 2)
+          wait_vm<2 * LOADS>();
+        else if (ahead == 1)
+          wait_vm<LOADS>();
+        else
+          wait_vm<0>();
+      }
+      lds_barrier();
+      const int phases = 2 * nk + 1;
+      for (int ph = 0; ph < phases; ++ph) {
+        const int rel = ph - G;
+        if (rel >= 0 && rel < 2 * nk) {
+          const int s = rel >> 1;
+          if ((rel & 1) == 0) {
+            if (s >= 1 && s + kNStage - 1 < nk) issue_at(s + kNStage - 1);
+            const char* slot = slot_of(s);
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+              for (int a = 0; a < FE; ++a) fr[ks].xa[a] = TA::frag(slot, a * C::FSM + wgrp_a, loff_a, ks);
+#pragma unroll
+              for (int j = 0; j < C::FN; ++j)
+                fr[ks].wb[j] = TB::frag(slot + C::A_BYTES, j * C::FSN + wgrp_b, loff_b, ks);
+            }
+          } else {
+            __builtin_amdgcn_s_setprio(2);
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+              for (int a = 0; a < FE; ++a)
+#pragma unroll
+                for (int j = 0; j < C::FN; ++j)
+                  acc[a][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fr[ks].wb[j], fr[ks].xa[a], acc[a][j], 0, 0, 0);
+            __builtin_amdgcn_s_setprio(0);
+          }
+        }
+        if (ph & 1) {
+          const int ahead = min(2, nk - 2 - (ph >> 1));  // copy batches this wave issued after slice q + 1's
+          if (ahead >= 2)
+            wait_vm<2 * LOADS>();
+          else if (ahead == 1)
+            wait_vm<LOADS>();
+          else if (ahead == 0)
+            wait_vm<0>();
+        }
+        lds_barrier();
+      }
+    };
     // a SwiGLU n-tile whose gate columns end within the first 64 of its 128 (e.g. the last n-tile at h = 320)
     // runs with the live B fragments only
     constexpr bool NHALF = EPI == EPI_SWIGLU && C::FN == 4;
     auto run_loop = [&](auto fe_tag) {
+      if constexpr (C::PP) {
+        pp_loop(fe_tag);
+        return;
+      }
       if constexpr (NHALF) {
         if (p.N - n0 <= C::BN / 4) {
           main_loop(fe_tag, std::integral_constant<int, 2>{});
@@ -1117,6 +1207,8 @@ using CfgL = Cfg<256, 256, 2, 2, 4>;
 using CfgS = Cfg<128, 128, 2, 2, 4>;
 using CfgL8 = Cfg<256, 256, 2, 2, 4, 1>;  // int8 weights (N-contiguous), bf16 activations
 using CfgS8 = Cfg<128, 128, 2, 2, 4, 1>;
+// Ping-pong: 256x256 tile, 8 waves of 128x64 (FM = 4, FN = 2: 128 accumulators each, two waves per SIMD)
+using CfgLP = Cfg<256, 256, 2, 4, 4, 2, true>;
 
 template <class C, int EPI>
 static inline int64_t mgroup_tiles(int64_t M, int64_t E, int64_t ncols) {
@@ -1161,10 +1253,18 @@ static bool pick_large_mgroup(int64_t tiles_large, int64_t ncols, int64_t K) {
   return K >= 16 * kBK;
 }
 
+static inline bool env_pp() {
+  const char* v = getenv("HMOE_GEMM_PP");
+  return v && v[0] == '1';
+}
+
 template <int MODE, bool A_MN, bool B_MN, int EPI>
 static int launch_mgroup(const GemmParams& p, int64_t ncols, hipStream_t s) {
   const int64_t tl = mgroup_tiles<CfgL, EPI>(p.M, p.E, ncols);
-  if (pick_large_mgroup<EPI>(tl, ncols, p.K)) return launch<CfgL, MODE, A_MN, B_MN, EPI>(p, tl, s);
+  if (pick_large_mgroup<EPI>(tl, ncols, p.K)) {
+    if (env_pp()) return launch<CfgLP, MODE, A_MN, B_MN, EPI>(p, tl, s);
+    return launch<CfgL, MODE, A_MN, B_MN, EPI>(p, tl, s);
+  }
   return launch<CfgS, MODE, A_MN, B_MN, EPI>(p, mgroup_tiles<CfgS, EPI>(p.M, p.E, ncols), s);
 }
 
