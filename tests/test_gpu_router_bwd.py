@@ -50,7 +50,8 @@ def test_router_bwd_and_unpermute(oracle, T, d, E, k, renorm):
 
 
 @pytest.mark.parametrize("T,d,E,k,dt", [(4100, 1536, 16, 2, torch.float32), (4096, 1024, 12, 3, torch.bfloat16),
-                                        (5000, 2048, 16, 1, torch.float32)])
+                                        (5000, 2048, 16, 1, torch.float32), (4099, 1536, 16, 2, torch.bfloat16),
+                                        (3001, 1536, 20, 2, torch.float32)])
 def test_unpermute_many_tokens(oracle, T, d, E, k, dt):
     """Many tokens (workgroups walk several tokens each): dx = sum_j dxs[inv_pos[t, j]] + dlogits @ Wr, fp32 and
     bf16 row sums, against float64, and bit-equal to the same sums taken for the first tokens alone."""
