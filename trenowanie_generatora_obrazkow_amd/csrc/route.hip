@@ -318,6 +318,70 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restr
   const int nwaves = blockDim.x >> 6;
   const int wave = threadIdx.x >> 6;
   constexpr int TPW = SEG ? 4 : 1;
+  if constexpr (SEG && NCH <= 4) {
+    // The four tokens together (rows up to 2048 elements): each 8-element piece of a weight row is loaded and widened
+    // once and serves all four tokens' partials, which accumulate in the same order as one token at a time (the x
+    // pieces of a chunk, for the four tokens, stay in registers meanwhile).  All experts fit one group (E <= G).
+    constexpr int H = G == 8 ? 3 : 4;
+    static_assert(G == 8 || G == 16, "four-token path: E <= 16");
+    for (int t0 = (blockIdx.x * nwaves + wave) * TPW; t0 < T; t0 += gridDim.x * nwaves * TPW) {
+      float p[TPW][G];
+#pragma unroll
+      for (int q = 0; q < TPW; ++q)
+#pragma unroll
+        for (int e = 0; e < G; ++e) p[q][e] = 0.0f;
+      // chunk by chunk (each partial still takes its chunks in order): the four tokens' 8 elements of the chunk,
+      // then every expert's piece of it
+#pragma unroll 1
+      for (int c = 0; c < NCH; ++c) {
+        const int idx = c * 512 + lane * 8;
+        uint4 xr[TPW];
+#pragma unroll
+        for (int q = 0; q < TPW; ++q) {
+          const int t = min(t0 + q, T - 1);  // a token past T repeats row T - 1; its results are not written
+          xr[q] = idx < d ? *reinterpret_cast<const uint4*>(x + (int64_t)t * ldx + idx) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int e = 0; e < G; ++e) {
+          const uint4 wv = *reinterpret_cast<const uint4*>(wr + (int64_t)min(e, E - 1) * d + min(idx, d - 8));
+          const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+          float wf[8];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            wf[2 * j] = bf_lo(ww[j]);
+            wf[2 * j + 1] = bf_hi(ww[j]);
+          }
+#pragma unroll
+          for (int q = 0; q < TPW; ++q) {
+            const uint32_t xw[4] = {xr[q].x, xr[q].y, xr[q].z, xr[q].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              p[q][e] = __builtin_fmaf(bf_lo(xw[j]), wf[2 * j], p[q][e]);
+              p[q][e] = __builtin_fmaf(bf_hi(xw[j]), wf[2 * j + 1], p[q][e]);
+            }
+          }
+          // loads of at most four experts' pieces in flight (registers: occupancy hides the load latency here)
+          if (e % 4 == 3) __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      float seglg = -__builtin_inff();  // token t0 + lane / 16's logit of expert lane % 16
+#pragma unroll
+      for (int q = 0; q < TPW; ++q) {
+        transposed_butterfly<G>(p[q], lane);
+        float v = p[q][0];
+        if constexpr (H < 4) v = bfly_add<4>(v);
+        v = bfly_add<2>(v);
+        v = bfly_add<1>(v);
+        const int my_e = lane >> (6 - H);
+        if (bias && my_e < E) v = __fadd_rn(v, bias[my_e]);
+        const int e = lane & 15;
+        const float val = __shfl(v, (e << (6 - H)) & 63, 64);
+        if ((lane >> 4) == q && e < G && e < E) seglg = val;
+      }
+      route_select16(seglg, t0, lane, T, E, k, renorm, scaling, logits, ids, wout);
+    }
+    return;
+  }
   for (int t0 = (blockIdx.x * nwaves + wave) * TPW; t0 < T; t0 += gridDim.x * nwaves * TPW) {
     [[maybe_unused]] float seglg = -__builtin_inff();  // SEG: token t0 + lane / 16's logit of expert lane % 16
 #pragma unroll 1
