@@ -94,6 +94,22 @@ int hmoe_dispatch(const void* topk_ids, int ids_dtype, const void* topk_w, int w
                   int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos, uint16_t* w_sorted,
                   void* workspace, size_t workspace_bytes, hmoe_stream_t stream);
 
+/* Bytes of the row-group tiles (xs_tiles) for M sorted rows of width d over E experts (an upper bound: it does not
+ * depend on the counts).  0 for invalid sizes. */
+size_t hmoe_xs_tiles_bytes(int64_t M, int E, int64_t d);
+
+/* hmoe_dispatch that can also write the permuted rows as row-group tiles (xs_tiles, NULL to skip;
+ * hmoe_xs_tiles_bytes(T * k, E, d) bytes, 16-byte aligned), the A operand of hmoe_gate_up_swiglu_tiles: the gather
+ * x[order // k] of aurora/hf_compat.py:83 in a layout for the gate/up GEMM's copies.  Layout: the sorted rows of
+ * expert e form groups of 128 rows (the last partial), expert e's first group being the sum over e' < e of
+ * ceil(count[e'] / 128); group g and 32-column slice s occupy the 8 KB at byte (g * ceil(d / 32) + s) * 8192; row r
+ * of a group at r * 64 within it, its 16-byte chunk c (columns 32 s + 8 c ..) at chunk position c ^ ((r >> 2) & 3).
+ * Positions of rows or columns that do not exist are not written.  Other arguments as hmoe_dispatch. */
+int hmoe_dispatch_tiles(const void* topk_ids, int ids_dtype, const void* topk_w, int w_dtype, int64_t T, int k, int E,
+                        const void* x, int64_t ldx, int64_t d, void* xs, void* xs_tiles, int32_t* counts,
+                        int64_t* counts64, int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos,
+                        uint16_t* w_sorted, void* workspace, size_t workspace_bytes, hmoe_stream_t stream);
+
 /* Allocation-free form of hmoe_dispatch.  No counterpart in the reference: it is for callers that cannot allocate
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same arguments, checks and
  * outputs as hmoe_dispatch, without the workspace: the kernels use a fixed device array of 8 MiB inside the library
@@ -137,6 +153,13 @@ int hmoe_grouped_mm(const void* a, int64_t lda, int a_dtype, const void* w, int 
 int hmoe_gate_up_swiglu(const void* x, int64_t ldx, const int32_t* a_idx, const void* wgu, int64_t E, int64_t d,
                         int64_t h, const void* counts, int counts_dtype, int64_t M, void* act, void* gu,
                         hmoe_stream_t stream);
+
+/* hmoe_gate_up_swiglu with the A rows taken from the row-group tiles of hmoe_dispatch_tiles (xs_tiles, written by
+ * a dispatch with the same counts, d and M): the same products and sums, so act and gu are identical; the copies of
+ * the GEMM then read 1 KB runs instead of 64-byte row pieces.  hmoe_xs_tiles_bytes(M, E, d) below 2^31. */
+int hmoe_gate_up_swiglu_tiles(const void* xs_tiles, const void* wgu, int64_t E, int64_t d, int64_t h,
+                              const void* counts, int counts_dtype, int64_t M, void* act, void* gu,
+                              hmoe_stream_t stream);
 
 /* Down projection with routing weight and scatter: replaces aurora/hf_compat.py:80-81 (grouped_mm(act, _wd,
  * counts, sched, y_idx=y_idx, scale=w)).  y[y_idx[r]] = bf16(fp32(act[r] @ wd[e]) * w_sorted[r]); yhat (M, d) bf16

@@ -38,6 +38,10 @@ SIGNATURES = {
     "hmoe_grouped_mm": (_I32, [_P, _I64, _I32, _P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P,
                                _I32, _P, _I32, _P, _I64, _P]),
     "hmoe_gate_up_swiglu": (_I32, [_P, _I64, _P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P]),
+    "hmoe_gate_up_swiglu_tiles": (_I32, [_P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P]),
+    "hmoe_xs_tiles_bytes": (_SZ, [_I64, _I32, _I64]),
+    "hmoe_dispatch_tiles": (_I32, [_P, _I32, _P, _I32, _I64, _I32, _I32, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P,
+                                   _P, _P, _P, _SZ, _P]),
     "hmoe_down_scatter": (_I32, [_P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P, _P, _P]),
     "hmoe_gate_up_swiglu_i8": (_I32, [_P, _I64, _P, _P, _P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _P, _P]),
     "hmoe_down_scatter_i8": (_I32, [_P, _P, _P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P, _P]),

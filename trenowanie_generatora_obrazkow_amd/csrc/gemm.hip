@@ -28,11 +28,13 @@ namespace hmoe {
 // ----------------------------------------------------------------------------------------------------------------
 // The kernel
 // ----------------------------------------------------------------------------------------------------------------
-template <class C, int MODE, bool A_MN, bool B_MN, int EPI>
+// A_BLK: the A rows (MGROUP) come from the row-group tiles of the sorted rows (gemm_common.h), not from A's rows.
+template <class C, int MODE, bool A_MN, bool B_MN, int EPI, bool A_BLK = false>
 __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   __shared__ int64_t s_rstart[kMaxEGemm + 1];
   __shared__ int s_tstart[kMaxEGemm + 1];  // MGROUP: prefix of ceil(count / BM); KGROUP: one m-tile per expert
+  __shared__ int s_gstart[A_BLK ? kMaxEGemm + 1 : 1];  // A_BLK: prefix of ceil(count / 128) (row groups)
   // per-row epilogue inputs of the tile (scatter index, routing weight), double-buffered by tile parity: a wave
   // that has finished its epilogue may already fill the next tile's while others still read this one
   // (2 KB each: 256 rows plus up to 3 leading rows, since the copy starts at the 16-byte boundary below row0)
@@ -51,7 +53,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
   if (wave == 0) {
     const int per = (E + 63) / 64;
     int64_t rs = 0;
-    int ts = 0;
+    int ts = 0, gs = 0;
     for (int i = 0; i < per; ++i) {
       const int e = lane * per + i;
       if (e < E) {
@@ -59,21 +61,24 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
         c = c < 0 ? 0 : (c > p.M ? p.M : c);  // garbage counts must not blow up the tile loop
         rs += c;
         ts += MODE == MGROUP ? (int)((c + C::BM - 1) / C::BM) : 1;
+        if constexpr (A_BLK) gs += (int)((c + kTileGroupRows - 1) / kTileGroupRows);
       }
     }
     int64_t irs = rs;
-    int its = ts;
+    int its = ts, igs = gs;
 #pragma unroll
     for (int s = 1; s < 64; s <<= 1) {
       const int64_t o = __shfl_up(irs, s, 64);
       const int ot = __shfl_up(its, s, 64);
+      const int og = __shfl_up(igs, s, 64);
       if (lane >= s) {
         irs += o;
         its += ot;
+        igs += og;
       }
     }
     int64_t r0 = irs - rs;
-    int t0 = its - ts;
+    int t0 = its - ts, g0 = igs - gs;
     for (int i = 0; i < per; ++i) {
       const int e = lane * per + i;
       if (e < E) {
@@ -83,6 +88,10 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
         s_tstart[e] = t0;
         r0 += c;
         t0 += MODE == MGROUP ? (int)((c + C::BM - 1) / C::BM) : 1;
+        if constexpr (A_BLK) {
+          s_gstart[e] = g0;
+          g0 += (int)((c + kTileGroupRows - 1) / kTileGroupRows);
+        }
       }
     }
     if (lane == 63) {
@@ -180,20 +189,38 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
     if constexpr (MODE == MGROUP) {
       static_assert(!A_MN, "MGROUP A is K-contiguous");
       ta.K = p.K;
-      // gathered rows are addressed from A itself; contiguous rows from the tile's first row
-      ta.rsrc = make_rsrc(p.a_idx ? p.A : p.A + row0 * p.lda);
+      if constexpr (A_BLK) {
+        // row-group tiles: instruction I's 16 rows (tile rows 16 I ..) are one 1 KB run of their group's slice
+        ta.kmul = kTileSliceBytes / kBK;
+        ta.rsrc = make_rsrc(p.A);
+        const int64_t nsl = (p.K + kBK - 1) / kBK;
+        const int64_t rel0 = row0 - s_rstart[e];  // tile start within the expert (a multiple of 64)
 #pragma unroll
-      for (int i = 0; i < ta.PER_WAVE; ++i) {
-        const int rr = ta.row_of(wave, lane, i);
-        const int64_t r = row0 + rr;
-        const int c = (lane & 3) ^ swz_k(rr);
-        uint32_t vo = kOOB;
-        if (r < row_end) {
-          const int64_t src = p.a_idx ? (int64_t)p.a_idx[r] : (int64_t)rr;
-          vo = (uint32_t)(src * p.lda * 2 + c * 16);
+        for (int i = 0; i < ta.PER_WAVE; ++i) {
+          const int rr = ta.row_of(wave, lane, i);
+          const int64_t rel = rel0 + 16 * (wave * ta.PER_WAVE + i);  // the instruction's first row in the expert
+          const int64_t g = s_gstart[e] + rel / kTileGroupRows;
+          ta.voff[i] = row0 + rr < row_end
+                           ? (uint32_t)(g * nsl * kTileSliceBytes + (rel % kTileGroupRows) * 64 + lane * 16)
+                           : kOOB;
+          ta.chunk[i] = (lane & 3) ^ swz_k(rr);
         }
-        ta.voff[i] = vo;
-        ta.chunk[i] = c;
+      } else {
+        // gathered rows are addressed from A itself; contiguous rows from the tile's first row
+        ta.rsrc = make_rsrc(p.a_idx ? p.A : p.A + row0 * p.lda);
+#pragma unroll
+        for (int i = 0; i < ta.PER_WAVE; ++i) {
+          const int rr = ta.row_of(wave, lane, i);
+          const int64_t r = row0 + rr;
+          const int c = (lane & 3) ^ swz_k(rr);
+          uint32_t vo = kOOB;
+          if (r < row_end) {
+            const int64_t src = p.a_idx ? (int64_t)p.a_idx[r] : (int64_t)rr;
+            vo = (uint32_t)(src * p.lda * 2 + c * 16);
+          }
+          ta.voff[i] = vo;
+          ta.chunk[i] = c;
+        }
       }
       tb.rsrc = make_rsrc(static_cast<const char*>(p.B) + (int64_t)e * p.strideBe * C::BE);
       auto gcol = [&](int nn, int& col) -> bool {  // tile column -> weight column
@@ -778,9 +805,9 @@ static int num_cus() {
   return n;
 }
 
-template <class C, int MODE, bool A_MN, bool B_MN, int EPI>
+template <class C, int MODE, bool A_MN, bool B_MN, int EPI, bool A_BLK = false>
 static int launch(const GemmParams& p, int64_t tiles_upper, hipStream_t s) {
-  auto kern = grouped_gemm_kernel<C, MODE, A_MN, B_MN, EPI>;
+  auto kern = grouped_gemm_kernel<C, MODE, A_MN, B_MN, EPI, A_BLK>;
   static std::atomic<bool> attr_set[64];  // per device: the (idempotent) attribute call is done
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return HMOE_ERR_DEVICE;
@@ -852,11 +879,11 @@ static bool pick_large_mgroup(int64_t tiles_large, int64_t ncols, int64_t K) {
   return K >= 16 * kBK;
 }
 
-template <int MODE, bool A_MN, bool B_MN, int EPI>
+template <int MODE, bool A_MN, bool B_MN, int EPI, bool A_BLK = false>
 static int launch_mgroup(const GemmParams& p, int64_t ncols, hipStream_t s) {
   const int64_t tl = mgroup_tiles<CfgL, EPI>(p.M, p.E, ncols);
-  if (pick_large_mgroup<EPI>(tl, ncols, p.K)) return launch<CfgL, MODE, A_MN, B_MN, EPI>(p, tl, s);
-  return launch<CfgS, MODE, A_MN, B_MN, EPI>(p, mgroup_tiles<CfgS, EPI>(p.M, p.E, ncols), s);
+  if (pick_large_mgroup<EPI>(tl, ncols, p.K)) return launch<CfgL, MODE, A_MN, B_MN, EPI, A_BLK>(p, tl, s);
+  return launch<CfgS, MODE, A_MN, B_MN, EPI, A_BLK>(p, mgroup_tiles<CfgS, EPI>(p.M, p.E, ncols), s);
 }
 
 // int8 weights: same tile choice, int8 tile configurations
@@ -974,6 +1001,31 @@ int hmoe_gate_up_swiglu(const void* x, int64_t ldx, const int32_t* a_idx, const 
   p.ldc = h;
   p.aux = static_cast<uint16_t*>(gu);
   return launch_mgroup<MGROUP, false, true, EPI_SWIGLU>(p, h, reinterpret_cast<hipStream_t>(stream));
+}
+
+int hmoe_gate_up_swiglu_tiles(const void* xs_tiles, const void* wgu, int64_t E, int64_t d, int64_t h,
+                              const void* counts, int counts_dtype, int64_t M, void* act, void* gu,
+                              hmoe_stream_t stream) {
+  int rc = check_common(counts, counts_dtype, E, M);
+  if (rc) return rc;
+  if (M == 0) return HMOE_OK;
+  if (!xs_tiles || !wgu || !act || d <= 0 || h <= 0) return HMOE_ERR_ARG;
+  if (d % 8 || h % 8) return HMOE_ERR_SHAPE;
+  if (!al16(xs_tiles) || !al16(wgu) || !al16(act) || !al16(gu)) return HMOE_ERR_ARG;
+  if (!off32(tiles_bytes(M, E, d)) || !off32(d * 2 * h * 2)) return HMOE_ERR_SHAPE;
+  GemmParams p = base_params(counts, counts_dtype, E, M);
+  p.A = static_cast<const uint16_t*>(xs_tiles);
+  p.lda = d;
+  p.B = (wgu);
+  p.ldb = 2 * h;
+  p.strideBe = d * 2 * h;
+  p.K = (int)d;
+  p.N = (int)h;
+  p.h = (int)h;
+  p.C = act;
+  p.ldc = h;
+  p.aux = static_cast<uint16_t*>(gu);
+  return launch_mgroup<MGROUP, false, true, EPI_SWIGLU, true>(p, h, reinterpret_cast<hipStream_t>(stream));
 }
 
 int hmoe_down_scatter(const void* act, const void* wd, int64_t E, int64_t h, int64_t d, const void* counts,

@@ -28,6 +28,16 @@ struct Cfg {
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be a multiple of 32");
 };
 
+// Row-group tiles ("xs tiles"): a copy of the sorted rows of A laid out as the K-major LDS image, so that each direct
+// copy reads 1 KB contiguous instead of 16 rows x 64 bytes.  The sorted rows of expert e form groups of 128 rows
+// (the last one partial); group g of all experts (expert e's first is gstart[e] = sum over e' < e of
+// ceil(count[e'] / 128)) and 32-wide k-slice s occupy the 8 KB at (g * nslices + s) * 8 KB, nslices = ceil(K / 32):
+// row r of the group at r * 64 bytes, its logical 16-byte chunk c at physical chunk c ^ swz_k(r).  A 256-row tile
+// reads two consecutive groups, a 128-row tile one (tiles start at multiples of 64 rows of an expert; the swizzle
+// uses bits 2-3 of the row only, so any 16-row run of a group is a valid piece of a tile's image).
+static_assert(kTileK == kBK, "row-group tiles hold one LDS slice per 32 k");
+constexpr int kTileSliceBytes = kTileGroupRows * kBK * 2;
+
 // ----------------------------------------------------------------------------------------------------------------
 // LDS tile layouts (one k-slice of BK = 32)
 //   K-major  [ROWS][32]: 64-byte rows, four 16-byte chunks; chunk c of row r stored at c ^ ((r >> 2) & 3).
@@ -94,10 +104,11 @@ struct KTile {
   int chunk[PER_WAVE];      // logical k-chunk this lane copies
   i32x4 rsrc;
   int K;
+  uint32_t kmul = 2;  // scalar-offset bytes per k: 2 (rows of A), 256 (row-group tiles: 8 KB per 32-k slice)
   // lane l of instruction (wave w, i) fills LDS row 16*(w*PER_WAVE + i) + l/4, physical chunk l%4
   __device__ __forceinline__ static int row_of(int wave, int lane, int i) { return 16 * (wave * PER_WAVE + i) + lane / 4; }
   __device__ __forceinline__ void issue(char* lds_tile, int wave, int lane, int k0) const {
-    const uint32_t soff = (uint32_t)k0 * 2u;
+    const uint32_t soff = (uint32_t)k0 * kmul;
     if (k0 + kBK <= K) {
 #pragma unroll
       for (int i = 0; i < PER_WAVE; ++i) buf2lds(voff[i], rsrc, soff, lds_tile + (wave * PER_WAVE + i) * 1024);
@@ -110,11 +121,11 @@ struct KTile {
   // the i-th of issue()'s copies alone (the caller spreads them between MFMAs)
   __device__ __forceinline__ void issue_one(char* lds_tile, int wave, int i, int k0) const {
     const uint32_t vo = (k0 + kBK <= K || k0 + chunk[i] * 8 < K) ? voff[i] : kOOB;
-    buf2lds(vo, rsrc, (uint32_t)k0 * 2u, lds_tile + (wave * PER_WAVE + i) * 1024);
+    buf2lds(vo, rsrc, (uint32_t)k0 * kmul, lds_tile + (wave * PER_WAVE + i) * 1024);
   }
   // the same for a slice known to lie inside K (no tail test)
   __device__ __forceinline__ void issue_one_full(char* lds_tile, int wave, int i, int k0) const {
-    buf2lds(voff[i], rsrc, (uint32_t)k0 * 2u, lds_tile + (wave * PER_WAVE + i) * 1024);
+    buf2lds(voff[i], rsrc, (uint32_t)k0 * kmul, lds_tile + (wave * PER_WAVE + i) * 1024);
   }
   // Lane part of a fragment read address: row w32*32 + lane%32, k-chunk lane/32 (ks = 0), swizzled.  The
   // swizzle of row grp64 + w32*32 + lane%32 is that of lane%32, and chunk 2 + c stored at (2 + c) ^ s = (c ^ s) ^ 2,

@@ -9,6 +9,15 @@ namespace hmoe {
 
 constexpr int kWave = 64;
 
+// Row-group tiles of the sorted rows (the layout is described in gemm_common.h): groups of 128 rows, 32-wide k
+// slices of 8 KB.  Bytes needed for M sorted rows of width d over E experts: at most ceil(M / 128) + E groups.
+constexpr int kTileGroupRows = 128;
+constexpr int kTileK = 32;
+inline int64_t tiles_groups_max(int64_t M, int64_t E) { return (M + kTileGroupRows - 1) / kTileGroupRows + E; }
+inline int64_t tiles_bytes(int64_t M, int64_t E, int64_t d) {
+  return tiles_groups_max(M, E) * ((d + kTileK - 1) / kTileK) * (int64_t)(kTileGroupRows * kTileK * 2);
+}
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));

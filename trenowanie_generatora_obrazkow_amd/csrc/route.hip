@@ -628,10 +628,11 @@ __global__ __launch_bounds__(64) void dispatch_hist_kernel(const void* __restric
 __global__ __launch_bounds__(1024) void dispatch_scan_kernel(int32_t* __restrict__ hist, int nblk, int E,
                                                              int32_t* __restrict__ counts,
                                                              int64_t* __restrict__ counts64,
-                                                             int32_t* __restrict__ starts) {
+                                                             int32_t* __restrict__ starts,
+                                                             int32_t* __restrict__ gstart) {
   __shared__ int part[1024];              // [G][E] group sums, then their exclusive prefix per expert
   __shared__ int tot[kMaxEDispatch + 1];  // totals, then exclusive starts
-  __shared__ int wsum[16];
+  __shared__ int wsum[16], gsum[16];
   const int tid = threadIdx.x;
   int G = 1;
   while (G * 2 * E <= 1024) G *= 2;
@@ -669,27 +670,44 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(int32_t* __restrict
   }
   __syncthreads();
   // exclusive scan of the totals over the experts: a wave prefix per 64 experts, then the wave totals
+  // (and, for the row-group tiles, of the experts' group counts ceil(total / 128))
   const int lane = tid & 63, w = tid >> 6;
   const int v = tid < E ? tot[tid] : 0;
-  int incl = v;
+  const int gv = (v + kTileGroupRows - 1) / kTileGroupRows;
+  int incl = v, gincl = gv;
 #pragma unroll
   for (int sft = 1; sft < 64; sft <<= 1) {
     const int o = __shfl_up(incl, sft, 64);
-    if (lane >= sft) incl += o;
+    const int og = __shfl_up(gincl, sft, 64);
+    if (lane >= sft) {
+      incl += o;
+      gincl += og;
+    }
   }
-  if (lane == 63) wsum[w] = incl;
+  if (lane == 63) {
+    wsum[w] = incl;
+    gsum[w] = gincl;
+  }
   __syncthreads();
-  int wbase = 0;
-  for (int ww = 0; ww < w; ++ww) wbase += wsum[ww];
+  int wbase = 0, gbase = 0;
+  for (int ww = 0; ww < w; ++ww) {
+    wbase += wsum[ww];
+    gbase += gsum[ww];
+  }
   __syncthreads();
   if (tid < E) {
     tot[tid] = wbase + incl - v;
     starts[tid] = wbase + incl - v;
+    if (gstart) gstart[tid] = gbase + gincl - gv;
   }
   if (tid == 0) {
-    int all = 0;
-    for (int ww = 0; ww < 16; ++ww) all += wsum[ww];
+    int all = 0, gall = 0;
+    for (int ww = 0; ww < 16; ++ww) {
+      all += wsum[ww];
+      gall += gsum[ww];
+    }
     starts[E] = all;
+    if (gstart) gstart[E] = gall;
   }
   __syncthreads();
   if (mine) {
@@ -713,24 +731,37 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(int32_t* __restrict
   }
 }
 
-// one wave per token: sorted positions of its k rows, index arrays, then the row copy x[t] -> xs[pos_j]
+// one wave per token: sorted positions of its k rows, index arrays, then the row copies x[t] -> xs[pos_j] and into
+// the row-group tiles (64-byte pieces: slice s of row pos_j, its chunks swizzled as in the K-major LDS image)
 __global__ __launch_bounds__(256) void dispatch_scatter_kernel(
     const void* __restrict__ ids, int ids64, const void* __restrict__ tw, int tw_dtype, int64_t T, int k, int E,
     const int32_t* __restrict__ blkoff, const int32_t* __restrict__ rank, const uint16_t* __restrict__ x,
     int64_t ldx, int64_t d, uint16_t* __restrict__ xs, int32_t* __restrict__ order, int32_t* __restrict__ a_idx,
-    int32_t* __restrict__ inv_pos, uint16_t* __restrict__ w_sorted) {
+    int32_t* __restrict__ inv_pos, uint16_t* __restrict__ w_sorted, char* __restrict__ xs_tiles,
+    const int32_t* __restrict__ starts, const int32_t* __restrict__ gstart) {
   const int lane = threadIdx.x & 63;
   const int nwaves = blockDim.x >> 6;
   const int64_t nvec = d / 8;
   for (int64_t t = (int64_t)blockIdx.x * nwaves + (threadIdx.x >> 6); t < T; t += (int64_t)gridDim.x * nwaves) {
     int64_t pos[kMaxK];
+    int64_t tpos[kMaxK];  // tiles: byte offset of the row's slice 0 (its group's slice 0 + 64 * row in group)
+    int tsw[kMaxK];       // tiles: the row's chunk swizzle
 #pragma unroll
     for (int j = 0; j < kMaxK; ++j) {
       pos[j] = -1;
+      tpos[j] = 0;
+      tsw[j] = 0;
       if (j < k) {
         const int64_t f = t * k + j;
         const int e = load_id(ids, ids64, f);
         if (e >= 0 && e < E) pos[j] = (int64_t)blkoff[(f / kFPB) * E + e] + rank[f];
+        if (xs_tiles && pos[j] >= 0) {
+          const int64_t rel = pos[j] - starts[e];
+          const int64_t g = gstart[e] + rel / kTileGroupRows;
+          const int rr = (int)(rel % kTileGroupRows);
+          tpos[j] = g * ((d + kTileK - 1) / kTileK) * (kTileGroupRows * kTileK * 2) + rr * 64;
+          tsw[j] = (rr >> 2) & 3;
+        }
         if (lane == j && pos[j] >= 0) {
           order[pos[j]] = (int32_t)f;
           if (a_idx) a_idx[pos[j]] = (int32_t)t;
@@ -746,13 +777,19 @@ __global__ __launch_bounds__(256) void dispatch_scatter_kernel(
         if (lane == j && inv_pos) inv_pos[f] = (int32_t)pos[j];
       }
     }
-    if (xs) {
+    if (xs || xs_tiles) {
       const uint4* src = reinterpret_cast<const uint4*>(x + t * ldx);
       for (int64_t c = lane; c < nvec; c += 64) {
         const uint4 v = src[c];
 #pragma unroll
         for (int j = 0; j < kMaxK; ++j)
-          if (j < k && pos[j] >= 0) reinterpret_cast<uint4*>(xs + pos[j] * d)[c] = v;
+          if (j < k && pos[j] >= 0) {
+            if (xs) reinterpret_cast<uint4*>(xs + pos[j] * d)[c] = v;
+            if (xs_tiles) {  // chunk c: slice c / 4, logical chunk c % 4 of the row's 64 bytes
+              const int64_t off = tpos[j] + (c >> 2) * (kTileGroupRows * kTileK * 2) + (((c & 3) ^ tsw[j]) * 16);
+              *reinterpret_cast<uint4*>(xs_tiles + off) = v;
+            }
+          }
       }
     }
   }
@@ -1359,16 +1396,17 @@ static size_t dispatch_ws_bytes(int64_t T, int k, int E) {
   const int64_t nblk = (M + kFPB - 1) / kFPB;
   const size_t hist = (size_t)(nblk > 0 ? nblk : 1) * (size_t)E * 4;
   const size_t rank = (size_t)(M > 0 ? M : 1) * 4;
-  return ((hist + 255) / 256) * 256 + ((rank + 255) / 256) * 256;
+  const size_t gst = (size_t)(E + 1) * 4;  // row-group starts of the tiles
+  return ((hist + 255) / 256) * 256 + ((rank + 255) / 256) * 256 + ((gst + 255) / 256) * 256;
 }
 
 // hmoe_dispatch with its workspace given: every argument is checked before the first launch, so an error leaves
 // counts / starts untouched.  The workspace holds the per-block histograms (then their exclusive offsets) and the
 // per-row ranks; each call writes every entry it later reads, so nothing in it has to start at zero.
 static int dispatch_impl(const void* topk_ids, int ids_dtype, const void* topk_w, int w_dtype, int64_t T, int k, int E,
-                         const void* x, int64_t ldx, int64_t d, void* xs, int32_t* counts, int64_t* counts64,
-                         int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos, uint16_t* w_sorted,
-                         void* workspace, size_t workspace_bytes, hipStream_t s) {
+                         const void* x, int64_t ldx, int64_t d, void* xs, void* xs_tiles, int32_t* counts,
+                         int64_t* counts64, int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos,
+                         uint16_t* w_sorted, void* workspace, size_t workspace_bytes, hipStream_t s) {
   if (T < 0 || k <= 0 || E <= 0) return HMOE_ERR_ARG;
   if (E > kMaxEDispatch || k > kMaxK) return HMOE_ERR_SHAPE;
   if (!counts || !starts) return HMOE_ERR_ARG;
@@ -1378,12 +1416,17 @@ static int dispatch_impl(const void* topk_ids, int ids_dtype, const void* topk_w
   const int64_t M = T * k;
   if (M > INT32_MAX) return HMOE_ERR_SHAPE;
   if (M > 0 && (!topk_ids || !order)) return HMOE_ERR_ARG;
-  if (xs && (!x || d <= 0 || d % 8 || ldx % 8 || ldx < d || !al16(x) || !al16(xs))) return HMOE_ERR_ARG;
+  // the row copies read x only when there are rows
+  if (xs && M > 0 && (!x || d <= 0 || d % 8 || ldx % 8 || ldx < d || !al16(x) || !al16(xs))) return HMOE_ERR_ARG;
+  if (xs_tiles && M > 0 && (!x || d <= 0 || d % 8 || ldx % 8 || ldx < d || !al16(x) || !al16(xs_tiles)))
+    return HMOE_ERR_ARG;
   if (workspace_bytes < dispatch_ws_bytes(T, k, E) || !workspace) return HMOE_ERR_WORKSPACE;
   const int64_t nblk = (M + kFPB - 1) / kFPB;
   int32_t* hist = static_cast<int32_t*>(workspace);
   const size_t hist_bytes = (((size_t)(nblk > 0 ? nblk : 1) * (size_t)E * 4 + 255) / 256) * 256;
   int32_t* rank = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + hist_bytes);
+  const size_t rank_bytes = (((size_t)(M > 0 ? M : 1) * 4 + 255) / 256) * 256;
+  int32_t* gstart = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + hist_bytes + rank_bytes);
   int nbits = 0;
   while ((1 << nbits) < E) ++nbits;
   const int ids64 = ids_dtype == HMOE_DT_I64;
@@ -1392,13 +1435,15 @@ static int dispatch_impl(const void* topk_ids, int ids_dtype, const void* topk_w
                        hist, rank);
     HMOE_CHECK_LAUNCH();
   }
-  hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, s, hist, (int)nblk, E, counts, counts64, starts);
+  hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, s, hist, (int)nblk, E, counts, counts64, starts,
+                     gstart);
   HMOE_CHECK_LAUNCH();
   if (M > 0) {
     const int grid = grid_for(T, 4, 8192);
     hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(grid), dim3(256), 0, s, topk_ids, ids64, topk_w, w_dtype, T, k,
                        E, hist, rank, static_cast<const uint16_t*>(x), ldx, d, static_cast<uint16_t*>(xs), order,
-                       a_idx, inv_pos, w_sorted);
+                       a_idx, inv_pos, w_sorted,
+                       static_cast<char*>(xs_tiles), starts, gstart);
     HMOE_CHECK_LAUNCH();
   }
   return HMOE_OK;
@@ -1501,8 +1546,22 @@ int hmoe_dispatch(const void* topk_ids, int ids_dtype, const void* topk_w, int w
                   const void* x, int64_t ldx, int64_t d, void* xs, int32_t* counts, int64_t* counts64,
                   int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos, uint16_t* w_sorted,
                   void* workspace, size_t workspace_bytes, hmoe_stream_t stream) {
-  return dispatch_impl(topk_ids, ids_dtype, topk_w, w_dtype, T, k, E, x, ldx, d, xs, counts, counts64, starts, order,
-                       a_idx, inv_pos, w_sorted, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+  return dispatch_impl(topk_ids, ids_dtype, topk_w, w_dtype, T, k, E, x, ldx, d, xs, nullptr, counts, counts64, starts,
+                       order, a_idx, inv_pos, w_sorted, workspace, workspace_bytes,
+                       reinterpret_cast<hipStream_t>(stream));
+}
+
+size_t hmoe_xs_tiles_bytes(int64_t M, int E, int64_t d) {
+  return (M < 0 || E <= 0 || d <= 0) ? 0 : (size_t)tiles_bytes(M, E, d);
+}
+
+int hmoe_dispatch_tiles(const void* topk_ids, int ids_dtype, const void* topk_w, int w_dtype, int64_t T, int k, int E,
+                        const void* x, int64_t ldx, int64_t d, void* xs, void* xs_tiles, int32_t* counts,
+                        int64_t* counts64, int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos,
+                        uint16_t* w_sorted, void* workspace, size_t workspace_bytes, hmoe_stream_t stream) {
+  return dispatch_impl(topk_ids, ids_dtype, topk_w, w_dtype, T, k, E, x, ldx, d, xs, xs_tiles, counts, counts64,
+                       starts, order, a_idx, inv_pos, w_sorted, workspace, workspace_bytes,
+                       reinterpret_cast<hipStream_t>(stream));
 }
 
 int hmoe_dispatch_noalloc(const void* topk_ids, int ids_dtype, const void* topk_w, int w_dtype, int64_t T, int k,
@@ -1515,8 +1574,8 @@ int hmoe_dispatch_noalloc(const void* topk_ids, int ids_dtype, const void* topk_
   int rc = HMOE_OK;
   void* ws = dispatch_scratch(&rc);
   if (rc) return rc;
-  return dispatch_impl(topk_ids, ids_dtype, topk_w, w_dtype, T, k, E, x, ldx, d, xs, counts, counts64, starts, order,
-                       a_idx, inv_pos, w_sorted, ws, kDispatchScratchBytes, reinterpret_cast<hipStream_t>(stream));
+  return dispatch_impl(topk_ids, ids_dtype, topk_w, w_dtype, T, k, E, x, ldx, d, xs, nullptr, counts, counts64, starts,
+                       order, a_idx, inv_pos, w_sorted, ws, kDispatchScratchBytes, reinterpret_cast<hipStream_t>(stream));
 }
 
 int hmoe_make_schedule(const void* counts, int counts_dtype, int E, int64_t M, int block_m, int32_t* block_e,

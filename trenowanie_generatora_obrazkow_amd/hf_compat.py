@@ -26,9 +26,9 @@ def _fused_moe_infer(self, x, topk_ids, topk_weight):
     if self._act is not torch.nn.functional.silu and not isinstance(self._act, torch.nn.SiLU):
         raise NotImplementedError("the hmoe SwiGLU epilogue implements silu(g) * u only")
     x = x.contiguous()
-    disp = ops.dispatch(topk_ids.contiguous(), E, topk_w=topk_weight.contiguous(), want_inv=False)
+    disp, act, _ = ops.routed_gate_up(x, topk_ids.contiguous(), E, self._wgu, topk_w=topk_weight.contiguous(),
+                                      wgu_s=self._wgu_s, want_inv=False)
     M = n * k
-    act, _ = ops.gate_up_swiglu(x, self._wgu, disp.counts, M, a_idx=disp.a_idx, wgu_s=self._wgu_s)
     y, _ = ops.down_scatter(act, self._wd, disp.counts, M, disp.w_sorted, disp.order, wd_s=self._wd_s)
     return ops.combine(y, n, k)
 

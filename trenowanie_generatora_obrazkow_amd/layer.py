@@ -3,8 +3,8 @@
 backward pass -- neither exists in the reference (its MoE path is inference-only, aurora/hf_compat.py:62).
 
 Forward (all hmoe HIP kernels, one stream, no host sync):
-  route_topk -> dispatch (stable counting sort; with a backward to follow, also the permuted copy of x) ->
-  gate/up GEMM with fused SwiGLU (rows of x gathered by the GEMM when there is no copy) ->
+  route_topk -> dispatch (stable counting sort, the routed rows of x as row-group tiles for the GEMM's copies; with
+  a backward to follow, also the row-major permuted copy) -> gate/up GEMM with fused SwiGLU ->
   down GEMM x routing weight, scattered to (token, slot) order -> combine over the k slots.
 Backward:
   combine_bwd (weighted dY for the down wgrad, routing-weight grads) -> down dgrad (dY rows gathered, routing
@@ -61,13 +61,10 @@ class _MoEFunction(torch.autograd.Function):
         wr, wgu, wd = _bf16(wr), _bf16(wgu), _bf16(wd)
         need_grad = any(ctx.needs_input_grad[:4])
         logits, ids, tw = ops.route_topk(x, wr, k, bias=bias, renorm=renorm)
-        # With a backward to follow, the dispatch writes the permuted copy xs of x (the gate/up weight gradient
-        # reads it again); a forward alone gathers the rows of x inside the gate/up GEMM instead.
-        disp = ops.dispatch(ids, E, topk_w=tw, x=x if need_grad else None, want_inv=need_grad)
-        if need_grad:
-            act, gu = ops.gate_up_swiglu(disp.xs, wgu, disp.counts, M, keep_gu=True)
-        else:
-            act, gu = ops.gate_up_swiglu(x, wgu, disp.counts, M, a_idx=disp.a_idx)
+        # The dispatch writes the routed rows as row-group tiles for the gate/up GEMM; with a backward to follow,
+        # also the row-major permuted copy xs (the gate/up weight gradient reads it).
+        disp, act, gu = ops.routed_gate_up(x, ids, E, wgu, topk_w=tw, keep_gu=need_grad, want_xs=need_grad,
+                                           want_inv=need_grad)
         y, yhat = ops.down_scatter(act, wd, disp.counts, M, disp.w_sorted, disp.order, keep_yhat=need_grad)
         out = ops.combine(y, T, k)
         if need_grad:

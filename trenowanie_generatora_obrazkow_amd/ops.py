@@ -135,11 +135,14 @@ class Dispatch:
     inv_pos: torch.Tensor  # (M,) int32
     w_sorted: torch.Tensor  # (M,) bf16 or None
     xs: torch.Tensor  # (M, d) bf16 or None
+    xs_tiles: torch.Tensor = None  # the sorted rows as row-group tiles (bf16 storage) or None
 
 
-def dispatch(topk_ids: torch.Tensor, E: int, topk_w=None, x=None, want_counts64=False, want_inv=True) -> Dispatch:
-    """Stable counting sort of the flat routed rows (aurora/hf_compat.py:69-72, 78, 80) and optionally the row
-    permutation xs = x[a_idx]."""
+def dispatch(topk_ids: torch.Tensor, E: int, topk_w=None, x=None, want_counts64=False, want_inv=True,
+             want_xs=True, want_tiles=False) -> Dispatch:
+    """Stable counting sort of the flat routed rows (aurora/hf_compat.py:69-72, 78, 80) and optionally, with x, the
+    row permutation xs = x[a_idx] (want_xs) and the same rows as row-group tiles for gate_up_swiglu_tiles
+    (want_tiles)."""
     T, k = topk_ids.shape
     M = T * k
     dev = topk_ids.device
@@ -158,21 +161,24 @@ def dispatch(topk_ids: torch.Tensor, E: int, topk_w=None, x=None, want_counts64=
     a_idx = torch.empty(M, device=dev, dtype=torch.int32)
     inv = torch.empty(M, device=dev, dtype=torch.int32) if want_inv else None
     w_sorted = torch.empty(M, device=dev, dtype=torch.bfloat16) if topk_w is not None else None
-    xs = None
+    xs = tiles = None
     d = 0
     ldx = 0
     if x is not None:
         _need(x, "x", (T, None), _BF16, contig=False)  # xs = x[a_idx] reads rows a_idx < T
         d = x.shape[1]
         ldx = x.stride(0)
-        xs = torch.empty(M, d, device=dev, dtype=torch.bfloat16)
+        if want_xs:
+            xs = torch.empty(M, d, device=dev, dtype=torch.bfloat16)
+        if want_tiles:
+            tiles = torch.empty(L.lib().hmoe_xs_tiles_bytes(M, E, d) // 2, device=dev, dtype=torch.bfloat16)
     ws_bytes = L.lib().hmoe_dispatch_workspace_size(T, k, E)
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
     with _Probe("dispatch"):
-        L.call("hmoe_dispatch", L.ptr(ids), L.dt(ids), L.ptr(topk_w), L.dt(topk_w) if topk_w is not None else 0, T, k, E,
-               L.ptr(x), ldx, d, L.ptr(xs), L.ptr(counts), L.ptr(counts64), L.ptr(starts), L.ptr(order), L.ptr(a_idx),
-               L.ptr(inv), L.ptr(w_sorted), L.ptr(ws), ws_bytes, s)
-    return Dispatch(counts, counts64, starts, order, a_idx, inv, w_sorted, xs)
+        L.call("hmoe_dispatch_tiles", L.ptr(ids), L.dt(ids), L.ptr(topk_w), L.dt(topk_w) if topk_w is not None else 0,
+               T, k, E, L.ptr(x), ldx, d, L.ptr(xs), L.ptr(tiles), L.ptr(counts), L.ptr(counts64), L.ptr(starts),
+               L.ptr(order), L.ptr(a_idx), L.ptr(inv), L.ptr(w_sorted), L.ptr(ws), ws_bytes, s)
+    return Dispatch(counts, counts64, starts, order, a_idx, inv, w_sorted, xs, tiles)
 
 
 def make_schedule(counts: torch.Tensor, M: int, block_m: int = 64):
@@ -269,6 +275,45 @@ def gate_up_swiglu(x, wgu, counts, M, a_idx=None, keep_gu=False, wgu_s=None):
         L.call("hmoe_gate_up_swiglu", L.ptr(x), x.stride(0), L.ptr(a_idx), L.ptr(wgu), E, d, h, L.ptr(counts),
                L.dt(counts), M, L.ptr(act), L.ptr(gu), s)
     return act, gu
+
+
+def gate_up_swiglu_tiles(xs_tiles, wgu, counts, M, keep_gu=False):
+    """gate_up_swiglu on the row-group tiles a dispatch(want_tiles=True) wrote (bf16 weights): identical act / gu."""
+    if wgu.dim() != 3 or wgu.dtype != torch.bfloat16 or wgu.shape[2] % 2:
+        raise TypeError(f"wgu must be an (E, d, 2h) bf16 stack (got {tuple(wgu.shape)} {wgu.dtype})")
+    E, d, h2 = wgu.shape
+    h = h2 // 2
+    s = _dev_stream(xs_tiles)
+    wgu = _contig(wgu, "wgu")
+    counts = _counts(counts, E)
+    _need(xs_tiles, "xs_tiles", (L.lib().hmoe_xs_tiles_bytes(M, E, d) // 2,), _BF16)
+    act = torch.empty(M, h, device=xs_tiles.device, dtype=torch.bfloat16)
+    gu = torch.empty(M, h2, device=xs_tiles.device, dtype=torch.bfloat16) if keep_gu else None
+    with _Probe("gate_up_swiglu"):
+        L.call("hmoe_gate_up_swiglu_tiles", L.ptr(xs_tiles), L.ptr(wgu), E, d, h, L.ptr(counts), L.dt(counts), M,
+               L.ptr(act), L.ptr(gu), s)
+    return act, gu
+
+
+def routed_gate_up(x, ids, E, wgu, topk_w=None, wgu_s=None, keep_gu=False, want_xs=False, want_inv=True):
+    """dispatch + gate/up GEMM of the routed rows: with bf16 weights the dispatch writes the rows as row-group tiles
+    and the GEMM reads them (1 KB copies); int8 weights, or tiles past the GEMM's 32-bit offsets, gather the rows
+    of x inside the GEMM instead.  want_xs: also the row-major permuted copy (the gate/up weight gradient reads it).
+    Returns (Dispatch, act, gu)."""
+    T, k = ids.shape
+    M = T * k
+    d = x.shape[1]
+    tiles = wgu_s is None and wgu.dtype == torch.bfloat16 and L.lib().hmoe_xs_tiles_bytes(M, E, d) < (1 << 31)
+    disp = dispatch(ids, E, topk_w=topk_w, x=x if (tiles or want_xs) else None, want_inv=want_inv, want_xs=want_xs,
+                    want_tiles=tiles)
+    if tiles:
+        act, gu = gate_up_swiglu_tiles(disp.xs_tiles, wgu, disp.counts, M, keep_gu=keep_gu)
+        disp.xs_tiles = None  # read once: not kept alive with the dispatch
+    elif want_xs:
+        act, gu = gate_up_swiglu(disp.xs, wgu, disp.counts, M, keep_gu=keep_gu, wgu_s=wgu_s)
+    else:
+        act, gu = gate_up_swiglu(x, wgu, disp.counts, M, a_idx=disp.a_idx, keep_gu=keep_gu, wgu_s=wgu_s)
+    return disp, act, gu
 
 
 def down_scatter(act, wd, counts, M, w_sorted, y_idx, keep_yhat=False, wd_s=None):

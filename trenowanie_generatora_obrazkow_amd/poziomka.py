@@ -137,9 +137,8 @@ class PoziomkaMoE(nn.Module):
         gw, gb = self._gate_tensors()
         _, ids, w = ops.route_sigmoid_group(x2, gw, k, self.n_group, self.topk_group, expert_bias=gb,
                                             scaling=self.scaling)
-        disp = ops.dispatch(ids, E, topk_w=w, want_inv=False)
+        disp, act, _ = ops.routed_gate_up(x2, ids, E, self._wgu, topk_w=w, wgu_s=self._wgu_s, want_inv=False)
         M = T * k
-        act, _ = ops.gate_up_swiglu(x2, self._wgu, disp.counts, M, a_idx=disp.a_idx, wgu_s=self._wgu_s)
         y, _ = ops.down_scatter(act, self._wd, disp.counts, M, disp.w_sorted, disp.order, wd_s=self._wd_s)
         wgu_sh, wd_sh = self.shared_experts._stack.get(self.shared_experts)
         shared = _dense_swiglu(x2, wgu_sh, wd_sh)
