@@ -10,7 +10,9 @@ A step is one pass of the layer over one batch of seeded synthetic tokens, input
   bailing       forward of the BailingMoeV2 block at its real shape (PoziomkaMoE: 8192 tokens, d=2048, 128 int8
                 experts, sigmoid group-limited top-8 of 8 groups keeping 2, h=320, one shared expert h=320)
 value = algorithmic grouped-GEMM TFLOP/s of the layer step (routed rows only: 6*M*d*h forward, 18*M*d*h forward +
-backward) / measured step time; ms_per_step is the layer time.  One JSON line is printed.
+backward) / measured step time; ms_per_step is the layer time of the eager step (with --graph: of replays of the
+step captured once as a HIP graph, eager_ms_per_step beside it).  The roofline kernel's launch time comes from HIP
+events around its launches in the eager timed pass.  One JSON line is printed.
 """
 from __future__ import annotations
 
@@ -72,7 +74,47 @@ def zipf_bias(E, seed=0, s=1.2, n_empty=2):
     return b
 
 
-def run_gpu(w, steps, warmup, probe_kernel="gate_up_swiglu"):
+def time_steps(step, steps, warmup, graph, probe_kernel, probe_every=1):
+    """The timed region.  graph: the step is captured once as a HIP graph (graphs.StepGraph, after the warm-ups) and
+    the timed region replays it `steps` times; an eager pass of the same number of steps follows, with events
+    around the probe kernel's launches on its stream (its average launch time, for the roofline) and its own wall
+    time (eager_ms).  Without graph the timed region is that eager pass.  Returns (ms per step, eager ms per step,
+    probe kernel ms per launch)."""
+    import torch
+
+    from trenowanie_generatora_obrazkow_amd import ops
+    from trenowanie_generatora_obrazkow_amd.graphs import StepGraph
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ms = None
+    if graph:
+        g = StepGraph(step)
+        for _ in range(max(warmup, 3)):  # the first replays of a new graph carry one-time setup
+            g.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            g.replay()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        del g
+    ops.probe = {probe_kernel: []}
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3 / steps
+    # every probe_every-th launch of the probe kernel (the BailingMoeV2 block launches it for the routed experts,
+    # then the shared expert)
+    dom = [a.elapsed_time(b) for a, b in ops.probe[probe_kernel][0::probe_every]]
+    ops.probe = None
+    return (ms if graph else eager_ms), eager_ms, statistics.mean(dom)
+
+
+def run_gpu(w, steps, warmup, graph=False, probe_kernel="gate_up_swiglu"):
     import torch
 
     from trenowanie_generatora_obrazkow_amd import moe_swiglu, ops
@@ -104,20 +146,7 @@ def run_gpu(w, steps, warmup, probe_kernel="gate_up_swiglu"):
             with torch.no_grad():
                 moe_swiglu(x, wr, wgu, wd, k, logit_bias=bias)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    # timed region: exactly `steps` steps, events around the dominant kernel on its launch stream
-    ops.probe = {probe_kernel: []}
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    dom = [a.elapsed_time(b) for a, b in ops.probe[probe_kernel]]
-    ops.probe = None
-    ms = (t1 - t0) * 1e3 / steps
+    ms, eager_ms, dom = time_steps(step, steps, warmup, graph, probe_kernel)
 
     # per-kernel breakdown: a second pass with events around every op (reported, not the headline)
     names = ["route_topk", "dispatch", "gate_up_swiglu", "down_scatter", "combine", "combine_bwd",
@@ -138,7 +167,7 @@ def run_gpu(w, steps, warmup, probe_kernel="gate_up_swiglu"):
         else:
             kern[n] = statistics.median(ts)
     ops.probe = None
-    return ms, statistics.mean(dom), kern
+    return ms, eager_ms, dom, kern
 
 
 def _poziomka_block(w, g):
@@ -161,7 +190,7 @@ def _poziomka_block(w, g):
     return m.to(torch.bfloat16)
 
 
-def run_gpu_poziomka(w, steps, warmup):
+def run_gpu_poziomka(w, steps, warmup, graph=False):
     """Forward of the BailingMoeV2 block; the dominant kernel is the routed gate/up GEMM (int8 experts), the first
     of the two gate/up launches of a step (the second is the shared expert)."""
     import torch
@@ -177,19 +206,7 @@ def run_gpu_poziomka(w, steps, warmup):
     def step():
         m(x)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    ops.probe = {"gate_up_swiglu": []}
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    dom = [a.elapsed_time(b) for a, b in ops.probe["gate_up_swiglu"][0::2]]
-    ops.probe = None
-    ms = (t1 - t0) * 1e3 / steps
+    ms, eager_ms, dom = time_steps(step, steps, warmup, graph, "gate_up_swiglu", probe_every=2)
     names = ["route_topk", "dispatch", "gate_up_swiglu", "down_scatter", "combine"]
     ops.probe = {n: [] for n in names}
     nb = max(3, min(steps, 10))
@@ -205,7 +222,7 @@ def run_gpu_poziomka(w, steps, warmup):
         else:
             kern[n] = statistics.median(ts)
     ops.probe = None
-    return ms, statistics.mean(dom), kern
+    return ms, eager_ms, dom, kern
 
 
 def cpu_threads():
@@ -340,6 +357,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="c5", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--graph", action="store_true",
+                    help="time replays of the step captured once as a HIP graph instead of the eager step (kernels "
+                         "launched from Python op by op); measured alternately in one process the two are within "
+                         "noise at every workload here")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain device copy of 256 MiB three times (the known-size reference for the "
                          "FETCH_SIZE / WRITE_SIZE counters)")
@@ -359,7 +380,8 @@ def main():
         sys.exit(2)
     w = WORKLOADS[args.workload]
     pz = bool(w.get("poziomka"))
-    ms, dom_ms, kern = (run_gpu_poziomka if pz else run_gpu)(w, args.steps, args.warmup)
+    ms, eager_ms, dom_ms, kern = (run_gpu_poziomka if pz else run_gpu)(w, args.steps, args.warmup,
+                                                                     graph=args.graph)
     flops = gemm_flops(w)
     tflops = flops / (ms * 1e-3) / 1e12
     M = w["T"] * w["k"]
@@ -386,6 +408,8 @@ def main():
         "config": {"workload": w["desc"], "tokens": w["T"], "d_model": w["d"], "experts": w["E"], "top_k": w["k"],
                    "hidden": w["h"], "pass": "forward+backward" if w["backward"] else "forward"},
         "layer_us": round(ms * 1e3, 1),
+        "execution": "hip_graph" if args.graph else "eager",
+        "eager_ms_per_step": round(eager_ms, 4),
         "pct_bf16_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2),
         "gemm_flops_per_step": flops,
         "roofline": {"bound": "mfma", "kernel": "hmoe gate/up grouped GEMM + fused SwiGLU (grouped_gemm_kernel, "
