@@ -12,7 +12,9 @@ A step is one pass of the layer over one batch of seeded synthetic tokens, input
 value = algorithmic grouped-GEMM TFLOP/s of the layer step (routed rows only: 6*M*d*h forward, 18*M*d*h forward +
 backward) / measured step time; ms_per_step is the layer time of the eager step (with --graph: of replays of the
 step captured once as a HIP graph, eager_ms_per_step beside it).  The roofline kernel's launch time comes from HIP
-events around its launches in the eager timed pass.  One JSON line is printed.
+events around its launches in the eager timed pass.  With the default c5 workload the same run also times c2, c3,
+c4 and bailing (--extras) and reports each under other_workloads (layer µs, grouped-GEMM TFLOP/s, per-op µs).  One
+JSON line is printed.
 """
 from __future__ import annotations
 
@@ -361,6 +363,11 @@ def main():
                     help="time replays of the step captured once as a HIP graph instead of the eager step (kernels "
                          "launched from Python op by op); measured alternately in one process the two are within "
                          "noise at every workload here")
+    ap.add_argument("--extras", default="c2,c3,c4,bailing",
+                    help="with the default c5 workload, also time these workloads (comma-separated, 'none' for "
+                         "none) with --extra-steps timed steps each and report them under other_workloads; value "
+                         "and metric stay those of the main workload")
+    ap.add_argument("--extra-steps", type=int, default=10)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain device copy of 256 MiB three times (the known-size reference for the "
                          "FETCH_SIZE / WRITE_SIZE counters)")
@@ -424,9 +431,30 @@ def main():
     if pz:
         res["config"].update(shared_hidden=w["shared_h"], n_group=w["n_group"], topk_group=w["topk_group"],
                              weights="int8 experts, bf16 router and shared expert")
+    if args.workload == "c5" and args.extras != "none":
+        res["other_workloads"] = {n: run_extra(n, args.extra_steps) for n in args.extras.split(",") if n}
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = (cpu_baseline_poziomka if pz else cpu_baseline)(w)
     print(json.dumps(res), flush=True)
+
+
+def run_extra(name, steps):
+    """One more workload timed in the same process (eager, steps timed steps after 3 warm-ups): layer time, grouped-
+    GEMM rate and the per-op breakdown."""
+    if name not in WORKLOADS:
+        raise SystemExit(f"bench.py: unknown extra workload {name!r}")
+    w = WORKLOADS[name]
+    pz = bool(w.get("poziomka"))
+    ms, _, dom_ms, kern = (run_gpu_poziomka if pz else run_gpu)(w, steps, 3)
+    flops = gemm_flops(w)
+    tflops = flops / (ms * 1e-3) / 1e12
+    M = w["T"] * w["k"]
+    dom_tflops = 4 * M * w["d"] * w["h"] / (dom_ms * 1e-3) / 1e12
+    return {"config": w["desc"], "pass": "forward+backward" if w["backward"] else "forward", "steps": steps,
+            "layer_us": round(ms * 1e3, 1), "gemm_tflops": round(tflops, 2),
+            "pct_bf16_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2),
+            "gate_up_frac": round(dom_tflops / PEAK_BF16_TFLOPS, 4),
+            "kernels_us": {k_: round(v, 1) for k_, v in kern.items()}}
 
 
 if __name__ == "__main__":
