@@ -144,6 +144,21 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
     int mt, nb;
     {
       const int per_group = C::GM * nb_n;  // bands of GM m-tiles x all n-tiles
+      // Band residency.  With the XCD-aware slots, XCD x runs tiles [r G + x G/8, r G + (x+1) G/8) in round r: one
+      // block of G/8 tiles of a band.  In plain band order an XCD moves on to other bands every round and its L2
+      // fetches new A rows each time.  Within every complete super-group of 8 bands the blocks are permuted so that
+      // XCD x keeps band 8 s + x for per_group / (G/8) rounds in a row and walks its n-blocks, which keeps the band's
+      // A rows in its L2.  Only the order in which workgroups take tiles changes, not what a tile computes.  (Not for
+      // the weight gradients: their bands' A columns, 4 MB at the C5 shape, do not stay in a 4 MB L2, and the order
+      // measured slower there.)
+      if (MODE == MGROUP && (G & 7) == 0) {
+        const int XB = G >> 3;
+        if (per_group % XB == 0) {
+          const int BPB = per_group / XB, SG = 8 * BPB;  // blocks per band, per super-group
+          const int j = tile / XB, sg = j / SG, jj = j - sg * SG;
+          if ((sg + 1) * SG * XB <= full_units) tile = (sg * SG + (jj & 7) * BPB + (jj >> 3)) * XB + tile % XB;
+        }
+      }
       const int g = tile / per_group;
       const int first = g * C::GM;
       const int gsz = min(total_m - first, C::GM);
