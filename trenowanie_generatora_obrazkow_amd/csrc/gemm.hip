@@ -869,44 +869,67 @@ static inline int env_force() {
   return v[0] == 'L' ? 1 : v[0] == 'S' ? 2 : 0;
 }
 
-// large tiles once they alone give every CU at least two tiles
-static inline bool pick_large(int64_t tiles_large) {
-  const int f = env_force();
-  if (f) return f == 1;
-  const int cus = num_cus();
-  return tiles_large >= 2 * (int64_t)(cus > 0 ? cus : 256);
+static inline int64_t cu_count() {
+  const int c = num_cus();
+  return c > 0 ? c : 256;
 }
 
-// Row-grouped launches take the small tiles also when the large ones would pad the output columns noticeably more
-// (a SwiGLU n-tile with at most 64 live columns of 128 counts as 64: its main loop skips the dead half) or when K is
-// short (fewer than 16 slices: a tile's fixed cost, prologue and epilogue, then outweighs its main loop).  Measured
-// on MI355X: the C3/C5 shapes run 30% slower on small tiles; the BailingMoeV2 down GEMM (K = 320) 4% faster.
+// Large (256x256) or small (128x128) tiles.  The rules follow a sweep of every grouped GEMM (forward, both dgrads,
+// both weight gradients; bf16 and int8 weights) over 512-16384 tokens, d 256-2048, 8-128 experts, top-2 and top-8,
+// h 320-4096, with large tiles, small tiles and the rule alternated in one process on MI355X.  A large tile costs
+// about 1.5x less per flop than two co-resident small ones, so large tiles win unless they leave too few tiles to
+// spread over the CUs or pad much more of the output.
+//
+// Row-grouped launches (bf16 weights): large tiles from 5/8 of a tile per CU on (160 tiles on 256 CUs): at 64-128
+// tiles small ones ran 15-55% faster, from 160 tiles on large ones ran 10-57% faster, also at K = 320 (the h = 320
+// down GEMM, 20-47%).  int8 weights: large tiles only with K of at least 16 slices (the h = 320 down GEMM ran 5-25%
+// faster on small int8 tiles) and, for the gate/up GEMM, from 2.5 tiles per CU (at 384-576 tiles the small int8
+// tiles ran up to 34% faster).  Either way, once the large tiles give two per CU, small ones where the large would
+// pad the output columns by more than 10% (a SwiGLU n-tile with at most 64 live columns of 128 counts as 64: its
+// main loop skips the dead half); with fewer tiles the rounds they save matter more (the h = 320 down dgrad ran 53%
+// faster on large tiles at 2048 tokens, 3% slower at 8192).
 template <int EPI>
-static bool pick_large_mgroup(int64_t tiles_large, int64_t ncols, int64_t K) {
+static bool pick_large_mgroup(int64_t tiles_large, int64_t ncols, int64_t K, bool int8) {
   const int f = env_force();
   if (f) return f == 1;
-  if (!pick_large(tiles_large)) return false;
-  const int64_t bl = EPI == EPI_SWIGLU ? CfgL::BN / 2 : CfgL::BN, bs = EPI == EPI_SWIGLU ? CfgS::BN / 2 : CfgS::BN;
-  int64_t padl = (ncols + bl - 1) / bl * bl;
-  const int64_t pads = (ncols + bs - 1) / bs * bs;
-  if (EPI == EPI_SWIGLU && ncols % bl && ncols % bl <= bl / 2) padl -= bl / 2;  // a half-live last n-tile runs at half width
-  if (padl * 10 > pads * 11) return false;  // > 10% more padded columns on large tiles
-  return K >= 16 * kBK;
+  const int64_t cus = cu_count();
+  if (tiles_large >= 2 * cus) {
+    const int64_t bl = EPI == EPI_SWIGLU ? CfgL::BN / 2 : CfgL::BN, bs = EPI == EPI_SWIGLU ? CfgS::BN / 2 : CfgS::BN;
+    int64_t padl = (ncols + bl - 1) / bl * bl;
+    const int64_t pads = (ncols + bs - 1) / bs * bs;
+    if (EPI == EPI_SWIGLU && ncols % bl && ncols % bl <= bl / 2) padl -= bl / 2;
+    if (padl * 10 > pads * 11) return false;
+  }
+  if (!int8) return tiles_large * 8 >= cus * 5;
+  if (K < 16 * kBK) return false;
+  return EPI == EPI_SWIGLU ? tiles_large * 2 >= cus * 5 : tiles_large * 8 >= cus * 5;
 }
 
 template <int MODE, bool A_MN, bool B_MN, int EPI, bool A_BLK = false>
 static int launch_mgroup(const GemmParams& p, int64_t ncols, hipStream_t s) {
   const int64_t tl = mgroup_tiles<CfgL, EPI>(p.M, p.E, ncols);
-  if (pick_large_mgroup<EPI>(tl, ncols, p.K)) return launch<CfgL, MODE, A_MN, B_MN, EPI, A_BLK>(p, tl, s);
+  if (pick_large_mgroup<EPI>(tl, ncols, p.K, false)) return launch<CfgL, MODE, A_MN, B_MN, EPI, A_BLK>(p, tl, s);
   return launch<CfgS, MODE, A_MN, B_MN, EPI, A_BLK>(p, mgroup_tiles<CfgS, EPI>(p.M, p.E, ncols), s);
 }
 
-// int8 weights: same tile choice, int8 tile configurations
+// int8 weights: the int8 tile configurations
 template <int EPI>
 static int launch_mgroup_i8(const GemmParams& p, int64_t ncols, hipStream_t s) {
   const int64_t tl = mgroup_tiles<CfgL8, EPI>(p.M, p.E, ncols);
-  if (pick_large_mgroup<EPI>(tl, ncols, p.K)) return launch<CfgL8, MGROUP, false, true, EPI>(p, tl, s);
+  if (pick_large_mgroup<EPI>(tl, ncols, p.K, true)) return launch<CfgL8, MGROUP, false, true, EPI>(p, tl, s);
   return launch<CfgS8, MGROUP, false, true, EPI>(p, mgroup_tiles<CfgS8, EPI>(p.M, p.E, ncols), s);
+}
+
+// Weight gradients: large tiles once they give every CU two tiles, unless they pad the (P, N) output area by more
+// than 10% over the small ones (at h = 320 the 256-row tiles pad 320 rows to 512: small ones ran 9-41% faster for
+// the down weight gradient and up to 8% for the gate/up one, N = 640).
+static bool pick_large_kgroup(int64_t E, int64_t P, int64_t N) {
+  const int f = env_force();
+  if (f) return f == 1;
+  if (kgroup_tiles<CfgL>(E, P, N) < 2 * cu_count()) return false;
+  const int64_t al = (P + CfgL::BM - 1) / CfgL::BM * CfgL::BM * ((N + CfgL::BN - 1) / CfgL::BN * CfgL::BN);
+  const int64_t as = (P + CfgS::BM - 1) / CfgS::BM * CfgS::BM * ((N + CfgS::BN - 1) / CfgS::BN * CfgS::BN);
+  return al * 10 <= as * 11;
 }
 
 static inline bool al16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -1204,8 +1227,7 @@ int hmoe_grouped_wgrad(const void* a, int64_t lda, const void* b, int64_t ldb, i
   p.strideCe = P * N;
   p.c_f32 = dw_dtype == HMOE_DT_F32;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int64_t tl = kgroup_tiles<CfgL>(E, P, N);
-  if (pick_large(tl)) return launch<CfgL, KGROUP, true, true, EPI_WGRAD>(p, tl, s);
+  if (pick_large_kgroup(E, P, N)) return launch<CfgL, KGROUP, true, true, EPI_WGRAD>(p, kgroup_tiles<CfgL>(E, P, N), s);
   return launch<CfgS, KGROUP, true, true, EPI_WGRAD>(p, kgroup_tiles<CfgS>(E, P, N), s);
 }
 
