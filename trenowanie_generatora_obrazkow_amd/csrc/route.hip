@@ -566,7 +566,8 @@ __global__ __launch_bounds__(kSgThreads) void route_sigmoid_kernel(const uint16_
 // Dispatch: stable counting sort of flat ids.  Pass 1 (one wave per block of kFPB flat rows): per-block expert
 // histogram and the stable rank of each flat row among earlier rows of the same expert inside its block (wave
 // ballots: a lane's peers are the lanes whose id agrees on every bit).  Pass 2 (one workgroup): per-expert totals,
-// expert starts, and per-(block, expert) first sorted row.  Pass 3: positions, index arrays and the row copy.
+// expert starts, and per-(block, expert) first sorted row.  Pass 3: positions, index arrays and the row copies
+// (per token), or the index arrays alone (per flat row) when no rows are copied.
 // ---------------------------------------------------------------------------------------------------------------
 constexpr int kFPB = 256;        // flat rows per histogram block (one wave each: 128 waves at M = 32768)
 constexpr int kMaxEDispatch = 1024;
@@ -728,6 +729,30 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(int32_t* __restrict
       hist[(int64_t)b * E + e] = run;
       run += c;
     }
+  }
+}
+
+// Pass 3 without row copies: the index arrays only, one thread per flat row f (token f / k), so that every row's
+// lookups are in flight together (the per-token pass below visits a token's k rows one after another: at top-8 its
+// lookups are eight dependent round trips per wave).  Same values as the per-token pass.
+__global__ __launch_bounds__(256) void dispatch_index_kernel(const void* __restrict__ ids, int ids64,
+                                                             const void* __restrict__ tw, int tw_dtype, int64_t M,
+                                                             int k, int E, const int32_t* __restrict__ blkoff,
+                                                             const int32_t* __restrict__ rank,
+                                                             int32_t* __restrict__ order, int32_t* __restrict__ a_idx,
+                                                             int32_t* __restrict__ inv_pos,
+                                                             uint16_t* __restrict__ w_sorted) {
+  for (int64_t f = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; f < M; f += (int64_t)gridDim.x * blockDim.x) {
+    const int e = load_id(ids, ids64, f);
+    const int64_t pos = (e >= 0 && e < E) ? (int64_t)blkoff[(f / kFPB) * E + e] + rank[f] : -1;
+    if (pos >= 0) {
+      order[pos] = (int32_t)f;
+      if (a_idx) a_idx[pos] = (int32_t)(f / k);
+      if (w_sorted)
+        w_sorted[pos] = tw_dtype == HMOE_DT_F32 ? (uint16_t)f2bf(reinterpret_cast<const float*>(tw)[f])
+                                                : reinterpret_cast<const uint16_t*>(tw)[f];
+    }
+    if (inv_pos) inv_pos[f] = (int32_t)pos;
   }
 }
 
@@ -1438,12 +1463,16 @@ static int dispatch_impl(const void* topk_ids, int ids_dtype, const void* topk_w
   hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, s, hist, (int)nblk, E, counts, counts64, starts,
                      gstart);
   HMOE_CHECK_LAUNCH();
-  if (M > 0) {
+  if (M > 0 && (xs || xs_tiles)) {
     const int grid = grid_for(T, 4, 8192);
     hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(grid), dim3(256), 0, s, topk_ids, ids64, topk_w, w_dtype, T, k,
                        E, hist, rank, static_cast<const uint16_t*>(x), ldx, d, static_cast<uint16_t*>(xs), order,
                        a_idx, inv_pos, w_sorted,
                        static_cast<char*>(xs_tiles), starts, gstart);
+    HMOE_CHECK_LAUNCH();
+  } else if (M > 0) {
+    hipLaunchKernelGGL(dispatch_index_kernel, dim3(grid_for(M, 256, 8192)), dim3(256), 0, s, topk_ids, ids64, topk_w,
+                       w_dtype, M, k, E, hist, rank, order, a_idx, inv_pos, w_sorted);
     HMOE_CHECK_LAUNCH();
   }
   return HMOE_OK;
