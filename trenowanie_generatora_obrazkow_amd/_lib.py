@@ -100,7 +100,17 @@ def ptr(t):
     return None if t is None else t.data_ptr()
 
 
+# torch's raw current-stream lookup (what its generated kernels launch on), without building a Stream object: the
+# per-op stream query is otherwise a visible part of the host time of a small layer call
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream(device=None):
+    """Handle of the current stream of `device` (a torch.device, an index or None for the current device)."""
+    if _raw_stream is not None:
+        if isinstance(device, torch.device):
+            device = device.index
+        return _raw_stream(torch.cuda.current_device() if device is None else device)
     return torch.cuda.current_stream(device).cuda_stream
 
 
