@@ -1,6 +1,6 @@
 """Dispatch parity on the GPU: counts, stable order, a_idx, inverse permutation and sorted routing weights bit-exact
 with the reference operations themselves (torch.argsort(stable=True) / bincount on CPU, aurora/hf_compat.py:69-72,
-78, 80) and with the oracle; the permuted rows equal x[a_idx]; make_schedule equals the oracle."""
+78, 80) and with the oracle, with and without the row copies; the permuted rows equal x[a_idx]; make_schedule equals the oracle."""
 import numpy as np
 import pytest
 import torch
@@ -33,8 +33,10 @@ def test_dispatch_bitexact(oracle, T, E, k, skew):
     d = 264
     x = torch.randn(T, d, generator=g).bfloat16()
     dev = torch.device("cuda")
-    for ids_dt in (torch.int64, torch.int32):
-        disp = ops.dispatch(ids.to(ids_dt).to(dev), E, topk_w=w.to(dev), x=x.to(dev), want_counts64=True)
+    # with x: the per-token pass that also copies the rows; without: the per-row pass that writes the index arrays
+    for ids_dt, with_x in ((torch.int64, True), (torch.int32, True), (torch.int32, False)):
+        disp = ops.dispatch(ids.to(ids_dt).to(dev), E, topk_w=w.to(dev), x=x.to(dev) if with_x else None,
+                            want_counts64=True)
         order, counts = _ref_dispatch(ids, E, k)
         np.testing.assert_array_equal(disp.counts.cpu().numpy(), counts.numpy())
         np.testing.assert_array_equal(disp.counts64.cpu().numpy(), counts.numpy())
@@ -46,7 +48,10 @@ def test_dispatch_bitexact(oracle, T, E, k, skew):
         inv[order.numpy()] = np.arange(T * k)
         np.testing.assert_array_equal(disp.inv_pos.cpu().numpy(), inv)
         np.testing.assert_array_equal(bits(disp.w_sorted), bits(w.reshape(-1)[order].bfloat16()))
-        np.testing.assert_array_equal(bits(disp.xs), bits(x[order // k]))
+        if with_x:
+            np.testing.assert_array_equal(bits(disp.xs), bits(x[order // k]))
+        else:
+            assert disp.xs is None
         ref_o = oracle.dispatch_c(ids.numpy(), E)
         np.testing.assert_array_equal(disp.order.cpu().numpy(), ref_o["order"])
 
