@@ -367,7 +367,7 @@ def main():
                     help="with the default c5 workload, also time these workloads (comma-separated, 'none' for "
                          "none) with --extra-steps timed steps each and report them under other_workloads; value "
                          "and metric stay those of the main workload")
-    ap.add_argument("--extra-steps", type=int, default=10)
+    ap.add_argument("--extra-steps", type=int, default=20)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain device copy of 256 MiB three times (the known-size reference for the "
                          "FETCH_SIZE / WRITE_SIZE counters)")
@@ -439,13 +439,13 @@ def main():
 
 
 def run_extra(name, steps):
-    """One more workload timed in the same process (eager, steps timed steps after 3 warm-ups): layer time, grouped-
-    GEMM rate and the per-op breakdown."""
+    """One more workload timed in the same process (eager, steps timed steps after 5 warm-ups, as the main
+    workload): layer time, grouped-GEMM rate and the per-op breakdown."""
     if name not in WORKLOADS:
         raise SystemExit(f"bench.py: unknown extra workload {name!r}")
     w = WORKLOADS[name]
     pz = bool(w.get("poziomka"))
-    ms, _, dom_ms, kern = (run_gpu_poziomka if pz else run_gpu)(w, steps, 3)
+    ms, _, dom_ms, kern = (run_gpu_poziomka if pz else run_gpu)(w, steps, 5)
     flops = gemm_flops(w)
     tflops = flops / (ms * 1e-3) / 1e12
     M = w["T"] * w["k"]
