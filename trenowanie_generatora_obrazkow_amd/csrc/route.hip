@@ -1197,6 +1197,63 @@ __global__ __launch_bounds__(256) void router_dwr_partial_kernel(const float* __
 // out[i] = sum over chunks c of part[c][i]: block 1024 = 64 outputs x kRedGroups chunk groups; each group adds its
 // chunks in order (eight loads in flight), then the group sums are added in group order, so the result does not
 // depend on the launch.
+// dwr partials on the fp32 MFMA for E <= 16 (the chunks and partial layout of router_dwr_partial_kernel).  Wave
+// w of the workgroup owns 128 columns (lane l: 8 columns 8 (l % 16) + 0..7 of them, 16 bytes of each token row) and
+// all kDwrChunk tokens of the chunk, in steps of 4 tokens: v_mfma_f32_16x16x4_f32 with A = dlogits^T (16 experts x
+// 4 tokens: lane l holds expert l % 16 of token l / 16) and, for column block b, B = x (4 tokens x 16 columns: lane l
+// holds column 8 (l % 16) + b of token l / 16), so block b's output column n is column 8 n + b.  Experts past E get
+// zero dlogits, tokens past T zero rows.  The fp32 MFMA accumulates in fp32 in a fixed order (deterministic); the
+// result differs from the VALU kernel's only by fp32 rounding.
+constexpr int kDwrQ = 16;  // 4-token steps whose loads are in flight together
+
+__global__ __launch_bounds__(256) void router_dwr_mfma_kernel(const float* __restrict__ dlogits,
+                                                              const uint16_t* __restrict__ x, int64_t ldx, int64_t T,
+                                                              int E, int64_t d, float* __restrict__ part) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int q = lane >> 4;   // token within a 4-token step (the MFMA k index)
+  const int r = lane & 15;   // A: expert row; B: column group
+  const int64_t chunk = blockIdx.x;
+  const int64_t col = (int64_t)blockIdx.y * 512 + wave * 128 + 8 * r;  // the lane's first column
+  const bool active = col < d;
+  const bool expert = r < E;
+  const int64_t t0 = chunk * kDwrChunk;
+  f32x4 acc[8];
+#pragma unroll
+  for (int b = 0; b < 8; ++b) acc[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s0 = 0; s0 < kDwrChunk; s0 += 4 * kDwrQ) {
+    uint4 xv[kDwrQ];
+    float dv[kDwrQ];
+#pragma unroll
+    for (int u = 0; u < kDwrQ; ++u) {
+      const int64_t t = t0 + s0 + 4 * u + q;
+      xv[u] = make_uint4(0, 0, 0, 0);
+      dv[u] = 0.0f;
+      if (t < T) {
+        if (active) xv[u] = *reinterpret_cast<const uint4*>(x + t * ldx + col);
+        if (expert) dv[u] = dlogits[t * E + r];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kDwrQ; ++u) {
+      const float xf[8] = {bf_lo(xv[u].x), bf_hi(xv[u].x), bf_lo(xv[u].y), bf_hi(xv[u].y),
+                           bf_lo(xv[u].z), bf_hi(xv[u].z), bf_lo(xv[u].w), bf_hi(xv[u].w)};
+#pragma unroll
+      for (int b = 0; b < 8; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(dv[u], xf[b], acc[b], 0, 0, 0);
+    }
+  }
+  // lane l holds, for block b, experts 4 (l / 16) + 0..3 at output column n = l % 16, i.e. column col + b
+  if (!active) return;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = 4 * q + j;
+    if (e >= E) continue;
+    float* dst = part + (chunk * E + e) * d + col;
+    *reinterpret_cast<float4*>(dst) = make_float4(acc[0][j], acc[1][j], acc[2][j], acc[3][j]);
+    *reinterpret_cast<float4*>(dst + 4) = make_float4(acc[4][j], acc[5][j], acc[6][j], acc[7][j]);
+  }
+}
+
 constexpr int kRedGroups = 16;
 
 __global__ __launch_bounds__(1024) void router_dwr_reduce_kernel(const float* __restrict__ part, int nchunk, int E,
@@ -1671,7 +1728,7 @@ int hmoe_router_bwd(const float* logits, const int32_t* topk_ids, const float* d
   // T = 0 still writes dwr (zeros); nothing per token is read or written then, so those pointers may be NULL
   if (T > 0 && (!logits || !topk_ids || !dtopk_w || !dlogits)) return HMOE_ERR_ARG;
   if (dwr && dwr_dtype != HMOE_DT_F32 && dwr_dtype != HMOE_DT_BF16) return HMOE_ERR_DTYPE;
-  if (dwr && ((T > 0 && !x) || d % 8 || ldx % 8 || !al16(x))) return HMOE_ERR_ARG;
+  if (dwr && ((T > 0 && !x) || d % 8 || ldx % 8 || ldx < d || !al16(x))) return HMOE_ERR_ARG;
   if (dwr && (!workspace || workspace_bytes < hmoe_router_bwd_workspace_size(T, E, d))) return HMOE_ERR_WORKSPACE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (T > 0) {
@@ -1687,8 +1744,12 @@ int hmoe_router_bwd(const float* logits, const int32_t* topk_ids, const float* d
     const int nchunk = (int)((T + kDwrChunk - 1) / kDwrChunk);
     float* part = static_cast<float*>(workspace);
     if (nchunk > 0) {
-      hipLaunchKernelGGL(router_dwr_partial_kernel, dim3(nchunk, (unsigned)((d + 511) / 512)), dim3(256), 0, s,
-                         dlogits, static_cast<const uint16_t*>(x), ldx, T, E, d, part);
+      if (E <= 16)
+        hipLaunchKernelGGL(router_dwr_mfma_kernel, dim3(nchunk, (unsigned)((d + 511) / 512)), dim3(256), 0, s,
+                           dlogits, static_cast<const uint16_t*>(x), ldx, T, E, d, part);
+      else
+        hipLaunchKernelGGL(router_dwr_partial_kernel, dim3(nchunk, (unsigned)((d + 511) / 512)), dim3(256), 0, s,
+                           dlogits, static_cast<const uint16_t*>(x), ldx, T, E, d, part);
       HMOE_CHECK_LAUNCH();
     }
     hipLaunchKernelGGL(router_dwr_reduce_kernel, dim3(grid_for((int64_t)E * d, 64, 4096)), dim3(1024), 0, s, part,
