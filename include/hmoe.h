@@ -225,7 +225,8 @@ int hmoe_grouped_wgrad(const void* a, int64_t lda, const void* b, int64_t ldb, i
 size_t hmoe_router_bwd_workspace_size(int64_t T, int E, int64_t d);
 
 /* Router backward (softmax -> top-k gather -> renormalise, as in hmoe_route_topk): dlogits (T, E) fp32 from
- * dtopk_w (T, k) fp32, and dwr (E, d) = dlogits^T @ x (fp32 or bf16 per dwr_dtype; fixed-order reduction).
+ * dtopk_w (T, k) fp32, and dwr (E, d) = dlogits^T @ x (fp32 or bf16 per dwr_dtype; fixed-order reduction, on the
+ * fp32 MFMA when E <= 16).  x is bf16 with row stride ldx >= d (ldx and d multiples of 8, x 16-byte aligned).
  * T = 0 writes zeros to dwr; the per-token pointers may then be NULL. */
 int hmoe_router_bwd(const float* logits, const int32_t* topk_ids, const float* dtopk_w, int64_t T, int E, int k,
                     int renorm, float scaling, const void* x, int64_t ldx, int64_t d, float* dlogits, void* dwr,
