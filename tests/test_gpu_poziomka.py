@@ -121,6 +121,23 @@ def test_poziomka_varying_tokens(oracle):
     assert_close_bf16(y[sample], ref, "T=8192 sample")
 
 
+def test_poziomka_shared_overlap_bit_exact(oracle):
+    """The shared expert on its side stream (overlap_shared, the default) gives the serial block's output bit for bit,
+    for empty, single-token and larger calls, with other work queued on the current stream before each call."""
+    m = _make_block(oracle, 512, 320, 32, 4, 4, 2, 320, seed=21).cuda()
+    g = torch.Generator().manual_seed(22)
+    for T in (0, 1, 300, 4096):
+        print(f"PoziomkaMoE overlap T={T}", flush=True)
+        x = torch.randn(T, 512, generator=g).bfloat16().cuda()
+        m.overlap_shared = False
+        ref = m(x).clone()
+        m.overlap_shared = True
+        torch.ones(1 << 20, device="cuda").mul_(2.0)  # unrelated work on the current stream ahead of the call
+        got = m(x)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), f"T={T}"
+
+
 def test_poziomka_graph_replay(oracle):
     """The forward at a fixed token count captured in a HIP graph (no host synchronisation, no allocation outside the
     graph's pool) and replayed on new inputs: every replay equals the eager forward bit for bit."""

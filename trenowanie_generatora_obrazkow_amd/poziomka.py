@@ -61,6 +61,18 @@ class _StackedMLP:
         return self.wgu, self.wd
 
 
+_SIDE_STREAMS = {}  # device index -> the side stream of PoziomkaMoE's shared expert (kept off the modules, which
+                    # may be copied or pickled)
+
+
+def _side_stream(device: torch.device):
+    """One side stream per device, created with the default priority."""
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    if key not in _SIDE_STREAMS:
+        _SIDE_STREAMS[key] = torch.cuda.Stream(device=key)
+    return _SIDE_STREAMS[key]
+
+
 def _dense_swiglu(x2: torch.Tensor, wgu: torch.Tensor, wd: torch.Tensor) -> torch.Tensor:
     """bf16(bf16(silu(bf16(x Wg))) * bf16(x Wu)) Wd rounded to bf16 -- F.linear / F.silu in bf16 (aurora/
     hf_pipeline.py:322) -- for x2 (T, d) bf16."""
@@ -116,6 +128,9 @@ class PoziomkaMoE(nn.Module):
         self.register_buffer("_wd_s", torch.zeros(experts, d, dtype=torch.bfloat16))
         self._gate_key = None
         self._gate_w = None
+        # The shared expert runs on a side stream of the same (default) priority, so its GEMMs can take the CUs the
+        # routed GEMMs leave idle in their last rounds; False runs it after the routed path on the current stream.
+        self.overlap_shared = True
 
     def _gate_tensors(self):
         """bf16 router weight and fp32 expert bias as the kernel takes them, converted once per weight version."""
@@ -135,14 +150,26 @@ class PoziomkaMoE(nn.Module):
             raise TypeError(f"hmoe PoziomkaMoE runs bf16 activations (got {x2.dtype})")
         T, k, E = x2.shape[0], self.top_k, self._wgu.shape[0]
         gw, gb = self._gate_tensors()
+        wgu_sh, wd_sh = self.shared_experts._stack.get(self.shared_experts)
+        side = _side_stream(x2.device) if self.overlap_shared and T > 0 else None
+        if side is not None:  # fork: the shared expert needs only x
+            main = torch.cuda.current_stream(x2.device)
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                shared = _dense_swiglu(x2, wgu_sh, wd_sh)
+            x2.record_stream(side)
         _, ids, w = ops.route_sigmoid_group(x2, gw, k, self.n_group, self.topk_group, expert_bias=gb,
                                             scaling=self.scaling)
         disp, act, _ = ops.routed_gate_up(x2, ids, E, self._wgu, topk_w=w, wgu_s=self._wgu_s, want_inv=False)
         M = T * k
         y, _ = ops.down_scatter(act, self._wd, disp.counts, M, disp.w_sorted, disp.order, wd_s=self._wd_s)
-        wgu_sh, wd_sh = self.shared_experts._stack.get(self.shared_experts)
-        shared = _dense_swiglu(x2, wgu_sh, wd_sh)
+        if side is not None:  # join before the combine reads the shared output
+            main.wait_stream(side)
+            shared.record_stream(main)
+        else:
+            shared = _dense_swiglu(x2, wgu_sh, wd_sh)
         return ops.combine(y, T, k, add=shared).view(shape)
+
 
 
 # ---------------------------------------------------------------------------------------------------------------
