@@ -14,6 +14,17 @@ def _dev_stream(t):
     return L.stream(t.device)
 
 
+_SIDE_STREAMS = {}  # device index -> side stream (kept off the modules, which may be copied or pickled)
+
+
+def side_stream(device: torch.device):
+    """One side stream per device for work that overlaps the main stream's, created with the default priority."""
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    if key not in _SIDE_STREAMS:
+        _SIDE_STREAMS[key] = torch.cuda.Stream(device=key)
+    return _SIDE_STREAMS[key]
+
+
 # Optional event probe: when `probe` is set to {op name: list}, each listed op records a (start, end) pair of
 # torch.cuda.Events on the stream its kernels are launched on (the current stream) around its C call.
 probe = None

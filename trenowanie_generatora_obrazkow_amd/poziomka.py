@@ -61,18 +61,6 @@ class _StackedMLP:
         return self.wgu, self.wd
 
 
-_SIDE_STREAMS = {}  # device index -> the side stream of PoziomkaMoE's shared expert (kept off the modules, which
-                    # may be copied or pickled)
-
-
-def _side_stream(device: torch.device):
-    """One side stream per device, created with the default priority."""
-    key = device.index if device.index is not None else torch.cuda.current_device()
-    if key not in _SIDE_STREAMS:
-        _SIDE_STREAMS[key] = torch.cuda.Stream(device=key)
-    return _SIDE_STREAMS[key]
-
-
 def _dense_swiglu(x2: torch.Tensor, wgu: torch.Tensor, wd: torch.Tensor) -> torch.Tensor:
     """bf16(bf16(silu(bf16(x Wg))) * bf16(x Wu)) Wd rounded to bf16 -- F.linear / F.silu in bf16 (aurora/
     hf_pipeline.py:322) -- for x2 (T, d) bf16."""
@@ -151,7 +139,7 @@ class PoziomkaMoE(nn.Module):
         T, k, E = x2.shape[0], self.top_k, self._wgu.shape[0]
         gw, gb = self._gate_tensors()
         wgu_sh, wd_sh = self.shared_experts._stack.get(self.shared_experts)
-        side = _side_stream(x2.device) if self.overlap_shared and T > 0 else None
+        side = ops.side_stream(x2.device) if self.overlap_shared and T > 0 else None
         if side is not None:  # fork: the shared expert needs only x
             main = torch.cuda.current_stream(x2.device)
             side.wait_stream(main)
