@@ -76,7 +76,7 @@ def zipf_bias(E, seed=0, s=1.2, n_empty=2):
     return b
 
 
-def time_steps(step, steps, warmup, graph, probe_kernel, probe_every=1):
+def time_steps(step, steps, warmup, graph, probe_kernel, probe_every=1, probe_first=0):
     """The timed region.  graph: the step is captured once as a HIP graph (graphs.StepGraph, after the warm-ups) and
     the timed region replays it `steps` times; an eager pass of the same number of steps follows, with events
     around the probe kernel's launches on its stream (its average launch time, for the roofline) and its own wall
@@ -109,9 +109,9 @@ def time_steps(step, steps, warmup, graph, probe_kernel, probe_every=1):
         step()
     torch.cuda.synchronize()
     eager_ms = (time.perf_counter() - t0) * 1e3 / steps
-    # every probe_every-th launch of the probe kernel (the BailingMoeV2 block launches it for the routed experts,
-    # then the shared expert)
-    dom = [a.elapsed_time(b) for a, b in ops.probe[probe_kernel][0::probe_every]]
+    # every probe_every-th launch of the probe kernel from launch probe_first on (the BailingMoeV2 block launches it
+    # twice per step: for the shared expert and the routed experts)
+    dom = [a.elapsed_time(b) for a, b in ops.probe[probe_kernel][probe_first::probe_every]]
     ops.probe = None
     return (ms if graph else eager_ms), eager_ms, statistics.mean(dom)
 
@@ -193,8 +193,10 @@ def _poziomka_block(w, g):
 
 
 def run_gpu_poziomka(w, steps, warmup, graph=False):
-    """Forward of the BailingMoeV2 block; the dominant kernel is the routed gate/up GEMM (int8 experts), the first
-    of the two gate/up launches of a step (the second is the shared expert)."""
+    """Forward of the BailingMoeV2 block; the dominant kernel is the routed gate/up GEMM (int8 experts).  A step
+    launches the gate/up and down GEMMs twice: the shared expert's first when it runs on its side stream
+    (overlap_shared, the default), else the routed experts' first.  With the shared expert overlapping, the routed
+    GEMMs' event times include the CUs they share with it."""
     import torch
 
     from trenowanie_generatora_obrazkow_amd import ops
@@ -208,7 +210,8 @@ def run_gpu_poziomka(w, steps, warmup, graph=False):
     def step():
         m(x)
 
-    ms, eager_ms, dom = time_steps(step, steps, warmup, graph, "gate_up_swiglu", probe_every=2)
+    routed = 1 if m.overlap_shared else 0  # position of the routed launch among a step's two
+    ms, eager_ms, dom = time_steps(step, steps, warmup, graph, "gate_up_swiglu", probe_every=2, probe_first=routed)
     names = ["route_topk", "dispatch", "gate_up_swiglu", "down_scatter", "combine"]
     ops.probe = {n: [] for n in names}
     nb = max(3, min(steps, 10))
@@ -218,9 +221,9 @@ def run_gpu_poziomka(w, steps, warmup, graph=False):
     kern = {}
     for n in names:
         ts = [a.elapsed_time(b) * 1e3 for a, b in ops.probe[n]]
-        if n in ("gate_up_swiglu", "down_scatter"):  # routed experts, then the shared expert
-            kern[n] = statistics.median(ts[0::2])
-            kern[n + "_shared"] = statistics.median(ts[1::2])
+        if n in ("gate_up_swiglu", "down_scatter"):  # the routed experts' and the shared expert's launches
+            kern[n] = statistics.median(ts[routed::2])
+            kern[n + "_shared"] = statistics.median(ts[1 - routed::2])
         else:
             kern[n] = statistics.median(ts)
     ops.probe = None
