@@ -196,7 +196,8 @@ int hmoe_combine_add(const void* y, int64_t T, int k, int64_t d, const void* add
  * ------------------------------------------------------------------------------------------------------------- */
 
 /* Backward of :80-82 (weight multiply + combine).  For each sorted row r (token t = a_idx[r], flat f = order[r]):
- * dys[r] = bf16(w_sorted[r] * dout[t]) (M, d) and dtopk_w[f] = <dout[t], yhat[r]> (fp32, fixed order). */
+ * dys[r] = bf16(w_sorted[r] * dout[t]) (M, d) and dtopk_w[f] = <dout[t], yhat[r]> (fp32, fixed order).  yhat NULL:
+ * dys only (order and dtopk_w unused; hmoe_down_dgrad_swiglu_dw then gives dtopk_w). */
 int hmoe_combine_bwd(const void* dout, const void* yhat, const int32_t* order, const int32_t* a_idx,
                      const uint16_t* w_sorted, int64_t M, int k, int64_t d, void* dys, float* dtopk_w,
                      hmoe_stream_t stream);
@@ -208,6 +209,18 @@ int hmoe_combine_bwd(const void* dout, const void* yhat, const int32_t* order, c
 int hmoe_down_dgrad_swiglu(const void* dy, const int32_t* a_idx, const uint16_t* w_sorted, const void* wd,
                            int64_t E, int64_t h, int64_t d, const void* counts, int counts_dtype, int64_t M,
                            const void* gu, void* dgu, hmoe_stream_t stream);
+
+/* hmoe_down_dgrad_swiglu plus the routing-weight gradient from the same product (backward of :81's scale): for each
+ * sorted row r (flat f = order[r]), dtopk_w[f] = sum_n (dy[a_idx[r]] @ wd[e]^T)[n] * act[r][n] with
+ * act = bf16(bf16(silu(g)) * u) recomputed from gu[r] exactly as the forward rounds it -- <dy[t], act[r] @ wd[e]> in
+ * fp32, without a rounded copy of the down projection's output.  Per-(row, column block) partials go to the
+ * workspace (hmoe_down_dgrad_dw_workspace_size(M, h) bytes, 16-byte aligned) and are added in column-block order.
+ * Has no counterpart in the reference (its MoE path has no backward). */
+size_t hmoe_down_dgrad_dw_workspace_size(int64_t M, int64_t h);
+int hmoe_down_dgrad_swiglu_dw(const void* dy, const int32_t* a_idx, const uint16_t* w_sorted, const void* wd,
+                              int64_t E, int64_t h, int64_t d, const void* counts, int counts_dtype, int64_t M,
+                              const void* gu, void* dgu, const int32_t* order, float* dtopk_w, void* workspace,
+                              size_t workspace_bytes, hmoe_stream_t stream);
 
 /* Backward of :79 to the sorted input rows: dxs[r] = dgu[r] @ wgu[e]^T, stored bf16 or fp32 (dxs_dtype). */
 int hmoe_gate_up_dgrad(const void* dgu, const void* wgu, int64_t E, int64_t d, int64_t h, const void* counts,

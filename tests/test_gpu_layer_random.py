@@ -1,0 +1,59 @@
+"""Seeded random layer configurations, forward and backward, against the float64 oracle: token counts, widths, expert
+counts, top-k, renormalisation and logit biases (Zipf-skewed with never-routed experts) drawn from one generator, so
+every run checks the same cases.  Routing is bit-exact; the output and the four gradients meet the bf16 tolerance."""
+import numpy as np
+import pytest
+import torch
+
+from tests.util import assert_close_bf16, bits, f32, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _configs(n=12, seed=2024):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        E = int(rng.integers(2, 41))
+        k = int(rng.integers(1, min(E, 6) + 1))
+        T = int(rng.integers(1, 701))
+        d = 8 * int(rng.integers(1, 66))    # 8 .. 520
+        h = 8 * int(rng.integers(1, 66))
+        renorm = bool(rng.integers(0, 2))
+        zipf = bool(rng.integers(0, 3) == 0) and E - 2 >= k  # the two never-routed experts leave k to pick from
+        out.append((i, T, d, E, k, h, renorm, zipf))
+    return out
+
+
+@pytest.mark.parametrize("case,T,d,E,k,h,renorm,zipf", _configs())
+def test_layer_random_config(oracle, case, T, d, E, k, h, renorm, zipf):
+    from trenowanie_generatora_obrazkow_amd import moe_swiglu
+    print(f"random layer case {case}: T={T} d={d} E={E} k={k} h={h} renorm={renorm} zipf={zipf}", flush=True)
+    x, wr, wgu, wd = make_inputs(T, d, E, h, seed=100 + case)
+    g = torch.Generator().manual_seed(200 + case)
+    dout = torch.randn(T, d, generator=g).bfloat16()
+    bias = oracle.zipf_bias(E, seed=case) if zipf else None
+    dev = torch.device("cuda")
+    xg, wrg, wgug, wdg = (t.to(dev).requires_grad_(True) for t in (x, wr, wgu, wd))
+    b = None if bias is None else torch.as_tensor(bias).float().to(dev)
+    out, ids, tw = moe_swiglu(xg, wrg, wgug, wdg, k, logit_bias=b, renorm=renorm)
+    out.backward(dout.to(dev))
+    torch.cuda.synchronize()
+
+    logits, rids, rw = oracle.route(bits(x), bits(wr), k, bias=bias, renorm=renorm)
+    np.testing.assert_array_equal(ids.cpu().numpy(), rids)
+    np.testing.assert_array_equal(tw.detach().cpu().numpy().view(np.uint32), rw.view(np.uint32))
+    fwd = oracle.moe_forward(f32(x), rids, rw, f32(wgu), f32(wd))
+    assert_close_bf16(f32(out), fwd["out"], "out")
+    ref = oracle.layer_backward(f32(x), f32(wr), rids, rw, logits, f32(wgu), f32(wd), f32(dout), renorm=renorm,
+                                fwd=fwd)
+    R = oracle.round_bf16
+    assert_close_bf16(f32(xg.grad), R(ref["dx"]), "dx")
+    assert_close_bf16(f32(wgug.grad), R(ref["dwgu"]), "dwgu")
+    assert_close_bf16(f32(wdg.grad), R(ref["dwd"]), "dwd")
+    if k == 1 and renorm:
+        # one renormalised weight is exactly 1: its logit gradient, and so dWr, is zero up to fp32 rounding (the
+        # float64 oracle's is zero up to float64 rounding, so a relative comparison would divide noise by noise)
+        assert np.abs(f32(wrg.grad)).max() <= 1e-6, "dwr of a top-1 renormalised router"
+    else:
+        assert_close_bf16(f32(wrg.grad), R(ref["dwr"]), "dwr")

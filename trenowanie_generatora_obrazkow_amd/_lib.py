@@ -49,6 +49,9 @@ SIGNATURES = {
     "hmoe_combine_add": (_I32, [_P, _I64, _I32, _I64, _P, _P, _P]),
     "hmoe_combine_bwd": (_I32, [_P, _P, _P, _P, _P, _I64, _I32, _I64, _P, _P, _P]),
     "hmoe_down_dgrad_swiglu": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P]),
+    "hmoe_down_dgrad_dw_workspace_size": (_SZ, [_I64, _I64]),
+    "hmoe_down_dgrad_swiglu_dw": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P, _P, _P, _SZ,
+                                         _P]),
     "hmoe_gate_up_dgrad": (_I32, [_P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P, _I32, _P]),
     "hmoe_grouped_wgrad": (_I32, [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I32, _I64, _P, _I32, _P]),
     "hmoe_router_bwd_workspace_size": (_SZ, [_I64, _I32, _I64]),

@@ -762,6 +762,9 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
         if (a == 0) issue_gu(0);
         wait_vm<0>();  // this pass's [g | u] (and the previous pass's stores: in-order counter)
         asm volatile("" ::: "memory");
+        // With dw_part: the routing-weight gradient of the lane's row, sum over its columns of the unscaled product
+        // (dy @ wd^T) times the forward's act = bf16(bf16(silu(g)) * u), in a fixed order (b, g, t).
+        float dwl = 0.0f;
 #pragma unroll
         for (int b = 0; b < C::FN; ++b) {
           pin_agpr(acc[a][b]);
@@ -779,12 +782,22 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
               const float sig = sigmoid_f(gg[t]);
               const float sl = gg[t] * sig;
               // du uses the forward's stored factor bf16(silu(g)); silu_f(g) = g * sig
-              du[t] = da * bf_lo(cvt_bf2(sl, sl));
+              const float slb = bf_lo(cvt_bf2(sl, sl));
+              du[t] = da * slb;
               dg[t] = da * uu[t] * sig * (1.0f + gg[t] * (1.0f - sig));
+              if (p.dw_part) {
+                const float av = slb * uu[t];
+                dwl = __builtin_fmaf(acc[a][b][4 * g + t], bf_lo(cvt_bf2(av, av)), dwl);
+              }
             }
             park_bf16(0, b, g, cvt_bf2(dg[0], dg[1]), cvt_bf2(dg[2], dg[3]));
             park_bf16(NSP, b, g, cvt_bf2(du[0], du[1]), cvt_bf2(du[2], du[3]));
           }
+        }
+        if (p.dw_part) {  // lanes l and l + 32 hold the two column halves of one row
+          dwl += __shfl_xor(dwl, 32);
+          const int64_t row = row0 + rbase + lrow;
+          if (lane < 32 && row < row_end) p.dw_part[row * p.dw_ld + 2 * nb + wn] = dwl;
         }
         // the next pass's inputs load while this pass drains (its g / u sub-planes have been read above)
         if (a + 1 < fe_rows) issue_gu(a + 1);
@@ -1152,17 +1165,19 @@ int hmoe_down_scatter_i8(const void* act, const void* wd_q, const void* wd_s, in
   return launch_mgroup_i8<EPI_STORE>(p, d, reinterpret_cast<hipStream_t>(stream));
 }
 
-int hmoe_down_dgrad_swiglu(const void* dy, const int32_t* a_idx, const uint16_t* w_sorted, const void* wd,
-                           int64_t E, int64_t h, int64_t d, const void* counts, int counts_dtype, int64_t M,
-                           const void* gu, void* dgu, hmoe_stream_t stream) {
-  int rc = check_common(counts, counts_dtype, E, M);
-  if (rc) return rc;
-  if (M == 0) return HMOE_OK;
-  if (!dy || !wd || !gu || !dgu || d <= 0 || h <= 0) return HMOE_ERR_ARG;
-  if (d % 8 || h % 8) return HMOE_ERR_SHAPE;
-  if (!al16(dy) || !al16(wd) || !al16(gu) || !al16(dgu)) return HMOE_ERR_ARG;
-  if ((a_idx && !off32(M * d * 2)) || !off32(h * d * 2)) return HMOE_ERR_SHAPE;
-  GemmParams p = base_params(counts, counts_dtype, E, M);
+// Checks and parameters shared by the two down-dgrad entry points (rc: HMOE_OK, or the error to return).
+static GemmParams down_dgrad_params(const void* dy, const int32_t* a_idx, const uint16_t* w_sorted, const void* wd,
+                                    int64_t E, int64_t h, int64_t d, const void* counts, int counts_dtype, int64_t M,
+                                    const void* gu, void* dgu, int* rc) {
+  GemmParams p = {};
+  *rc = check_common(counts, counts_dtype, E, M);
+  if (*rc || M == 0) return p;
+  if (!dy || !wd || !gu || !dgu || d <= 0 || h <= 0) *rc = HMOE_ERR_ARG;
+  else if (d % 8 || h % 8) *rc = HMOE_ERR_SHAPE;
+  else if (!al16(dy) || !al16(wd) || !al16(gu) || !al16(dgu)) *rc = HMOE_ERR_ARG;
+  else if ((a_idx && !off32(M * d * 2)) || !off32(h * d * 2)) *rc = HMOE_ERR_SHAPE;
+  if (*rc) return p;
+  p = base_params(counts, counts_dtype, E, M);
   p.A = static_cast<const uint16_t*>(dy);
   p.lda = d;
   p.a_idx = a_idx;
@@ -1175,7 +1190,62 @@ int hmoe_down_dgrad_swiglu(const void* dy, const int32_t* a_idx, const uint16_t*
   p.C = dgu;
   p.scale = w_sorted;
   p.gu_in = static_cast<const uint16_t*>(gu);
+  return p;
+}
+
+int hmoe_down_dgrad_swiglu(const void* dy, const int32_t* a_idx, const uint16_t* w_sorted, const void* wd,
+                           int64_t E, int64_t h, int64_t d, const void* counts, int counts_dtype, int64_t M,
+                           const void* gu, void* dgu, hmoe_stream_t stream) {
+  int rc = HMOE_OK;
+  GemmParams p = down_dgrad_params(dy, a_idx, w_sorted, wd, E, h, d, counts, counts_dtype, M, gu, dgu, &rc);
+  if (rc || M == 0) return rc;
   return launch_mgroup<MGROUP, false, false, EPI_SWIGLU_BWD>(p, h, reinterpret_cast<hipStream_t>(stream));
+}
+
+// partials per row of hmoe_down_dgrad_swiglu_dw's routing-weight gradient: two per n-tile of the chosen tile size
+static int64_t dw_partials(int64_t h, bool large) {
+  const int64_t bn = large ? CfgL::BN : CfgS::BN;
+  return 2 * ((h + bn - 1) / bn);
+}
+
+size_t hmoe_down_dgrad_dw_workspace_size(int64_t M, int64_t h) {
+  if (M <= 0 || h <= 0) return 256;
+  return (size_t)(M * dw_partials(h, false) * 4 + 255) / 256 * 256;  // the small tiles' count is the larger
+}
+
+// dtopk_w[order[r]] = sum over p of part[r * P + p], in p order
+__global__ __launch_bounds__(256) void dw_reduce_kernel(const float* __restrict__ part, int P, int64_t M,
+                                                        const int32_t* __restrict__ order, float* __restrict__ dtw) {
+  for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < M; r += (int64_t)gridDim.x * blockDim.x) {
+    const float* pr = part + r * P;
+    float s = 0.0f;
+    for (int q = 0; q < P; ++q) s += pr[q];
+    dtw[order[r]] = s;
+  }
+}
+
+int hmoe_down_dgrad_swiglu_dw(const void* dy, const int32_t* a_idx, const uint16_t* w_sorted, const void* wd,
+                              int64_t E, int64_t h, int64_t d, const void* counts, int counts_dtype, int64_t M,
+                              const void* gu, void* dgu, const int32_t* order, float* dtopk_w, void* workspace,
+                              size_t workspace_bytes, hmoe_stream_t stream) {
+  int rc = HMOE_OK;
+  GemmParams p = down_dgrad_params(dy, a_idx, w_sorted, wd, E, h, d, counts, counts_dtype, M, gu, dgu, &rc);
+  if (rc || M == 0) return rc;
+  if (!order || !dtopk_w) return HMOE_ERR_ARG;
+  if (!workspace || workspace_bytes < hmoe_down_dgrad_dw_workspace_size(M, h) || !al16(workspace))
+    return HMOE_ERR_WORKSPACE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t tl = mgroup_tiles<CfgL, EPI_SWIGLU_BWD>(M, E, h);
+  const bool large = pick_large_mgroup<EPI_SWIGLU_BWD>(tl, h, d, false);
+  p.dw_part = static_cast<float*>(workspace);
+  p.dw_ld = (int)dw_partials(h, large);
+  rc = large ? launch<CfgL, MGROUP, false, false, EPI_SWIGLU_BWD>(p, tl, s)
+             : launch<CfgS, MGROUP, false, false, EPI_SWIGLU_BWD>(p, mgroup_tiles<CfgS, EPI_SWIGLU_BWD>(M, E, h), s);
+  if (rc) return rc;
+  hipLaunchKernelGGL(dw_reduce_kernel, dim3((unsigned)std::min<int64_t>((M + 255) / 256, 4096)), dim3(256), 0, s,
+                     p.dw_part, p.dw_ld, M, order, dtopk_w);
+  HMOE_CHECK_LAUNCH();
+  return HMOE_OK;
 }
 
 int hmoe_gate_up_dgrad(const void* dgu, const void* wgu, int64_t E, int64_t d, int64_t h, const void* counts,

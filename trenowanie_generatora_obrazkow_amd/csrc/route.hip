@@ -921,6 +921,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
 }
 
 // one wave per sorted row: dys[r] = bf16(w_r * dout[t]); dtopk_w[f] = <dout[t], yhat[r]>
+// DW: also dtopk_w[order[r]] = <dout[t], yhat[r]>; without it the scaled rows dys only.
+template <bool DW>
 __global__ __launch_bounds__(256) void combine_bwd_kernel(const uint16_t* __restrict__ dout,
                                                           const uint16_t* __restrict__ yhat,
                                                           const int32_t* __restrict__ order,
@@ -936,24 +938,29 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(const uint16_t* __rest
     const int64_t t = a_idx[r];
     const float wr = bf2f(w_sorted[r]);
     const uint4* go = reinterpret_cast<const uint4*>(dout + t * d);
-    const uint4* yh = reinterpret_cast<const uint4*>(yhat + r * d);
     uint4* dy = reinterpret_cast<uint4*>(dys + r * d);
     float acc = 0.0f;
     for (int64_t c = lane; c < nvec; c += 64) {
-      const uint4 g = go[c], yv = yh[c];
+      const uint4 g = go[c];
+      uint4 yv = make_uint4(0, 0, 0, 0);
+      if constexpr (DW) yv = reinterpret_cast<const uint4*>(yhat + r * d)[c];
       const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, yw[4] = {yv.x, yv.y, yv.z, yv.w};
       uint32_t ow[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const float g0 = bf_lo(gw[q]), g1 = bf_hi(gw[q]);
-        acc = __fadd_rn(acc, __fmul_rn(g0, bf_lo(yw[q])));
-        acc = __fadd_rn(acc, __fmul_rn(g1, bf_hi(yw[q])));
+        if constexpr (DW) {
+          acc = __fadd_rn(acc, __fmul_rn(g0, bf_lo(yw[q])));
+          acc = __fadd_rn(acc, __fmul_rn(g1, bf_hi(yw[q])));
+        }
         ow[q] = pack_bf2(__fmul_rn(wr, g0), __fmul_rn(wr, g1));
       }
       dy[c] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
     }
-    acc = wave_sum_butterfly(acc);
-    if (lane == 0) dtopk_w[order[r]] = acc;
+    if constexpr (DW) {
+      acc = wave_sum_butterfly(acc);
+      if (lane == 0) dtopk_w[order[r]] = acc;
+    }
   }
 }
 
@@ -1705,12 +1712,19 @@ int hmoe_combine_bwd(const void* dout, const void* yhat, const int32_t* order, c
                      hmoe_stream_t stream) {
   if (M < 0 || k <= 0 || d <= 0) return HMOE_ERR_ARG;
   if (M == 0) return HMOE_OK;
-  if (!dout || !yhat || !order || !a_idx || !w_sorted || !dys || !dtopk_w) return HMOE_ERR_ARG;
+  const bool dw = yhat != nullptr;  // without yhat: the scaled rows only (dtopk_w and order unused)
+  if (!dout || !a_idx || !w_sorted || !dys || (dw && (!order || !dtopk_w))) return HMOE_ERR_ARG;
   if (d % 8 || !al16(dout) || !al16(yhat) || !al16(dys)) return HMOE_ERR_ARG;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(combine_bwd_kernel, dim3(grid_for(M, 4, 16384)), dim3(256), 0, s,
-                     static_cast<const uint16_t*>(dout), static_cast<const uint16_t*>(yhat), order, a_idx, w_sorted,
-                     M, k, d, static_cast<uint16_t*>(dys), dtopk_w);
+#define HMOE_CBWD(DW)                                                                                              \
+  hipLaunchKernelGGL((combine_bwd_kernel<DW>), dim3(grid_for(M, 4, 16384)), dim3(256), 0, s,                        \
+                     static_cast<const uint16_t*>(dout), static_cast<const uint16_t*>(yhat), order, a_idx, w_sorted, \
+                     M, k, d, static_cast<uint16_t*>(dys), dtopk_w)
+  if (dw)
+    HMOE_CBWD(true);
+  else
+    HMOE_CBWD(false);
+#undef HMOE_CBWD
   HMOE_CHECK_LAUNCH();
   return HMOE_OK;
 }

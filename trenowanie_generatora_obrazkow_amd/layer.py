@@ -7,8 +7,8 @@ Forward (all hmoe HIP kernels, one stream, no host sync):
   a backward to follow, also the row-major permuted copy) -> gate/up GEMM with fused SwiGLU ->
   down GEMM x routing weight, scattered to (token, slot) order -> combine over the k slots.
 Backward:
-  combine_bwd (weighted dY for the down wgrad, routing-weight grads) -> down dgrad (dY rows gathered, routing
-  weight applied in fp32) with fused SwiGLU backward -> down wgrad -> gate/up dgrad (fp32 rows) ->
+  combine_bwd (weighted dY for the down wgrad) -> down wgrad -> down dgrad (dY rows gathered, routing weight
+  applied in fp32) with fused SwiGLU backward and the routing-weight gradients -> gate/up dgrad (fp32 rows) ->
   gate/up wgrad -> router backward (softmax + renormalisation Jacobian, dWr) -> un-permute (sum over
   the k slots) + router input gradient.
 
@@ -65,11 +65,11 @@ class _MoEFunction(torch.autograd.Function):
         # also the row-major permuted copy xs (the gate/up weight gradient reads it).
         disp, act, gu = ops.routed_gate_up(x, ids, E, wgu, topk_w=tw, keep_gu=need_grad, want_xs=need_grad,
                                            want_inv=need_grad)
-        y, yhat = ops.down_scatter(act, wd, disp.counts, M, disp.w_sorted, disp.order, keep_yhat=need_grad)
+        y, _ = ops.down_scatter(act, wd, disp.counts, M, disp.w_sorted, disp.order)
         out = ops.combine(y, T, k)
         if need_grad:
             ctx.save_for_backward(x, wr, wgu, wd, logits, ids, disp.counts, disp.order, disp.a_idx, disp.inv_pos,
-                                  disp.w_sorted, disp.xs, gu, act, yhat)
+                                  disp.w_sorted, disp.xs, gu, act)
         ctx.k, ctx.renorm = k, renorm
         ctx.mark_non_differentiable(ids)
         ctx.set_materialize_grads(False)  # absent output gradients stay None (no zero-filled tensors)
@@ -79,8 +79,7 @@ class _MoEFunction(torch.autograd.Function):
     def backward(ctx, dout, _dids, dtw_out):
         if dout is None and dtw_out is None:
             return None, None, None, None, None, None, None
-        (x, wr, wgu, wd, logits, ids, counts, order, a_idx, inv_pos, w_sorted, xs, gu, act,
-         yhat) = ctx.saved_tensors
+        x, wr, wgu, wd, logits, ids, counts, order, a_idx, inv_pos, w_sorted, xs, gu, act = ctx.saved_tensors
         k = ctx.k
         T, d = x.shape
         E = wgu.shape[0]
@@ -92,13 +91,14 @@ class _MoEFunction(torch.autograd.Function):
         dout = dout.contiguous().to(torch.bfloat16)
         # One stream: every GEMM is a persistent launch sized to own all CUs, so two of them side by side only
         # queue each other's workgroups behind long-running tiles.
-        dys, dtw = ops.combine_bwd(dout, yhat, disp, k)
-        if dtw_out is not None:  # the returned routing weights are outputs too: their gradient joins the combine's
-            dtw = dtw + dtw_out.to(torch.float32)
+        dys, _ = ops.combine_bwd(dout, None, disp, k)
         dwd = dwgu = None
         if ctx.needs_input_grad[3]:
             dwd = ops.grouped_wgrad(act, dys, counts, E, dtype=wd_dt)
-        dgu = ops.down_dgrad_swiglu(dout, wd, counts, M, gu, a_idx=a_idx, w_sorted=w_sorted)
+        # dgu, and the routing-weight gradient <dout[t], act[r] @ wd[e]> from the same fp32 product
+        dgu, dtw = ops.down_dgrad_swiglu_dw(dout, wd, counts, M, gu, order, k, a_idx=a_idx, w_sorted=w_sorted)
+        if dtw_out is not None:  # the returned routing weights are outputs too: their gradient joins the combine's
+            dtw = dtw + dtw_out.to(torch.float32)
         if ctx.needs_input_grad[2]:
             dwgu = ops.grouped_wgrad(xs, dgu, counts, E, dtype=wgu_dt)
         dxs = ops.gate_up_dgrad(dgu, wgu, counts, M)

@@ -381,16 +381,19 @@ def combine(y, T, k, add=None):
 
 
 def combine_bwd(dout, yhat, disp: Dispatch, k):
-    M, d = yhat.shape
-    T = M // k
+    """(dys (M, d) bf16, dtopk_w (T, k) fp32): the routing-weighted upstream rows in sorted order and, with yhat
+    (the unscaled down-projection rows, sorted), <dout[t], yhat[r]>; yhat None: (dys, None)."""
+    T, d = dout.shape
+    M = T * k
     dout = dout.contiguous()
-    _need(yhat, "yhat", (T * k, d), _BF16)
+    if yhat is not None:
+        _need(yhat, "yhat", (M, d), _BF16)
     _need(dout, "dout", (T, d), _BF16)
     for t_, n_ in ((disp.order, "order"), (disp.a_idx, "a_idx")):
         _need(t_, n_, (M,), _I32)
     _need(disp.w_sorted, "w_sorted", (M,), _BF16)
     dys = torch.empty(M, d, device=dout.device, dtype=torch.bfloat16)
-    dtw = torch.empty(T, k, device=dout.device, dtype=torch.float32)
+    dtw = torch.empty(T, k, device=dout.device, dtype=torch.float32) if yhat is not None else None
     with _Probe("combine_bwd"):
         L.call("hmoe_combine_bwd", L.ptr(dout), L.ptr(yhat), L.ptr(disp.order), L.ptr(disp.a_idx), L.ptr(disp.w_sorted),
                M, k, d, L.ptr(dys), L.ptr(dtw), _dev_stream(dout))
@@ -413,6 +416,33 @@ def down_dgrad_swiglu(dy, wd, counts, M, gu, a_idx=None, w_sorted=None):
         L.call("hmoe_down_dgrad_swiglu", L.ptr(dy), L.ptr(a_idx), L.ptr(w_sorted), L.ptr(wd), E, h, d, L.ptr(counts),
                L.dt(counts), M, L.ptr(gu), L.ptr(dgu), _dev_stream(dy))
     return dgu
+
+
+def down_dgrad_swiglu_dw(dy, wd, counts, M, gu, order, k, a_idx=None, w_sorted=None):
+    """(dgu, dtopk_w): down_dgrad_swiglu's dgu and, from the same product, the routing-weight gradient dtopk_w (T, k)
+    fp32 = sum_n (dy[t] @ wd[e]^T)[n] * act[r][n], act recomputed from gu as the forward rounds it."""
+    _need(wd, "wd", (None, None, None), _BF16)
+    E, h, d = wd.shape
+    counts = _counts(counts, E)
+    a_idx = _rows_index(a_idx, "a_idx", M)
+    _need(dy, "dy", (None, d), _BF16, min_rows=min(1, M) if a_idx is not None else M)
+    _need(gu, "gu", (M, 2 * h), _BF16)
+    order = _rows_index(order, "order", M)
+    if order is None:
+        raise ValueError("order is required")
+    if w_sorted is not None:
+        _need(w_sorted, "w_sorted", (M,), _BF16)
+    if M % k:
+        raise ValueError(f"M = {M} is not a multiple of k = {k}")
+    dgu = torch.empty(M, 2 * h, device=dy.device, dtype=torch.bfloat16)
+    dtw = torch.empty(M // k, k, device=dy.device, dtype=torch.float32)
+    ws_bytes = L.lib().hmoe_down_dgrad_dw_workspace_size(M, h)
+    ws = torch.empty(ws_bytes, device=dy.device, dtype=torch.uint8)
+    with _Probe("down_dgrad_swiglu"):
+        L.call("hmoe_down_dgrad_swiglu_dw", L.ptr(dy), L.ptr(a_idx), L.ptr(w_sorted), L.ptr(wd), E, h, d,
+               L.ptr(counts), L.dt(counts), M, L.ptr(gu), L.ptr(dgu), L.ptr(order), L.ptr(dtw), L.ptr(ws), ws_bytes,
+               _dev_stream(dy))
+    return dgu, dtw
 
 
 def gate_up_dgrad(dgu, wgu, counts, M, dtype=torch.float32):
