@@ -797,7 +797,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
         if (p.dw_part) {  // lanes l and l + 32 hold the two column halves of one row
           dwl += __shfl_xor(dwl, 32);
           const int64_t row = row0 + rbase + lrow;
-          if (lane < 32 && row < row_end) p.dw_part[row * p.dw_ld + 2 * nb + wn] = dwl;
+          if (lane < 32 && row < row_end) p.dw_part[(int64_t)(2 * nb + wn) * p.M + row] = dwl;  // (partial, row)
         }
         // the next pass's inputs load while this pass drains (its g / u sub-planes have been read above)
         if (a + 1 < fe_rows) issue_gu(a + 1);
@@ -1213,13 +1213,12 @@ size_t hmoe_down_dgrad_dw_workspace_size(int64_t M, int64_t h) {
   return (size_t)(M * dw_partials(h, false) * 4 + 255) / 256 * 256;  // the small tiles' count is the larger
 }
 
-// dtopk_w[order[r]] = sum over p of part[r * P + p], in p order
+// dtopk_w[order[r]] = sum over q of part[q * M + r], in q order (partial-major: a thread per row, coalesced rows)
 __global__ __launch_bounds__(256) void dw_reduce_kernel(const float* __restrict__ part, int P, int64_t M,
                                                         const int32_t* __restrict__ order, float* __restrict__ dtw) {
   for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < M; r += (int64_t)gridDim.x * blockDim.x) {
-    const float* pr = part + r * P;
     float s = 0.0f;
-    for (int q = 0; q < P; ++q) s += pr[q];
+    for (int q = 0; q < P; ++q) s += part[(int64_t)q * M + r];
     dtw[order[r]] = s;
   }
 }

@@ -336,7 +336,7 @@ struct GemmParams {
   int scale_f32;
   uint16_t* aux;            // EPI_STORE: yhat (unscaled, sorted); EPI_SWIGLU: gu store
   const uint16_t* gu_in;    // EPI_SWIGLU_BWD: [g | u]
-  float* dw_part;           // EPI_SWIGLU_BWD: per-(row, column block) partials of the routing-weight gradient, or NULL
+  float* dw_part;           // EPI_SWIGLU_BWD: (partial, row) array of the routing-weight gradient's partials, or NULL
   int dw_ld;                //   partials per row: 2 per n-tile (one per wave column)
   const void* w_scale;      // int8 weights: per-(expert, column) scale (E, ldws), bf16 or fp32
   int w_scale_f32;
