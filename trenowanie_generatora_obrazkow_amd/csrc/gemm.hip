@@ -1218,7 +1218,14 @@ __global__ __launch_bounds__(256) void dw_reduce_kernel(const float* __restrict_
                                                         const int32_t* __restrict__ order, float* __restrict__ dtw) {
   for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < M; r += (int64_t)gridDim.x * blockDim.x) {
     float s = 0.0f;
-    for (int q = 0; q < P; ++q) s += part[(int64_t)q * M + r];
+    for (int q0 = 0; q0 < P; q0 += 8) {  // eight loads in flight, added in q order
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = q0 + u < P ? part[(int64_t)(q0 + u) * M + r] : 0.0f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (q0 + u < P) s += v[u];
+    }
     dtw[order[r]] = s;
   }
 }
