@@ -1,6 +1,12 @@
 """Seeded random layer configurations, forward and backward, against the float64 oracle: token counts, widths, expert
 counts, top-k, renormalisation and logit biases (Zipf-skewed with never-routed experts) drawn from one generator, so
-every run checks the same cases.  Routing is bit-exact; the output and the four gradients meet the bf16 tolerance."""
+every run checks the same cases.  Routing is bit-exact; the output and the four gradients meet the bf16 tolerance.
+
+Of the first 80 draws (HMOE_RANDOM_CASES=80) one misses the mean tolerance: case 19 (419 tokens, d 8, h 24, 22
+experts, top-1, Zipf) with dWgu at 2.03e-3.  The backward holds dgu = [dg | du] in bf16, as autograd holds the
+gradient of bf16 tensors; for experts with a handful of rows its 2^-9 rounding reaches dWgu almost unaveraged."""
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -25,7 +31,8 @@ def _configs(n=12, seed=2024):
     return out
 
 
-@pytest.mark.parametrize("case,T,d,E,k,h,renorm,zipf", _configs())
+# HMOE_RANDOM_CASES widens the draw (the same seed: the first 12 cases are always these)
+@pytest.mark.parametrize("case,T,d,E,k,h,renorm,zipf", _configs(int(os.environ.get("HMOE_RANDOM_CASES", "12"))))
 def test_layer_random_config(oracle, case, T, d, E, k, h, renorm, zipf):
     from trenowanie_generatora_obrazkow_amd import moe_swiglu
     print(f"random layer case {case}: T={T} d={d} E={E} k={k} h={h} renorm={renorm} zipf={zipf}", flush=True)
