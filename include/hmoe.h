@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define HMOE_ABI_VERSION 1
+#define HMOE_ABI_VERSION 2
 
 #define HMOE_OK 0
 #define HMOE_ERR_ARG (-1)       /* null pointer, negative size, misaligned pointer or leading dimension */
@@ -86,13 +86,18 @@ size_t hmoe_dispatch_workspace_size(int64_t T, int k, int E);
  * topk_ids (T, k) int32 or int64 (ids_dtype), topk_w (T, k) fp32 or bf16 (w_dtype; NULL to skip w_sorted).
  * Outputs (NULL skips an optional one): counts (E,) int32 [required], counts64 (E,) int64, starts (E+1,) int32
  * [required; starts[e] = first sorted row of expert e], order (M,) int32 (= y_idx), a_idx (M,) int32,
- * inv_pos (M,) int32, w_sorted (M,) bf16, xs (M, d) bf16 = x[a_idx] (needs x (T, d) bf16 with row stride ldx).
- * Expert ids outside [0, E) are counted nowhere and make the rows they own undefined; the caller validates ids.
- * E <= 1024. */
+ * inv_pos (M,) int32, w_sorted (M,) bf16, xs (M, d) bf16 = x[a_idx] (needs x (T, d) bf16 with row stride ldx),
+ * n_invalid (1,) int32.
+ * Expert ids outside [0, E) route nowhere: their flat rows are counted in no expert and get inv_pos = -1, the
+ * Sigma counts sorted rows hold the valid ones (the sorted rows past that are not written), and n_invalid receives
+ * how many there are (on the device, no host sync: the caller reads it when it chooses).  hmoe_combine with inv_pos
+ * then adds zeros for those slots and hmoe_unpermute_bwd skips them, so the layer's output is defined (the slot
+ * contributes nothing).  The reference leaves such ids undefined (torch.bincount raises on negative ones and grows
+ * the count array for ids >= E, aurora/hf_compat.py:72).  E <= 1024. */
 int hmoe_dispatch(const void* topk_ids, int ids_dtype, const void* topk_w, int w_dtype, int64_t T, int k, int E,
                   const void* x, int64_t ldx, int64_t d, void* xs, int32_t* counts, int64_t* counts64,
                   int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos, uint16_t* w_sorted,
-                  void* workspace, size_t workspace_bytes, hmoe_stream_t stream);
+                  int32_t* n_invalid, void* workspace, size_t workspace_bytes, hmoe_stream_t stream);
 
 /* Bytes of the row-group tiles (xs_tiles) for M sorted rows of width d over E experts (an upper bound: it does not
  * depend on the counts).  0 for invalid sizes. */
@@ -108,7 +113,8 @@ size_t hmoe_xs_tiles_bytes(int64_t M, int E, int64_t d);
 int hmoe_dispatch_tiles(const void* topk_ids, int ids_dtype, const void* topk_w, int w_dtype, int64_t T, int k, int E,
                         const void* x, int64_t ldx, int64_t d, void* xs, void* xs_tiles, int32_t* counts,
                         int64_t* counts64, int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos,
-                        uint16_t* w_sorted, void* workspace, size_t workspace_bytes, hmoe_stream_t stream);
+                        uint16_t* w_sorted, int32_t* n_invalid, void* workspace, size_t workspace_bytes,
+                        hmoe_stream_t stream);
 
 /* Allocation-free form of hmoe_dispatch.  No counterpart in the reference: it is for callers that cannot allocate
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same arguments, checks and
@@ -121,7 +127,7 @@ int hmoe_dispatch_tiles(const void* topk_ids, int ids_dtype, const void* topk_w,
 int hmoe_dispatch_noalloc(const void* topk_ids, int ids_dtype, const void* topk_w, int w_dtype, int64_t T, int k,
                           int E, const void* x, int64_t ldx, int64_t d, void* xs, int32_t* counts, int64_t* counts64,
                           int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos, uint16_t* w_sorted,
-                          hmoe_stream_t stream);
+                          int32_t* n_invalid, hmoe_stream_t stream);
 
 /* make_schedule: replaces aurora/moe_triton.py:93-107.  For each of the ceil(M / block_m) + E blocks: the expert
  * (or -1), the first sorted row and the end row of that expert, int32, computed on the device from counts
@@ -181,14 +187,17 @@ int hmoe_down_scatter_i8(const void* act, const void* wd_q, const void* wd_s, in
                          int64_t d, const void* counts, int counts_dtype, int64_t M, const uint16_t* w_sorted,
                          const int32_t* y_idx, void* y, hmoe_stream_t stream);
 
-/* Combine: replaces aurora/hf_compat.py:82 (y.view(n, k, -1).sum(1)): out[t] = bf16(sum_j fp32(y[t*k + j])). */
-int hmoe_combine(const void* y, int64_t T, int k, int64_t d, void* out, hmoe_stream_t stream);
+/* Combine: replaces aurora/hf_compat.py:82 (y.view(n, k, -1).sum(1)): out[t] = bf16(sum_j fp32(y[t*k + j])).
+ * inv_pos (T * k,) int32 from the dispatch, or NULL: slots with a negative inv_pos (expert ids outside [0, E)) are
+ * read as zeros instead of their (unwritten) row of y. */
+int hmoe_combine(const void* y, const int32_t* inv_pos, int64_t T, int k, int64_t d, void* out, hmoe_stream_t stream);
 
 /* Combine plus a per-token addend: replaces aurora/hf_pipeline.py:370 (out.to(x.dtype) + self.shared_experts(x)):
  * out[t] = bf16(bf16(sum_j fp32(y[t*k + j])) + add[t]), add (T, d) bf16 (the shared expert's output).  The
  * reference sums the slots with index_add_ in expert order (:369); here they are summed in slot order (the same
  * terms, fp32 accumulation). */
-int hmoe_combine_add(const void* y, int64_t T, int k, int64_t d, const void* add, void* out, hmoe_stream_t stream);
+int hmoe_combine_add(const void* y, const int32_t* inv_pos, int64_t T, int k, int64_t d, const void* add, void* out,
+                     hmoe_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------------------------
  * Backward.  The reference has no backward for this path (aurora/hf_compat.py:62 is @torch.no_grad); each entry
@@ -247,7 +256,7 @@ int hmoe_router_bwd(const float* logits, const int32_t* topk_ids, const float* d
 
 /* Input gradient: backward of the gather x[order // k] (:83 / a_idx of :78) plus the router's x.float() @ wr^T:
  * dx[t] = bf16(sum_j dxs[inv_pos[t*k + j]] + sum_e dlogits[t, e] * wr[e]) in fp32 (dlogits NULL: expert part
- * only); dxs (M, d) bf16 or fp32 (dxs_dtype). */
+ * only); dxs (M, d) bf16 or fp32 (dxs_dtype); slots with a negative inv_pos add nothing. */
 int hmoe_unpermute_bwd(const void* dxs, int dxs_dtype, const int32_t* inv_pos, const float* dlogits, const void* wr,
                        int64_t T, int k, int64_t d, int E, void* dx, hmoe_stream_t stream);
 

@@ -79,3 +79,29 @@ def poziomka_forward(x, gate_w, expert_bias, wgu, wgu_s, wd, wd_s, shared_g, sha
     lin = lambda a, m: F.linear(a, m.to(a.dtype))  # noqa: E731
     shared = lin(F.silu(lin(x, shared_g)) * lin(x, shared_u), shared_d)
     return out.to(x.dtype) + shared
+
+
+def router_routed(x, wr, ids, bias=None, renorm=True, scaling=1.0):
+    """router() with the expert choice given (ids (T, k)): the same fp32 logits and softmax, the weights gathered at
+    ids instead of torch.topk's picks.  Where the two agree on the ids this is router() exactly; it keeps a near tie
+    that torch's GEMM order would break differently from routing the reference path onto other experts."""
+    logits = F.linear(x.float(), wr.float())
+    if bias is not None:
+        logits = logits + bias.float()
+    w = logits.softmax(-1).gather(1, ids.long())
+    if renorm:
+        w = w / (w.sum(-1, keepdim=True) + 1e-20) * scaling
+    else:
+        w = w * scaling
+    return logits, w
+
+
+def training_step_routed(x, wr, wgu, wd, ids, dout, bias=None, renorm=True):
+    """training_step() on given routing ids: the reference's bf16 CPU path (router weights, grouped GEMMs, two-rounding
+    weight multiply, un-permute sum) differentiated by autograd.  Used as the yardstick of the backward tolerance: the
+    error of this path against the float64 oracle is what the reference's own arithmetic achieves on the same
+    inputs."""
+    _, w = router_routed(x, wr, ids, bias, renorm)
+    out = fused_moe_grouped(x, ids.long(), w, wgu, wd)
+    out.backward(dout)
+    return out

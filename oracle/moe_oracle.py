@@ -267,8 +267,12 @@ def grouped_mm(a, w, counts, a_idx=None, y_idx=None, scale=None, w_scale=None, r
 
 
 def silu64(g):
+    """silu(g) = g / (1 + exp(-g)) in float64, except below g = -ln(FLT_MAX) = -88.7228: there torch's fp32 silu (the
+    opmath of a bf16 tensor) overflows exp(-g) and returns -0, where float64 would give a tiny normal number."""
     g = np.asarray(g, dtype=np.float64)
-    return g / (1.0 + np.exp(-g))
+    with np.errstate(over="ignore"):
+        s = g / (1.0 + np.exp(-g))
+    return np.where(g < -88.72283935546875, -0.0, s)
 
 
 def swiglu_fwd(gb, ub):

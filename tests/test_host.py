@@ -312,3 +312,61 @@ def test_poziomka_expert_bias_keeps_its_precision(tmp_path):
     got = load_export(str(tmp_path))[1]
     assert got.gate.expert_bias.dtype == torch.float32 and torch.equal(got.gate.expert_bias, bias)
     assert got.gate.weight.dtype == torch.bfloat16 and got._wgu_s.dtype == torch.bfloat16
+
+
+def _reference_rule(prefix, name, p):
+    """The group the reference's param_groups gives a parameter (train.py:314-325): the token embedding, 2-D matrices
+    under `.blocks.` of the text encoder or the denoiser ("hidden": Muon), other 2-D matrices ("proj": AdamW with
+    weight decay), everything else ("other": AdamW without)."""
+    full = f"{prefix}.{name}"
+    if full == "te.token_embedding.weight":
+        return "emb"
+    if prefix in ("te", "den") and ".blocks." in f".{name}" and p.ndim == 2 and not name.endswith("mod_table"):
+        return "hidden"
+    if p.ndim == 2 and not name.endswith("mod_table"):
+        return "proj"
+    return "other"
+
+
+def test_moe_param_groups_against_the_reference_rule():
+    """A denoiser-like module whose block MLP is a MoESwiGLU: under the reference's grouping rule alone the router
+    would go to Muon ("hidden") and the expert stacks to AdamW's "other" group (no weight decay); with
+    moe_param_groups the stacks get the hidden learning rate and weight decay, the router its own AdamW group, and
+    filtering the returned ids leaves no MoE parameter for the rule (so none is in two groups), while the block's
+    other matrices still go to Muon."""
+    from trenowanie_generatora_obrazkow_amd import moe_param_groups
+
+    class Block(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.attn = nn.Linear(64, 64, bias=False)
+            self.norm = nn.LayerNorm(64)
+            self.mlp = MoESwiGLU(64, 96, experts=4, top_k=2, device="cpu")
+
+    class Den(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.patch_in = nn.Linear(16, 64)
+            self.blocks = nn.ModuleList([Block(), Block()])
+
+    den = Den()
+    named = [("den", n, p) for n, p in den.named_parameters()]
+    before = {n: _reference_rule(pre, n, p) for pre, n, p in named}
+    assert before["blocks.0.mlp.router_weight"] == "hidden"
+    assert before["blocks.0.mlp.w_gu"] == "other" and before["blocks.1.mlp.w_d"] == "other"
+
+    groups, ids = moe_param_groups(den, lr=0.02, weight_decay=0.1, router_lr=1e-3)
+    by_name = {g["name"]: g for g in groups}
+    ex, rt = by_name["moe_experts"], by_name["moe_router"]
+    mlps = [b.mlp for b in den.blocks]
+    assert [id(p) for p in ex["params"]] == [id(p) for m in mlps for p in (m.w_gu, m.w_d)]
+    assert [id(p) for p in rt["params"]] == [id(m.router_weight) for m in mlps]
+    assert ex["lr"] == ex["base_lr"] == 0.02 and ex["weight_decay"] == 0.1
+    assert rt["lr"] == 1e-3 and rt["weight_decay"] == 0.0
+    rest = [(pre, n, p) for pre, n, p in named if id(p) not in ids]
+    after = {n: _reference_rule(pre, n, p) for pre, n, p in rest}
+    assert not any(".mlp." in n for n in after)
+    assert after["blocks.0.attn.weight"] == "hidden" and after["patch_in.weight"] == "proj"
+    assert len(rest) + len(ids) == len(named)
+    # the groups build an optimizer as they are
+    torch.optim.AdamW(groups, betas=(0.9, 0.95))

@@ -9,6 +9,6 @@
   ops         -- tensor-level wrappers of every C entry point
 """
 from . import _lib  # noqa: F401
-from .layer import MoESwiGLU, moe_swiglu  # noqa: F401
+from .layer import MoESwiGLU, moe_param_groups, moe_swiglu  # noqa: F401
 
-__all__ = ["MoESwiGLU", "moe_swiglu"]
+__all__ = ["MoESwiGLU", "moe_swiglu", "moe_param_groups"]

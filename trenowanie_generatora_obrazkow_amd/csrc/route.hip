@@ -572,8 +572,13 @@ __global__ __launch_bounds__(kSgThreads) void route_sigmoid_kernel(const uint16_
 constexpr int kFPB = 256;        // flat rows per histogram block (one wave each: 128 waves at M = 32768)
 constexpr int kMaxEDispatch = 1024;
 
+// an int64 id outside the int32 range becomes -1 (invalid) rather than wrapping onto a valid expert
 __device__ __forceinline__ int load_id(const void* ids, int is64, int64_t f) {
-  return is64 ? (int)reinterpret_cast<const int64_t*>(ids)[f] : reinterpret_cast<const int32_t*>(ids)[f];
+  if (is64) {
+    const int64_t v = reinterpret_cast<const int64_t*>(ids)[f];
+    return (v < 0 || v > INT32_MAX) ? -1 : (int)v;
+  }
+  return reinterpret_cast<const int32_t*>(ids)[f];
 }
 
 __global__ __launch_bounds__(64) void dispatch_hist_kernel(const void* __restrict__ ids, int ids64, int64_t M, int E,
@@ -626,11 +631,13 @@ __global__ __launch_bounds__(64) void dispatch_hist_kernel(const void* __restric
 // [g * C, (g + 1) * C) of expert e (C = ceil(nblk / G)): it sums them, the group sums are scanned per expert, the
 // totals are scanned over the experts by wave prefix sums, and each thread then rewrites its blocks' counts as
 // running first rows.  All integer, so the order of the sums does not matter.
+// n_invalid (optional): M minus the rows counted, i.e. the flat rows whose id lies outside [0, E).
 __global__ __launch_bounds__(1024) void dispatch_scan_kernel(int32_t* __restrict__ hist, int nblk, int E,
                                                              int32_t* __restrict__ counts,
                                                              int64_t* __restrict__ counts64,
                                                              int32_t* __restrict__ starts,
-                                                             int32_t* __restrict__ gstart) {
+                                                             int32_t* __restrict__ gstart, int64_t M,
+                                                             int32_t* __restrict__ n_invalid) {
   __shared__ int part[1024];              // [G][E] group sums, then their exclusive prefix per expert
   __shared__ int tot[kMaxEDispatch + 1];  // totals, then exclusive starts
   __shared__ int wsum[16], gsum[16];
@@ -709,6 +716,7 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(int32_t* __restrict
     }
     starts[E] = all;
     if (gstart) gstart[E] = gall;
+    if (n_invalid) n_invalid[0] = (int32_t)(M - all);
   }
   __syncthreads();
   if (mine) {
@@ -865,10 +873,13 @@ __global__ __launch_bounds__(256) void make_schedule_kernel(const void* __restri
 // computed in fp32 and rounded once, as torch adds two bf16 tensors)
 // out[t] = bf16(sum_j y[t*k + j]) (+ add[t], rounded again), one thread per 8 columns of a token.  KT > 0 is the
 // slot count at compile time: the thread issues its KT row loads before the first sum (KT = 0: a runtime loop).
-// Either way the slots are summed in order j = 0, 1, ..., so the result does not depend on KT.
+// Either way the slots are summed in order j = 0, 1, ..., so the result does not depend on KT.  With inv_pos, a slot
+// whose inv_pos is negative (an expert id outside [0, E): no GEMM wrote its row of y) is read as zeros.
 template <int KT>
-__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ y, int64_t T, int k, int64_t d,
-                                                      const uint16_t* __restrict__ add, uint16_t* __restrict__ out) {
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ y,
+                                                      const int32_t* __restrict__ inv_pos, int64_t T, int k,
+                                                      int64_t d, const uint16_t* __restrict__ add,
+                                                      uint16_t* __restrict__ out) {
   const int64_t nvec = d / 8;
   const int64_t total = T * nvec;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
@@ -892,16 +903,19 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
       }
     };
     const uint4 a = add ? reinterpret_cast<const uint4*>(add + t * d)[c] : make_uint4(0, 0, 0, 0);
+    auto row = [&](int j) {
+      return (inv_pos && inv_pos[t * k + j] < 0) ? make_uint4(0, 0, 0, 0) : src[j * nvec];
+    };
     if constexpr (KT > 0) {
       uint4 v[KT];
 #pragma unroll
-      for (int j = 0; j < KT; ++j) v[j] = src[j * nvec];
+      for (int j = 0; j < KT; ++j) v[j] = row(j);
       first(v[0]);
 #pragma unroll
       for (int j = 1; j < KT; ++j) accum(v[j]);
     } else {
-      first(src[0]);
-      for (int j = 1; j < k; ++j) accum(src[j * nvec]);
+      first(row(0));
+      for (int j = 1; j < k; ++j) accum(row(j));
     }
     uint4 o;
     o.x = pack_bf2(s[0], s[1]);
@@ -1331,6 +1345,7 @@ __global__ __launch_bounds__(256) void unpermute_bwd_kernel(const void* __restri
         const int64_t t = t0 + u;
         if (t >= T || !active) continue;
         const int64_t r = inv_pos[t * k + j];
+        if (r < 0) continue;  // an expert id outside [0, E): no sorted row, no gradient
         if constexpr (F32) {
           const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(dxs) + r * d + col);
           const float4 v0 = src[0], v1 = src[1];
@@ -1397,10 +1412,11 @@ static inline int grid_for(int64_t work, int per_block, int cap = 8192) {
 
 static inline bool al16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-static void combine_launch(const uint16_t* y, int64_t T, int k, int64_t d, const uint16_t* add, uint16_t* out,
-                           int64_t work, hipStream_t s) {
+static void combine_launch(const uint16_t* y, const int32_t* inv_pos, int64_t T, int k, int64_t d,
+                           const uint16_t* add, uint16_t* out, int64_t work, hipStream_t s) {
   const dim3 grid(grid_for(work, 256, 65536));
-#define HMOE_COMBINE(KT) hipLaunchKernelGGL((combine_kernel<KT>), grid, dim3(256), 0, s, y, T, k, d, add, out)
+#define HMOE_COMBINE(KT) \
+  hipLaunchKernelGGL((combine_kernel<KT>), grid, dim3(256), 0, s, y, inv_pos, T, k, d, add, out)
   switch (k) {
     case 1: HMOE_COMBINE(1); break;
     case 2: HMOE_COMBINE(2); break;
@@ -1495,7 +1511,8 @@ static size_t dispatch_ws_bytes(int64_t T, int k, int E) {
 static int dispatch_impl(const void* topk_ids, int ids_dtype, const void* topk_w, int w_dtype, int64_t T, int k, int E,
                          const void* x, int64_t ldx, int64_t d, void* xs, void* xs_tiles, int32_t* counts,
                          int64_t* counts64, int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos,
-                         uint16_t* w_sorted, void* workspace, size_t workspace_bytes, hipStream_t s) {
+                         uint16_t* w_sorted, int32_t* n_invalid, void* workspace, size_t workspace_bytes,
+                         hipStream_t s) {
   if (T < 0 || k <= 0 || E <= 0) return HMOE_ERR_ARG;
   if (E > kMaxEDispatch || k > kMaxK) return HMOE_ERR_SHAPE;
   if (!counts || !starts) return HMOE_ERR_ARG;
@@ -1525,7 +1542,7 @@ static int dispatch_impl(const void* topk_ids, int ids_dtype, const void* topk_w
     HMOE_CHECK_LAUNCH();
   }
   hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, s, hist, (int)nblk, E, counts, counts64, starts,
-                     gstart);
+                     gstart, M, n_invalid);
   HMOE_CHECK_LAUNCH();
   if (M > 0 && (xs || xs_tiles)) {
     const int grid = grid_for(T, 4, 8192);
@@ -1638,9 +1655,9 @@ size_t hmoe_dispatch_workspace_size(int64_t T, int k, int E) { return dispatch_w
 int hmoe_dispatch(const void* topk_ids, int ids_dtype, const void* topk_w, int w_dtype, int64_t T, int k, int E,
                   const void* x, int64_t ldx, int64_t d, void* xs, int32_t* counts, int64_t* counts64,
                   int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos, uint16_t* w_sorted,
-                  void* workspace, size_t workspace_bytes, hmoe_stream_t stream) {
+                  int32_t* n_invalid, void* workspace, size_t workspace_bytes, hmoe_stream_t stream) {
   return dispatch_impl(topk_ids, ids_dtype, topk_w, w_dtype, T, k, E, x, ldx, d, xs, nullptr, counts, counts64, starts,
-                       order, a_idx, inv_pos, w_sorted, workspace, workspace_bytes,
+                       order, a_idx, inv_pos, w_sorted, n_invalid, workspace, workspace_bytes,
                        reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -1651,16 +1668,17 @@ size_t hmoe_xs_tiles_bytes(int64_t M, int E, int64_t d) {
 int hmoe_dispatch_tiles(const void* topk_ids, int ids_dtype, const void* topk_w, int w_dtype, int64_t T, int k, int E,
                         const void* x, int64_t ldx, int64_t d, void* xs, void* xs_tiles, int32_t* counts,
                         int64_t* counts64, int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos,
-                        uint16_t* w_sorted, void* workspace, size_t workspace_bytes, hmoe_stream_t stream) {
+                        uint16_t* w_sorted, int32_t* n_invalid, void* workspace, size_t workspace_bytes,
+                        hmoe_stream_t stream) {
   return dispatch_impl(topk_ids, ids_dtype, topk_w, w_dtype, T, k, E, x, ldx, d, xs, xs_tiles, counts, counts64,
-                       starts, order, a_idx, inv_pos, w_sorted, workspace, workspace_bytes,
+                       starts, order, a_idx, inv_pos, w_sorted, n_invalid, workspace, workspace_bytes,
                        reinterpret_cast<hipStream_t>(stream));
 }
 
 int hmoe_dispatch_noalloc(const void* topk_ids, int ids_dtype, const void* topk_w, int w_dtype, int64_t T, int k,
                           int E, const void* x, int64_t ldx, int64_t d, void* xs, int32_t* counts, int64_t* counts64,
                           int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos, uint16_t* w_sorted,
-                          hmoe_stream_t stream) {
+                          int32_t* n_invalid, hmoe_stream_t stream) {
   if (T < 0 || k <= 0 || E <= 0) return HMOE_ERR_ARG;
   if (E > kMaxEDispatch || k > kMaxK) return HMOE_ERR_SHAPE;
   if (T > INT32_MAX / k || dispatch_ws_bytes(T, k, E) > kDispatchScratchBytes) return HMOE_ERR_TOO_LARGE;
@@ -1668,7 +1686,8 @@ int hmoe_dispatch_noalloc(const void* topk_ids, int ids_dtype, const void* topk_
   void* ws = dispatch_scratch(&rc);
   if (rc) return rc;
   return dispatch_impl(topk_ids, ids_dtype, topk_w, w_dtype, T, k, E, x, ldx, d, xs, nullptr, counts, counts64, starts,
-                       order, a_idx, inv_pos, w_sorted, ws, kDispatchScratchBytes, reinterpret_cast<hipStream_t>(stream));
+                       order, a_idx, inv_pos, w_sorted, n_invalid, ws, kDispatchScratchBytes,
+                       reinterpret_cast<hipStream_t>(stream));
 }
 
 int hmoe_make_schedule(const void* counts, int counts_dtype, int E, int64_t M, int block_m, int32_t* block_e,
@@ -1684,24 +1703,26 @@ int hmoe_make_schedule(const void* counts, int counts_dtype, int E, int64_t M, i
   return HMOE_OK;
 }
 
-int hmoe_combine(const void* y, int64_t T, int k, int64_t d, void* out, hmoe_stream_t stream) {
+int hmoe_combine(const void* y, const int32_t* inv_pos, int64_t T, int k, int64_t d, void* out,
+                 hmoe_stream_t stream) {
   if (T < 0 || k <= 0 || d <= 0) return HMOE_ERR_ARG;
   if (T == 0) return HMOE_OK;
   if (!y || !out || d % 8 || !al16(y) || !al16(out)) return HMOE_ERR_ARG;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int64_t work = T * (d / 8);
-  combine_launch(static_cast<const uint16_t*>(y), T, k, d, nullptr, static_cast<uint16_t*>(out), work, s);
+  combine_launch(static_cast<const uint16_t*>(y), inv_pos, T, k, d, nullptr, static_cast<uint16_t*>(out), work, s);
   HMOE_CHECK_LAUNCH();
   return HMOE_OK;
 }
 
-int hmoe_combine_add(const void* y, int64_t T, int k, int64_t d, const void* add, void* out, hmoe_stream_t stream) {
+int hmoe_combine_add(const void* y, const int32_t* inv_pos, int64_t T, int k, int64_t d, const void* add, void* out,
+                     hmoe_stream_t stream) {
   if (T < 0 || k <= 0 || d <= 0) return HMOE_ERR_ARG;
   if (T == 0) return HMOE_OK;
   if (!y || !add || !out || d % 8 || !al16(y) || !al16(add) || !al16(out)) return HMOE_ERR_ARG;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int64_t work = T * (d / 8);
-  combine_launch(static_cast<const uint16_t*>(y), T, k, d, static_cast<const uint16_t*>(add),
+  combine_launch(static_cast<const uint16_t*>(y), inv_pos, T, k, d, static_cast<const uint16_t*>(add),
                  static_cast<uint16_t*>(out), work, s);
   HMOE_CHECK_LAUNCH();
   return HMOE_OK;

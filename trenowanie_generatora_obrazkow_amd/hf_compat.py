@@ -18,7 +18,9 @@ def _fused_moe_infer(self, x, topk_ids, topk_weight):
     """aurora/hf_compat.py:63-82 (the fused branch): stable sort of the flat routed rows by expert, gate/up GEMM
     over gathered token rows with the SwiGLU fused into its epilogue, down GEMM scaled by the bf16-rounded routing
     weight and scattered back to (token, slot) order, sum over the k slots.  Layers fused with quant="int8" run the
-    int8-weight forms of the two GEMMs (per-column scales applied to the fp32 sums)."""
+    int8-weight forms of the two GEMMs (per-column scales applied to the fp32 sums).  An expert id outside [0, E)
+    in topk_ids routes its slot nowhere: the slot adds nothing to the output, and the count of such ids is kept on
+    the device in self._n_invalid (read by invalid_expert_ids, which is the only place that synchronises)."""
     n, k = topk_ids.shape
     E = self._wgu.shape[0]
     if self._mode is None:  # decided on the device the weights ended up on
@@ -27,10 +29,23 @@ def _fused_moe_infer(self, x, topk_ids, topk_weight):
         raise NotImplementedError("the hmoe SwiGLU epilogue implements silu(g) * u only")
     x = x.contiguous()
     disp, act, _ = ops.routed_gate_up(x, topk_ids.contiguous(), E, self._wgu, topk_w=topk_weight.contiguous(),
-                                      wgu_s=self._wgu_s, want_inv=False)
+                                      wgu_s=self._wgu_s, want_inv=True)
     M = n * k
     y, _ = ops.down_scatter(act, self._wd, disp.counts, M, disp.w_sorted, disp.order, wd_s=self._wd_s)
-    return ops.combine(y, n, k)
+    self._n_invalid = disp.n_invalid
+    return ops.combine(y, n, k, inv_pos=disp.inv_pos)
+
+
+def invalid_expert_ids(model) -> int:
+    """Expert ids outside [0, E) seen by the last moe_infer call of every fused block of `model` (one host sync).
+    The fused path gives such a slot no contribution instead of reading unwritten memory; this tells the caller that
+    its gate produced them."""
+    total = 0
+    for mod in model.modules():
+        n = getattr(mod, "_n_invalid", None)
+        if isinstance(n, torch.Tensor):
+            total += int(n.item())
+    return total
 
 
 def _dequant(w, scale, dtype):
@@ -81,7 +96,9 @@ def fuse_moe(model, quant=""):
         experts = getattr(mod, "experts", None)
         if experts is None or not hasattr(mod, "moe_infer") or not isinstance(experts, torch.nn.ModuleList):
             continue
-        # (E, in, out) contiguous: wgu = [gate | up] along out, wd = down; buffers, so .to() moves them
+        # stacked per-expert weights, (E, in, out) and contiguous: wgu holds the gate then the up projection along
+        # its last axis, wd the down projection; registered as non-persistent buffers so that moving the module to a
+        # device or dtype carries them along
         wgu = torch.stack([torch.cat([e.gate_proj.weight, e.up_proj.weight]).t() for e in experts]).contiguous()
         wd = torch.stack([e.down_proj.weight.t() for e in experts]).contiguous()
         for name, w in (("_wgu", wgu), ("_wd", wd)):
@@ -93,7 +110,7 @@ def fuse_moe(model, quant=""):
         mod._mode = None
         mod.moe_infer = types.MethodType(_fused_moe_infer, mod)
         del mod.experts
-        mod.experts = list(range(mod._wgu.shape[0]))  # len(self.experts) still works for any remaining code
+        mod.experts = list(range(mod._wgu.shape[0]))  # the expert count stays available as len(mod.experts)
         n += 1
     if torch.cuda.is_available():
         torch.cuda.empty_cache()

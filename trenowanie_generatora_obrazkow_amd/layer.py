@@ -192,3 +192,29 @@ class MoESwiGLU(nn.Module):
         self.last_topk_ids, self.last_topk_weight = ids, tw
         out = out.view(shape)
         return out if out.dtype == out_dtype else out.to(out_dtype)
+
+
+def moe_param_groups(module: nn.Module, lr: float, weight_decay: float, router_lr: float | None = None):
+    """Optimizer groups for every MoESwiGLU inside `module`, for a training script whose grouping rule sends 2-D
+    matrices under `.blocks.` to Muon and everything else to AdamW (train.py:305-338 of the reference).  Left to that
+    rule, a MoESwiGLU standing in for a block's dense SwiGLU would have its router (E, dim), a 2-D matrix, updated by
+    Muon and its 3-D expert stacks w_gu / w_d put in the AdamW "other" group (no weight decay, the Adam learning
+    rate), while the dense in_proj / out_proj they replace were Muon's hidden matrices.
+
+    Returns (groups, ids).  groups: AdamW parameter groups (`params`, `lr`, `base_lr`, `weight_decay`, `name`):
+      - "moe_experts": every w_gu and w_d, at `lr` (the hidden-matrix learning rate) with `weight_decay`;
+      - "moe_router": every router_weight, at `router_lr` (default `lr`) without weight decay, kept out of Muon (an
+        orthogonalised update would mix the experts' logit directions).
+    ids: the id() of each parameter placed, to remove from the list the script's own rule groups (its `named=`
+    argument), so that no parameter is in two groups."""
+    experts, routers = [], []
+    for m in module.modules():
+        if isinstance(m, MoESwiGLU):
+            experts += [p for p in (m.w_gu, m.w_d) if p.requires_grad]
+            if m.router_weight.requires_grad:
+                routers.append(m.router_weight)
+    rlr = lr if router_lr is None else router_lr
+    groups = [dict(params=experts, lr=lr, base_lr=lr, weight_decay=weight_decay, name="moe_experts"),
+              dict(params=routers, lr=rlr, base_lr=rlr, weight_decay=0.0, name="moe_router")]
+    groups = [g for g in groups if g["params"]]
+    return groups, {id(p) for g in groups for p in g["params"]}

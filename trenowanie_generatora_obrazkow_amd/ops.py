@@ -147,13 +147,15 @@ class Dispatch:
     w_sorted: torch.Tensor  # (M,) bf16 or None
     xs: torch.Tensor  # (M, d) bf16 or None
     xs_tiles: torch.Tensor = None  # the sorted rows as row-group tiles (bf16 storage) or None
+    n_invalid: torch.Tensor = None  # (1,) int32 on the device: flat rows whose expert id lies outside [0, E)
 
 
 def dispatch(topk_ids: torch.Tensor, E: int, topk_w=None, x=None, want_counts64=False, want_inv=True,
              want_xs=True, want_tiles=False) -> Dispatch:
     """Stable counting sort of the flat routed rows (aurora/hf_compat.py:69-72, 78, 80) and optionally, with x, the
     row permutation xs = x[a_idx] (want_xs) and the same rows as row-group tiles for gate_up_swiglu_tiles
-    (want_tiles)."""
+    (want_tiles).  Expert ids outside [0, E) route nowhere (inv_pos -1, counted in no expert); their number is left
+    on the device in n_invalid, read without a host sync only when the caller asks."""
     T, k = topk_ids.shape
     M = T * k
     dev = topk_ids.device
@@ -172,6 +174,7 @@ def dispatch(topk_ids: torch.Tensor, E: int, topk_w=None, x=None, want_counts64=
     a_idx = torch.empty(M, device=dev, dtype=torch.int32)
     inv = torch.empty(M, device=dev, dtype=torch.int32) if want_inv else None
     w_sorted = torch.empty(M, device=dev, dtype=torch.bfloat16) if topk_w is not None else None
+    n_invalid = torch.empty(1, device=dev, dtype=torch.int32)
     xs = tiles = None
     d = 0
     ldx = 0
@@ -188,8 +191,8 @@ def dispatch(topk_ids: torch.Tensor, E: int, topk_w=None, x=None, want_counts64=
     with _Probe("dispatch"):
         L.call("hmoe_dispatch_tiles", L.ptr(ids), L.dt(ids), L.ptr(topk_w), L.dt(topk_w) if topk_w is not None else 0,
                T, k, E, L.ptr(x), ldx, d, L.ptr(xs), L.ptr(tiles), L.ptr(counts), L.ptr(counts64), L.ptr(starts),
-               L.ptr(order), L.ptr(a_idx), L.ptr(inv), L.ptr(w_sorted), L.ptr(ws), ws_bytes, s)
-    return Dispatch(counts, counts64, starts, order, a_idx, inv, w_sorted, xs, tiles)
+               L.ptr(order), L.ptr(a_idx), L.ptr(inv), L.ptr(w_sorted), L.ptr(n_invalid), L.ptr(ws), ws_bytes, s)
+    return Dispatch(counts, counts64, starts, order, a_idx, inv, w_sorted, xs, tiles, n_invalid)
 
 
 def make_schedule(counts: torch.Tensor, M: int, block_m: int = 64):
@@ -364,19 +367,21 @@ def down_scatter(act, wd, counts, M, w_sorted, y_idx, keep_yhat=False, wd_s=None
     return y, yhat
 
 
-def combine(y, T, k, add=None):
-    """out[t] = bf16(sum_j y[t*k + j]) (+ add[t], rounded once more: bf16 + bf16)."""
+def combine(y, T, k, add=None, inv_pos=None):
+    """out[t] = bf16(sum_j y[t*k + j]) (+ add[t], rounded once more: bf16 + bf16).  inv_pos (T*k,) from the dispatch:
+    slots routed nowhere (inv_pos < 0: an expert id outside [0, E)) add zeros instead of their unwritten rows."""
     d = y.shape[1]
     _need(y, "y", (T * k, d), _BF16)
+    inv_pos = _rows_index(inv_pos, "inv_pos", T * k)
     out = torch.empty(T, d, device=y.device, dtype=y.dtype)
     with _Probe("combine"):
         if add is None:
-            L.call("hmoe_combine", L.ptr(_contig(y, "y")), T, k, d, L.ptr(out), _dev_stream(y))
+            L.call("hmoe_combine", L.ptr(_contig(y, "y")), L.ptr(inv_pos), T, k, d, L.ptr(out), _dev_stream(y))
         else:
             if add.shape != (T, d) or add.dtype != torch.bfloat16:
                 raise ValueError(f"add must be bf16 of shape {(T, d)}")
-            L.call("hmoe_combine_add", L.ptr(_contig(y, "y")), T, k, d, L.ptr(_contig(add, "add")), L.ptr(out),
-                   _dev_stream(y))
+            L.call("hmoe_combine_add", L.ptr(_contig(y, "y")), L.ptr(inv_pos), T, k, d, L.ptr(_contig(add, "add")),
+                   L.ptr(out), _dev_stream(y))
     return out
 
 
