@@ -11,8 +11,13 @@
  *   - sorted row r: rows grouped by expert in expert order, stable in f (argsort(stable=True), :71);
  *     order[r] = f, a_idx[r] = f / k, y_idx[r] = f (:78), inv_pos[f] = r;
  *   - stacked expert weights wgu (E, d, 2h) = [gate | up] and wd (E, h, d), N contiguous (:154-155);
- *   - bf16 storage, fp32 accumulation, one rounding on store; the routing weight is rounded to bf16 before use
- *     (:80) and applied to the fp32 accumulator (aurora/moe_triton.py:52-56).
+ *   - 16-bit storage, fp32 accumulation, one rounding on store; the routing weight is rounded to the activations'
+ *     type before use (:80) and applied to the fp32 accumulator (aurora/moe_triton.py:52-56).
+ * Activation types: the forward entry points (dispatch, the gate/up and down projections, grouped_mm, combine) take
+ * bf16 or fp16 activations, selected by a `dtype` argument (HMOE_DT_BF16 / HMOE_DT_F16) that also types their 16-bit
+ * weights, 16-bit row scales and outputs -- the reference's grouped_mm returns a.dtype for any floating input
+ * (aurora/moe_triton.py:80) and its LM loader takes a dtype (aurora/hf_compat.py:42).  fp16 runs on
+ * v_mfma_f32_32x32x16_f16 with fp16 rounding points in place of bf16 ones.  The routers and the backward are bf16.
  * Row offsets are 64-bit.  Index arrays (a_idx, y_idx, ...) are trusted to be in range.
  */
 #ifndef HMOE_H_
@@ -87,7 +92,8 @@ size_t hmoe_dispatch_workspace_size(int64_t T, int k, int E);
  * Outputs (NULL skips an optional one): counts (E,) int32 [required], counts64 (E,) int64, starts (E+1,) int32
  * [required; starts[e] = first sorted row of expert e], order (M,) int32 (= y_idx), a_idx (M,) int32,
  * inv_pos (M,) int32, w_sorted (M,) bf16, xs (M, d) bf16 = x[a_idx] (needs x (T, d) bf16 with row stride ldx),
- * n_invalid (1,) int32.
+ * n_invalid (1,) int32.  dtype: the 16-bit type of x / xs and of w_sorted (topk_w, fp32, bf16 or fp16, is rounded
+ * to it).
  * Expert ids outside [0, E) route nowhere: their flat rows are counted in no expert and get inv_pos = -1, the
  * Sigma counts sorted rows hold the valid ones (the sorted rows past that are not written), and n_invalid receives
  * how many there are (on the device, no host sync: the caller reads it when it chooses).  hmoe_combine with inv_pos
@@ -97,7 +103,7 @@ size_t hmoe_dispatch_workspace_size(int64_t T, int k, int E);
 int hmoe_dispatch(const void* topk_ids, int ids_dtype, const void* topk_w, int w_dtype, int64_t T, int k, int E,
                   const void* x, int64_t ldx, int64_t d, void* xs, int32_t* counts, int64_t* counts64,
                   int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos, uint16_t* w_sorted,
-                  int32_t* n_invalid, void* workspace, size_t workspace_bytes, hmoe_stream_t stream);
+                  int32_t* n_invalid, void* workspace, size_t workspace_bytes, int dtype, hmoe_stream_t stream);
 
 /* Bytes of the row-group tiles (xs_tiles) for M sorted rows of width d over E experts (an upper bound: it does not
  * depend on the counts).  0 for invalid sizes. */
@@ -113,7 +119,7 @@ size_t hmoe_xs_tiles_bytes(int64_t M, int E, int64_t d);
 int hmoe_dispatch_tiles(const void* topk_ids, int ids_dtype, const void* topk_w, int w_dtype, int64_t T, int k, int E,
                         const void* x, int64_t ldx, int64_t d, void* xs, void* xs_tiles, int32_t* counts,
                         int64_t* counts64, int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos,
-                        uint16_t* w_sorted, int32_t* n_invalid, void* workspace, size_t workspace_bytes,
+                        uint16_t* w_sorted, int32_t* n_invalid, void* workspace, size_t workspace_bytes, int dtype,
                         hmoe_stream_t stream);
 
 /* Allocation-free form of hmoe_dispatch.  No counterpart in the reference: it is for callers that cannot allocate
@@ -127,7 +133,7 @@ int hmoe_dispatch_tiles(const void* topk_ids, int ids_dtype, const void* topk_w,
 int hmoe_dispatch_noalloc(const void* topk_ids, int ids_dtype, const void* topk_w, int w_dtype, int64_t T, int k,
                           int E, const void* x, int64_t ldx, int64_t d, void* xs, int32_t* counts, int64_t* counts64,
                           int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos, uint16_t* w_sorted,
-                          int32_t* n_invalid, hmoe_stream_t stream);
+                          int32_t* n_invalid, int dtype, hmoe_stream_t stream);
 
 /* make_schedule: replaces aurora/moe_triton.py:93-107.  For each of the ceil(M / block_m) + E blocks: the expert
  * (or -1), the first sorted row and the end row of that expert, int32, computed on the device from counts
@@ -141,10 +147,11 @@ int hmoe_make_schedule(const void* counts, int counts_dtype, int E, int64_t M, i
 
 /* grouped_mm: replaces aurora/moe_triton.py:65-90 (_grouped_kernel :22-56).
  * y[y_idx[r] or r, :] = bf16((a[a_idx[r] or r, :] @ w[e(r)]) * w_scale[e, :] * scale[r]) for the M sorted rows r,
- * e(r) the expert owning row r under counts, the two scale products in that order on the fp32 sum.  a bf16 (rows of
- * lda elements), w (E, K, N) with element strides (stride_we, stride_wk, 1): bf16 (w_scale NULL) or int8
- * (HMOE_DT_I8, weight-only quantisation of aurora/moe_triton.py:44-51: w_scale (E, N) bf16 or fp32 required, N,
- * stride_wk and stride_we multiples of 16); scale (M,) bf16 or fp32 or NULL; y bf16 with row stride ldy.
+ * e(r) the expert owning row r under counts, the two scale products in that order on the fp32 sum.  a bf16 or fp16
+ * (a_dtype; rows of lda elements), w (E, K, N) with element strides (stride_we, stride_wk, 1): a's type (w_scale
+ * NULL) or int8 (HMOE_DT_I8, weight-only quantisation of aurora/moe_triton.py:44-51: w_scale (E, N) bf16 or fp32
+ * required, N, stride_wk and stride_we multiples of 16); scale (M,) fp32 or a's type, or NULL; y of a's type with
+ * row stride ldy.
  * K % 8 == 0, N % 8 == 0, lda/ldy/stride_wk % 8 == 0.  Rows of y not named by the schedule are not written. */
 int hmoe_grouped_mm(const void* a, int64_t lda, int a_dtype, const void* w, int w_dtype, int64_t E, int64_t K,
                     int64_t N, int64_t stride_we, int64_t stride_wk, const void* counts, int counts_dtype, int64_t M,
@@ -153,51 +160,55 @@ int hmoe_grouped_mm(const void* a, int64_t lda, int a_dtype, const void* w, int 
 
 /* Gate/up projection with the SwiGLU fused into the epilogue: replaces aurora/hf_compat.py:79 (grouped_mm(x,
  * _wgu, counts, sched, a_idx=a_idx).chunk(2)) and the self._act(g) * u of :81.
- * A rows: xs (M, d) in sorted order (a_idx NULL) or x (T, d) gathered through a_idx.  wgu (E, d, 2h) bf16.
- * act (M, h) bf16 = bf16(bf16(silu(g)) * u) with g, u the bf16-rounded gate / up outputs; gu (M, 2h) bf16 =
- * [g | u] when not NULL (kept for the backward).  d % 8 == 0, h % 8 == 0. */
+ * A rows: xs (M, d) in sorted order (a_idx NULL) or x (T, d) gathered through a_idx.  wgu (E, d, 2h).
+ * act (M, h) = R(R(silu(g)) * u) with g, u the rounded gate / up outputs, R the rounding to dtype (bf16 or fp16, the
+ * type of x, wgu, act and gu); gu (M, 2h) = [g | u] when not NULL (kept for the backward).  d % 8 == 0,
+ * h % 8 == 0. */
 int hmoe_gate_up_swiglu(const void* x, int64_t ldx, const int32_t* a_idx, const void* wgu, int64_t E, int64_t d,
-                        int64_t h, const void* counts, int counts_dtype, int64_t M, void* act, void* gu,
+                        int64_t h, const void* counts, int counts_dtype, int64_t M, void* act, void* gu, int dtype,
                         hmoe_stream_t stream);
 
 /* hmoe_gate_up_swiglu with the A rows taken from the row-group tiles of hmoe_dispatch_tiles (xs_tiles, written by
  * a dispatch with the same counts, d and M): the same products and sums, so act and gu are identical; the copies of
  * the GEMM then read 1 KB runs instead of 64-byte row pieces.  hmoe_xs_tiles_bytes(M, E, d) below 2^31. */
 int hmoe_gate_up_swiglu_tiles(const void* xs_tiles, const void* wgu, int64_t E, int64_t d, int64_t h,
-                              const void* counts, int counts_dtype, int64_t M, void* act, void* gu,
+                              const void* counts, int counts_dtype, int64_t M, void* act, void* gu, int dtype,
                               hmoe_stream_t stream);
 
 /* Down projection with routing weight and scatter: replaces aurora/hf_compat.py:80-81 (grouped_mm(act, _wd,
- * counts, sched, y_idx=y_idx, scale=w)).  y[y_idx[r]] = bf16(fp32(act[r] @ wd[e]) * w_sorted[r]); yhat (M, d) bf16
- * = bf16(act[r] @ wd[e]) in sorted order when not NULL (kept for the backward). */
+ * counts, sched, y_idx=y_idx, scale=w)).  y[y_idx[r]] = R(fp32(act[r] @ wd[e]) * w_sorted[r]); yhat (M, d)
+ * = R(act[r] @ wd[e]) in sorted order when not NULL (kept for the backward); act, wd, w_sorted, y and yhat of type
+ * dtype (bf16 or fp16), R the rounding to it. */
 int hmoe_down_scatter(const void* act, const void* wd, int64_t E, int64_t h, int64_t d, const void* counts,
                       int counts_dtype, int64_t M, const uint16_t* w_sorted, const int32_t* y_idx, void* y,
-                      void* yhat, hmoe_stream_t stream);
+                      void* yhat, int dtype, hmoe_stream_t stream);
 
 /* int8-weight forms of the two fused projections: replace aurora/hf_compat.py:79-80 on a layer fused with
  * quant="int8" (weights and scales from aurora/hf_compat.py:106-110, the kernel's int8 branch at
  * aurora/moe_triton.py:44-51).  wgu_q (E, d, 2h) int8 with scales wgu_s (E, 2h); wd_q (E, h, d) int8 with scales
  * wd_s (E, d); scales bf16 or fp32 (*_s_dtype).  Same outputs as hmoe_gate_up_swiglu / hmoe_down_scatter with the
- * per-column scale applied to the fp32 sum before any other step (inference only: no gu / yhat).  h % 16 == 0 and
- * d % 16 == 0. */
+ * per-column scale applied to the fp32 sum before any other step (inference only: no gu / yhat); activations,
+ * w_sorted and outputs of type dtype (bf16 or fp16; int8 widens exactly to either).  h % 16 == 0 and d % 16 == 0. */
 int hmoe_gate_up_swiglu_i8(const void* x, int64_t ldx, const int32_t* a_idx, const void* wgu_q, const void* wgu_s,
                            int wgu_s_dtype, int64_t E, int64_t d, int64_t h, const void* counts, int counts_dtype,
-                           int64_t M, void* act, hmoe_stream_t stream);
+                           int64_t M, void* act, int dtype, hmoe_stream_t stream);
 int hmoe_down_scatter_i8(const void* act, const void* wd_q, const void* wd_s, int wd_s_dtype, int64_t E, int64_t h,
                          int64_t d, const void* counts, int counts_dtype, int64_t M, const uint16_t* w_sorted,
-                         const int32_t* y_idx, void* y, hmoe_stream_t stream);
+                         const int32_t* y_idx, void* y, int dtype, hmoe_stream_t stream);
 
-/* Combine: replaces aurora/hf_compat.py:82 (y.view(n, k, -1).sum(1)): out[t] = bf16(sum_j fp32(y[t*k + j])).
+/* Combine: replaces aurora/hf_compat.py:82 (y.view(n, k, -1).sum(1)): out[t] = R(sum_j fp32(y[t*k + j])), y and
+ * out of type dtype (bf16 or fp16), R the rounding to it.
  * inv_pos (T * k,) int32 from the dispatch, or NULL: slots with a negative inv_pos (expert ids outside [0, E)) are
  * read as zeros instead of their (unwritten) row of y. */
-int hmoe_combine(const void* y, const int32_t* inv_pos, int64_t T, int k, int64_t d, void* out, hmoe_stream_t stream);
+int hmoe_combine(const void* y, const int32_t* inv_pos, int64_t T, int k, int64_t d, void* out, int dtype,
+                 hmoe_stream_t stream);
 
 /* Combine plus a per-token addend: replaces aurora/hf_pipeline.py:370 (out.to(x.dtype) + self.shared_experts(x)):
  * out[t] = bf16(bf16(sum_j fp32(y[t*k + j])) + add[t]), add (T, d) bf16 (the shared expert's output).  The
  * reference sums the slots with index_add_ in expert order (:369); here they are summed in slot order (the same
  * terms, fp32 accumulation). */
 int hmoe_combine_add(const void* y, const int32_t* inv_pos, int64_t T, int k, int64_t d, const void* add, void* out,
-                     hmoe_stream_t stream);
+                     int dtype, hmoe_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------------------------
  * Backward.  The reference has no backward for this path (aurora/hf_compat.py:62 is @torch.no_grad); each entry

@@ -3,7 +3,7 @@
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and only as the checker:
 the product package (trenowanie_generatora_obrazkow_amd) never imports it and has no CPU fallback.
 
-A numpy restatement (float64 arithmetic, with the reference's bf16 rounding points) of the path served by
+A numpy restatement (float64 arithmetic, with the reference's bf16 -- or fp16 -- rounding points) of the path served by
 aurora/moe_triton.py and aurora/hf_compat.py in the reference.  The router and the exact counting sort live in the C
 half of the oracle (oracle/router.c), loaded here through ctypes.
 
@@ -26,6 +26,9 @@ Pinning (what each function is checked against, in tests/test_oracle.py):
   moe_backward               torch float64 autograd of the forward and central finite differences on tiny shapes
   router_backward            torch float64 autograd of softmax -> gather -> renormalise
   quant_int8                 closed form: |q| <= 127, dequantised error <= scale / 2
+  round_f16 / dtype="f16"    fp16 rounding points (a model loaded in fp16): round_f16 vs a brute-force nearest-fp16
+                             search with ties to even; swiglu_fwd(dtype="f16") vs torch's fp16 F.silu(g) * u bit for
+                             bit; grouped_mm / moe_forward in fp16 vs the same per-token loop with fp16 rounding
 """
 from __future__ import annotations
 
@@ -75,6 +78,19 @@ def round_bf16(a) -> np.ndarray:
         out[nan] = np.nan
         return out
     return bf16_bits_to_f32(f32_to_bf16_bits(a.astype(np.float32)))
+
+
+def round_f16(a) -> np.ndarray:
+    """Round (float32 or float64) values to the nearest fp16 value (ties to even, overflow to inf), returned as
+    float32: numpy's float64 -> float16 conversion, one rounding from the exact value."""
+    return np.asarray(a, dtype=np.float64).astype(np.float16).astype(np.float32)
+
+
+def rounder(dtype: str):
+    """The rounding of an activation type: "bf16" (round_bf16) or "f16" (round_f16)."""
+    if dtype not in ("bf16", "f16"):
+        raise ValueError(dtype)
+    return round_bf16 if dtype == "bf16" else round_f16
 
 
 # ----------------------------------------------------------------------------------------------------------------
@@ -241,10 +257,11 @@ def make_schedule_c(counts, M, block_m=BLOCK_M):
 # rounding on store) -- restated with float64 accumulation; the fp32-vs-fp64 accumulation gap is what the tests'
 # tolerance covers.
 # ----------------------------------------------------------------------------------------------------------------
-def grouped_mm(a, w, counts, a_idx=None, y_idx=None, scale=None, w_scale=None, round_out=True):
+def grouped_mm(a, w, counts, a_idx=None, y_idx=None, scale=None, w_scale=None, round_out=True, dtype="bf16"):
     """a (T|M, K), w (E, K, N) (float values, int8 allowed with w_scale (E, N)), counts (E,) -> y (M, N).
     Row r of the sorted problem reads a[a_idx[r]] (or a[r]) and is written to y[y_idx[r]] (or y[r]).  Epilogue order
-    as the reference: acc * w_scale[e, n] then * scale[r], one bf16 rounding."""
+    as the reference: acc * w_scale[e, n] then * scale[r], one rounding to a.dtype (dtype: "bf16" or "f16")."""
+    R = rounder(dtype)
     counts = np.asarray(counts, dtype=np.int64)
     M = int(counts.sum()) if a_idx is None else len(a_idx)
     N = w.shape[2]
@@ -261,7 +278,7 @@ def grouped_mm(a, w, counts, a_idx=None, y_idx=None, scale=None, w_scale=None, r
         if scale is not None:
             acc = acc * np.asarray(scale, dtype=np.float64)[rows, None]
         dst = y_idx[rows] if y_idx is not None else rows
-        y[dst] = round_bf16(acc) if round_out else acc
+        y[dst] = R(acc) if round_out else acc
         start += c
     return y
 
@@ -275,11 +292,12 @@ def silu64(g):
     return np.where(g < -88.72283935546875, -0.0, s)
 
 
-def swiglu_fwd(gb, ub):
-    """act = self._act(g) * u on bf16 tensors (aurora/hf_compat.py:81): silu rounded to bf16, then the product
-    rounded to bf16 (gb, ub already bf16 values)."""
-    s = round_bf16(silu64(gb))
-    return round_bf16(s.astype(np.float64) * ub.astype(np.float64))
+def swiglu_fwd(gb, ub, dtype="bf16"):
+    """act = self._act(g) * u on 16-bit tensors (aurora/hf_compat.py:81): silu rounded to the tensors' type, then
+    the product rounded to it (gb, ub already values of that type; dtype "bf16" or "f16")."""
+    R = rounder(dtype)
+    s = R(silu64(gb))
+    return R(s.astype(np.float64) * ub.astype(np.float64))
 
 
 def quant_int8(w):
@@ -293,12 +311,14 @@ def quant_int8(w):
 # ----------------------------------------------------------------------------------------------------------------
 # layer forward: the Triton path of aurora/hf_compat.py:75-82
 # ----------------------------------------------------------------------------------------------------------------
-def moe_forward(x, ids, topk_w, wgu, wd, tokens=None, wgu_s=None, wd_s=None):
+def moe_forward(x, ids, topk_w, wgu, wd, tokens=None, wgu_s=None, wd_s=None, dtype="bf16"):
     """x (T, d) bf16 values (float32 array), ids (T, k), topk_w (T, k) fp32, wgu (E, d, 2h), wd (E, h, d).
     Returns dict with out (T, d) and the per-flat-row intermediates (gb, ub, act, yhat, y) in flat order
     f = t*k + j.  tokens: optional subset of token indices (then only those tokens' rows are computed; arrays are
     indexed by position in `tokens`).  wgu_s (E, 2h) / wd_s (E, d): int8 weights' per-column scales, applied to
-    the sums before any rounding (aurora/moe_triton.py:48-51 on a layer fused with quant="int8")."""
+    the sums before any rounding (aurora/moe_triton.py:48-51 on a layer fused with quant="int8").  dtype: the
+    activations' type whose rounding points apply, "bf16" or "f16" (a model loaded in fp16)."""
+    R = rounder(dtype)
     T, k = ids.shape
     E = wgu.shape[0]
     h = wgu.shape[2] // 2
@@ -310,7 +330,7 @@ def moe_forward(x, ids, topk_w, wgu, wd, tokens=None, wgu_s=None, wd_s=None):
     act = np.zeros((n * k, h), np.float32)
     yhat = np.zeros((n * k, d), np.float64)
     y = np.zeros((n * k, d), np.float32)
-    wb = round_bf16(topk_w[tok].reshape(-1))
+    wb = R(topk_w[tok].reshape(-1))
     flat_e = ids[tok].reshape(-1)
     rows_t = np.repeat(tok, k)
     for e in range(E):
@@ -320,15 +340,15 @@ def moe_forward(x, ids, topk_w, wgu, wd, tokens=None, wgu_s=None, wd_s=None):
         gu = x[rows_t[sel]].astype(np.float64) @ wgu[e].astype(np.float64)
         if wgu_s is not None:
             gu = gu * np.asarray(wgu_s[e], dtype=np.float64)[None, :]
-        gb[sel] = round_bf16(gu[:, :h])
-        ub[sel] = round_bf16(gu[:, h:])
-        act[sel] = swiglu_fwd(gb[sel], ub[sel])
+        gb[sel] = R(gu[:, :h])
+        ub[sel] = R(gu[:, h:])
+        act[sel] = swiglu_fwd(gb[sel], ub[sel], dtype)
         yh = act[sel].astype(np.float64) @ wd[e].astype(np.float64)
         if wd_s is not None:
             yh = yh * np.asarray(wd_s[e], dtype=np.float64)[None, :]
         yhat[sel] = yh
-        y[sel] = round_bf16(yh * wb[sel].astype(np.float64)[:, None])
-    out = round_bf16(y.reshape(n, k, d).astype(np.float64).sum(1))
+        y[sel] = R(yh * wb[sel].astype(np.float64)[:, None])
+    out = R(y.reshape(n, k, d).astype(np.float64).sum(1))
     return dict(out=out, gb=gb, ub=ub, act=act, yhat=yhat, y=y, wb=wb)
 
 

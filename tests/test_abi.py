@@ -72,21 +72,29 @@ def test_argument_validation_codes(lib):
     assert L.hmoe_route_sigmoid_group(P, 8, P, None, 0, 8, 128, 8, 8, 2, 2.5, None, P, P, None) == 0
     # dispatch: dtype, workspace, E bounds
     ws = L.hmoe_dispatch_workspace_size(16, 2, 4)
-    assert L.hmoe_dispatch(P, 2, None, 0, 16, 2, 4, None, 0, 0, None, P, None, P, P, P, P, None, None, P, ws, None) == -3
-    assert L.hmoe_dispatch(P, 4, None, 0, 16, 2, 4, None, 0, 0, None, P, None, P, P, P, P, None, None, P, ws - 1,
+    assert L.hmoe_dispatch(P, 2, None, 0, 16, 2, 4, None, 0, 0, None, P, None, P, P, P, P, None, None, P, ws, 0,
+                           None) == -3
+    assert L.hmoe_dispatch(P, 4, None, 0, 16, 2, 4, None, 0, 0, None, P, None, P, P, P, P, None, None, P, ws - 1, 0,
                            None) == -5
-    assert L.hmoe_dispatch(P, 4, None, 0, 16, 2, 2000, None, 0, 0, None, P, None, P, P, P, P, None, None, P, ws,
+    assert L.hmoe_dispatch(P, 4, None, 0, 16, 2, 2000, None, 0, 0, None, P, None, P, P, P, P, None, None, P, ws, 0,
                            None) == -2
     # a missing order or topk_ids is refused before the first launch (counts / starts stay untouched)
-    assert L.hmoe_dispatch(P, 4, None, 0, 16, 2, 4, None, 0, 0, None, P, None, P, None, P, P, None, None, P, ws,
+    assert L.hmoe_dispatch(P, 4, None, 0, 16, 2, 4, None, 0, 0, None, P, None, P, None, P, P, None, None, P, ws, 0,
                            None) == -1
-    assert L.hmoe_dispatch(None, 4, None, 0, 16, 2, 4, None, 0, 0, None, P, None, P, P, P, P, None, None, P, ws,
+    assert L.hmoe_dispatch(None, 4, None, 0, 16, 2, 4, None, 0, 0, None, P, None, P, P, P, P, None, None, P, ws, 0,
                            None) == -1
+    # the activation type: bf16 (0) or fp16 (1)
+    assert L.hmoe_dispatch(P, 4, None, 0, 16, 2, 4, None, 0, 0, None, P, None, P, P, P, P, None, None, P, ws, 2,
+                           None) == -3
     # grouped_mm: K % 8, fp32 input, int8 weights
     assert L.hmoe_grouped_mm(P, 64, 0, P, 0, 3, 60, 32, 60 * 32, 32, P, 4, 48, None, None, None, 0, None, 0, P, 32,
                              None) == -2
-    assert L.hmoe_grouped_mm(P, 64, 2, P, 0, 3, 64, 32, 64 * 32, 32, P, 4, 48, None, None, None, 0, None, 0, P, 32,
-                             None) == -3
+    assert L.hmoe_grouped_mm(P, 64, 2, P, 2, 3, 64, 32, 64 * 32, 32, P, 4, 48, None, None, None, 0, None, 0, P, 32,
+                             None) == -3  # fp32 activations
+    assert L.hmoe_grouped_mm(P, 64, 1, P, 0, 3, 64, 32, 64 * 32, 32, P, 4, 48, None, None, None, 0, None, 0, P, 32,
+                             None) == -3  # fp16 a with bf16 w
+    assert L.hmoe_grouped_mm(P, 64, 1, P, 1, 3, 64, 32, 64 * 32, 32, P, 4, 48, None, None, P, 0, None, 0, P, 32,
+                             None) == -3  # fp16 a with a bf16 row scale
     assert L.hmoe_grouped_mm(P, 64, 0, P, 0, 3, 64, 32, 64 * 32, 32, P, 4, 48, None, None, None, 0, P, 0, P, 32,
                              None) == -3
     assert L.hmoe_grouped_mm(P, 64, 0, P, 0, 3, 64, 32, 64 * 32, 32, P, 4, 0, None, None, None, 0, None, 0, P, 32,
@@ -100,18 +108,21 @@ def test_argument_validation_codes(lib):
                              None) == -2
     assert L.hmoe_grouped_mm(P, 64, 0, P, 5, 3, 64, 32, 64 * 32, 32, P, 4, 48, None, None, None, 0, P, 3, P, 32,
                              None) == -3
-    assert L.hmoe_gate_up_swiglu_i8(P, 64, None, P, P, 0, 3, 64, 24, P, 4, 48, P, None) == -2  # h % 16
-    assert L.hmoe_gate_up_swiglu_i8(P, 64, None, P, P, 0, 3, 64, 32, P, 4, 0, P, None) == 0
-    assert L.hmoe_gate_up_swiglu_i8(P, 64, None, None, P, 0, 3, 64, 32, P, 4, 48, P, None) == -1
-    assert L.hmoe_down_scatter_i8(P, P, P, 4, 3, 32, 64, P, 4, 48, P, P, P, None) == -3  # scale dtype
-    assert L.hmoe_down_scatter_i8(P, P, P, 0, 3, 32, 72, P, 4, 48, P, P, P, None) == -2  # d % 16
+    assert L.hmoe_gate_up_swiglu_i8(P, 64, None, P, P, 0, 3, 64, 24, P, 4, 48, P, 0, None) == -2  # h % 16
+    assert L.hmoe_gate_up_swiglu_i8(P, 64, None, P, P, 0, 3, 64, 32, P, 4, 0, P, 0, None) == 0
+    assert L.hmoe_gate_up_swiglu_i8(P, 64, None, None, P, 0, 3, 64, 32, P, 4, 48, P, 0, None) == -1
+    assert L.hmoe_gate_up_swiglu_i8(P, 64, None, P, P, 0, 3, 64, 32, P, 4, 48, P, 2, None) == -3  # fp32 activations
+    assert L.hmoe_down_scatter_i8(P, P, P, 4, 3, 32, 64, P, 4, 48, P, P, P, 0, None) == -3  # scale dtype
+    assert L.hmoe_down_scatter_i8(P, P, P, 0, 3, 32, 72, P, 4, 48, P, P, P, 1, None) == -2  # d % 16
     # direct-load offsets beyond 2^31 bytes
-    assert L.hmoe_gate_up_swiglu(P, 4096, P, P, 3, 4096, 65536, P, 4, 1 << 20, P, None, None) == -2
+    assert L.hmoe_gate_up_swiglu(P, 4096, P, P, 3, 4096, 65536, P, 4, 1 << 20, P, None, 0, None) == -2
+    assert L.hmoe_down_scatter(P, P, 3, 64, 64, P, 4, 48, P, P, P, None, 4, None) == -3  # int64 activations
     # wgrad: output dtype, shapes
     assert L.hmoe_grouped_wgrad(P, 64, P, 64, 3, 64, 64, P, 4, 48, P, 3, None) == -3
     assert L.hmoe_grouped_wgrad(P, 64, P, 64, 3, 60, 64, P, 4, 48, P, 2, None) == -2
     # combine / backward elementwise
-    assert L.hmoe_combine(P, None, 4, 2, 12, P, None) == -1
+    assert L.hmoe_combine(P, None, 4, 2, 12, P, 0, None) == -1
+    assert L.hmoe_combine(P, None, 4, 2, 16, P, 2, None) == -3
     assert L.hmoe_unpermute_bwd(P, 5, P, None, None, 4, 2, 64, 0, P, None) == -3
     assert L.hmoe_router_bwd(P, P, P, 16, 300, 2, 1, 1.0, P, 64, 64, P, None, 2, None, 0, None) == -2
     assert L.hmoe_router_bwd(P, P, P, 16, 8, 2, 1, 1.0, P, 64, 64, P, P, 2, None, 0, None) == -5

@@ -26,6 +26,20 @@ def test_swiglu_rounding_matches_torch_bf16(oracle):
     assert mism.size == 0, f"{mism.size} of {g.numel()} differ, first at g={g[mism[0]].item()} u={u[mism[0]].item()}"
 
 
+def test_swiglu_rounding_matches_torch_fp16(oracle):
+    """The same for a model loaded in fp16: silu rounded to fp16, then the product rounded to fp16, as torch's fp16
+    F.silu(g) * u."""
+    rng = np.random.default_rng(13)
+    n = 100_000
+    g = torch.from_numpy(np.concatenate([rng.normal(0, 1, n // 2), rng.normal(0, 8, n // 2 - 4),
+                                         [0.0, -12.0, 12.0, 1e-7]]).astype(np.float32)).half()
+    u = torch.from_numpy(rng.normal(0, 2, g.numel()).astype(np.float32)).half()
+    want = (F.silu(g) * u).numpy()
+    got = oracle.swiglu_fwd(g.float().numpy(), u.float().numpy(), dtype="f16").astype(np.float16)
+    mism = np.nonzero(got.view(np.uint16) != want.view(np.uint16))[0]
+    assert mism.size == 0, f"{mism.size} of {g.numel()} differ, first at g={g[mism[0]].item()} u={u[mism[0]].item()}"
+
+
 def test_swiglu_rounding_check_fails_on_one_rounding(oracle):
     """The check above can fail: a SwiGLU with one rounding (the product in float64, rounded once) differs from
     torch's on a large share of the same kind of inputs."""

@@ -200,7 +200,10 @@ def test_ops_reject_mismatched_stacks():
     with pytest.raises(ValueError):
         moe_swiglu(x, wr, wgu, wd, E + 1)
     with pytest.raises(TypeError):
-        moe_swiglu(x, wr, wgu.half(), wd, k)
+        moe_swiglu(x, wr, wgu.to(torch.int8), wd, k)
+    with pytest.raises(TypeError):  # 16-bit weights must have the activations' type (bf16 with bf16, fp16 with fp16)
+        ops.gate_up_swiglu(x, wgu.half(), torch.full((E,), M // E, dtype=torch.int32, device=dev), M,
+                           a_idx=torch.zeros(M, dtype=torch.int32, device=dev))
     with pytest.raises(ValueError):
         ops.route_topk(x, torch.zeros(E, d + 8, **bf), k)
     with pytest.raises(ValueError):
@@ -225,5 +228,9 @@ def test_ops_reject_mismatched_stacks():
         ops.grouped_mm(a, wgu, counts, M, out=torch.zeros(M - 1, 2 * h, **bf))
     with pytest.raises(TypeError):
         ops.grouped_mm(a, wgu.float(), counts, M)
+    with pytest.raises(TypeError):
+        ops.grouped_mm(a.half(), wgu, counts, M)
+    with pytest.raises(TypeError):
+        ops.grouped_mm(a.float(), wgu.float(), counts, M)
     with pytest.raises(ValueError):
         ops.dispatch(torch.zeros(T, k, dtype=torch.int32, device=dev), E, x=x[:T - 1])

@@ -164,7 +164,7 @@ def test_moe_swiglu_rejects_mismatched_shapes_before_launch():
     wr, wgu, wd = (torch.zeros(s, dtype=torch.bfloat16) for s in ((E, d), (E, d, 2 * h), (E, h, d)))
     for args, err in (((x, torch.zeros(E + 1, d, dtype=torch.bfloat16), wgu, wd, 2), ValueError),
                       ((x, wr, torch.zeros(E, d, 2 * h + 2, dtype=torch.bfloat16), wd, 2), ValueError),
-                      ((x, wr, wgu, torch.zeros(E, h, d, dtype=torch.float16), 2), TypeError),
+                      ((x, wr, wgu, torch.zeros(E, h, d, dtype=torch.int8), 2), TypeError),
                       ((x.float(), wr, wgu, wd, 2), TypeError),
                       ((x, wr, wgu, wd, 0), ValueError)):
         with pytest.raises(err):

@@ -235,17 +235,19 @@ def test_grouped_mm_int8_scale_is_dequantised_product(oracle):
 
 
 # ------------------------------------------------------------------------------------------------- layer forward
-def test_moe_forward_vs_token_loop(oracle):
-    """The per-expert batched oracle against a per-token loop with the same rounding points (tiny shapes)."""
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_moe_forward_vs_token_loop(oracle, dtype):
+    """The per-expert batched oracle against a per-token loop with the same rounding points (tiny shapes), for bf16
+    activations and for fp16 ones (a model loaded in fp16: every rounding point rounds to fp16 instead)."""
     rng = np.random.default_rng(8)
     T, d, E, k, h = 8, 16, 4, 2, 8
-    R = oracle.round_bf16
+    R = oracle.round_bf16 if dtype == "bf16" else oracle.round_f16
     x = R(rng.standard_normal((T, d)))
     wgu = R(rng.standard_normal((E, d, 2 * h)) * 0.3)
     wd = R(rng.standard_normal((E, h, d)) * 0.3)
     ids = np.stack([rng.permutation(E)[:k] for _ in range(T)])
     tw = rng.random((T, k)).astype(np.float32)
-    f = oracle.moe_forward(x, ids, tw, wgu, wd)
+    f = oracle.moe_forward(x, ids, tw, wgu, wd, dtype=dtype)
     for t in range(T):
         acc = np.zeros(d)
         for j in range(k):
@@ -259,6 +261,31 @@ def test_moe_forward_vs_token_loop(oracle):
             wb = float(R(np.array([tw[t, j]]))[0])
             acc += R(np.array(yh) * wb).astype(np.float64)
         np.testing.assert_array_equal(f["out"][t], R(acc))
+
+
+def test_round_f16_brute_force(oracle):
+    """round_f16 against a brute-force search over every finite fp16 value: the nearest, ties to the even bit
+    pattern, overflow to inf -- on random float64 values, exact midpoints between neighbours, and edges."""
+    allh = np.arange(0, 0x7C00, dtype=np.uint16).view(np.float16).astype(np.float64)  # +0 .. 65504
+    rng = np.random.default_rng(5)
+    mids = (allh[1:] + allh[:-1]) / 2  # exact midpoints (float64 holds them)
+    pick = rng.choice(mids.size, 3000, replace=False)
+    vals = np.concatenate([rng.standard_normal(3000) * 30.0, rng.standard_normal(1000) * 1e-5, mids[pick],
+                           [0.0, 65504.0, 65519.99, 65520.0, 1e6, 2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26]])
+    vals = np.concatenate([vals, -vals])
+    got = oracle.round_f16(vals).astype(np.float64)
+    for v, g in zip(vals, got):
+        a = abs(v)
+        if a >= 65520.0:  # beyond the largest finite value plus half an ulp: inf
+            assert np.isinf(g) and np.sign(g) == np.sign(v)
+            continue
+        i = np.searchsorted(allh, a)
+        cand = [j for j in (i - 1, i) if 0 <= j < allh.size]
+        dist = [abs(allh[j] - a) for j in cand]
+        best = min(dist)
+        ties = [j for j, dd in zip(cand, dist) if dd == best]
+        j = ties[0] if len(ties) == 1 else [t for t in ties if t % 2 == 0][0]
+        assert abs(g) == allh[j] and (g == 0 or np.sign(g) == np.sign(v)), (v, g, allh[j])
 
 
 def test_moe_forward_int8_scales(oracle):

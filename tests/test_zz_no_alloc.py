@@ -26,7 +26,7 @@ def _dispatch(L, name, ids, tw, x, E):
         nbytes = L.lib().hmoe_dispatch_workspace_size(T, k, E)
         ws = torch.empty(nbytes, device=dev, dtype=torch.uint8)
         args += [L.ptr(ws), nbytes]
-    L.call(name, *args, L.stream(dev))
+    L.call(name, *args, L.dt(x), L.stream(dev))
     torch.cuda.synchronize()
     return out
 
@@ -56,7 +56,7 @@ def test_dispatch_noalloc_refuses_inputs_beyond_its_scratch():
     P = 4096  # stand-in addresses: the size check comes before any launch, nothing is dereferenced
     T, k, E = 1 << 21, 2, 16
     assert lib.hmoe_dispatch_workspace_size(T, k, E) > 8 << 20
-    rc = lib.hmoe_dispatch_noalloc(P, 3, None, 0, T, k, E, None, 0, 0, None, P, None, P, P, P, P, None, None, None)
+    rc = lib.hmoe_dispatch_noalloc(P, 3, None, 0, T, k, E, None, 0, 0, None, P, None, P, P, P, P, None, None, 0, None)
     assert rc == -7 and "scratch" in lib.hmoe_error_string(rc).decode()
 
 
@@ -82,7 +82,8 @@ def test_dispatch_noalloc_graph_replay():
     def call(stream):
         L.call("hmoe_dispatch_noalloc", L.ptr(ids), L.dt(ids), L.ptr(tw), L.dt(tw), T, k, E, L.ptr(x), x.stride(0), d,
                L.ptr(out["xs"]), L.ptr(out["counts"]), None, L.ptr(out["starts"]), L.ptr(out["order"]),
-               L.ptr(out["a_idx"]), L.ptr(out["inv_pos"]), L.ptr(out["w_sorted"]), L.ptr(out["n_invalid"]), stream)
+               L.ptr(out["a_idx"]), L.ptr(out["inv_pos"]), L.ptr(out["w_sorted"]), L.ptr(out["n_invalid"]), L.dt(x),
+               stream)
 
     call(L.stream(dev))  # the eager first call on this device
     torch.cuda.synchronize()

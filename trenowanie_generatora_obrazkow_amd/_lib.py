@@ -31,22 +31,22 @@ SIGNATURES = {
                                         _P]),
     "hmoe_dispatch_workspace_size": (_SZ, [_I64, _I32, _I32]),
     "hmoe_dispatch": (_I32, [_P, _I32, _P, _I32, _I64, _I32, _I32, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P,
-                             _P, _P, _SZ, _P]),
+                             _P, _P, _SZ, _I32, _P]),
     "hmoe_dispatch_noalloc": (_I32, [_P, _I32, _P, _I32, _I64, _I32, _I32, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P,
-                                     _P, _P, _P]),
+                                     _P, _P, _I32, _P]),
     "hmoe_make_schedule": (_I32, [_P, _I32, _I32, _I64, _I32, _P, _P, _P, _P]),
     "hmoe_grouped_mm": (_I32, [_P, _I64, _I32, _P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P,
                                _I32, _P, _I32, _P, _I64, _P]),
-    "hmoe_gate_up_swiglu": (_I32, [_P, _I64, _P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P]),
-    "hmoe_gate_up_swiglu_tiles": (_I32, [_P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P]),
+    "hmoe_gate_up_swiglu": (_I32, [_P, _I64, _P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _I32, _P]),
+    "hmoe_gate_up_swiglu_tiles": (_I32, [_P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _I32, _P]),
     "hmoe_xs_tiles_bytes": (_SZ, [_I64, _I32, _I64]),
     "hmoe_dispatch_tiles": (_I32, [_P, _I32, _P, _I32, _I64, _I32, _I32, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P,
-                                   _P, _P, _P, _P, _SZ, _P]),
-    "hmoe_down_scatter": (_I32, [_P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P, _P, _P]),
-    "hmoe_gate_up_swiglu_i8": (_I32, [_P, _I64, _P, _P, _P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _P, _P]),
-    "hmoe_down_scatter_i8": (_I32, [_P, _P, _P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P, _P]),
-    "hmoe_combine": (_I32, [_P, _P, _I64, _I32, _I64, _P, _P]),
-    "hmoe_combine_add": (_I32, [_P, _P, _I64, _I32, _I64, _P, _P, _P]),
+                                   _P, _P, _P, _P, _SZ, _I32, _P]),
+    "hmoe_down_scatter": (_I32, [_P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P, _P, _I32, _P]),
+    "hmoe_gate_up_swiglu_i8": (_I32, [_P, _I64, _P, _P, _P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _P, _I32, _P]),
+    "hmoe_down_scatter_i8": (_I32, [_P, _P, _P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P, _I32, _P]),
+    "hmoe_combine": (_I32, [_P, _P, _I64, _I32, _I64, _P, _I32, _P]),
+    "hmoe_combine_add": (_I32, [_P, _P, _I64, _I32, _I64, _P, _P, _I32, _P]),
     "hmoe_combine_bwd": (_I32, [_P, _P, _P, _P, _P, _I64, _I32, _I64, _P, _P, _P]),
     "hmoe_down_dgrad_swiglu": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P]),
     "hmoe_down_dgrad_dw_workspace_size": (_SZ, [_I64, _I64]),

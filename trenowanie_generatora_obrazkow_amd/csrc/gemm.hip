@@ -29,8 +29,12 @@ namespace hmoe {
 // The kernel
 // ----------------------------------------------------------------------------------------------------------------
 // A_BLK: the A rows (MGROUP) come from the row-group tiles of the sorted rows (gemm_common.h), not from A's rows.
-template <class C, int MODE, bool A_MN, bool B_MN, int EPI, bool A_BLK = false>
+// F16: the 16-bit operands, row scales and outputs are fp16 (v_mfma_f32_32x32x16_f16) instead of bf16; forward
+// epilogues (store, SwiGLU) only.
+template <class C, int MODE, bool A_MN, bool B_MN, int EPI, bool A_BLK = false, bool F16 = false>
 __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
+  static_assert(!F16 || EPI == EPI_STORE || EPI == EPI_SWIGLU, "fp16: forward epilogues only");
+  using X = Elt<F16>;
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   __shared__ int64_t s_rstart[kMaxEGemm + 1];
   __shared__ int s_tstart[kMaxEGemm + 1];  // MGROUP: prefix of ceil(count / BM); KGROUP: one m-tile per expert
@@ -111,7 +115,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
   const int total = total_m * nb_n;
 
   typename TileSel<A_MN, C::BM, C::NWAVES>::type ta;
-  typename TileSel<B_MN, C::BN, C::NWAVES, C::BE, C::FN>::type tb;
+  typename TileSel<B_MN, C::BN, C::NWAVES, C::BE, C::FN, F16>::type tb;
   // A wave's fragment f along a dimension covers 32 rows / columns from f * FS + 32 w: the lane part of the read
   // address is that of wave (w & 1) inside a 64-wide group, and 64 * (w >> 1) selects the group.
   static_assert(C::FSM % 64 == 0 && C::FSN % 64 == 0, "fragment reads work on 64-wide groups");
@@ -378,7 +382,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
     // unchanged, so the wait counts hold); the accumulators of the other rows stay zero and are not stored.  Such a
     // tile takes about FE/FM of a full tile's time.
     typedef typename TileSel<A_MN, C::BM, C::NWAVES>::type TA;
-    typedef typename TileSel<B_MN, C::BN, C::NWAVES, C::BE, C::FN>::type TB;
+    typedef typename TileSel<B_MN, C::BN, C::NWAVES, C::BE, C::FN, F16>::type TB;
     struct Frags {
       bf16x8 xa[C::FM], wb[C::FN];
     };
@@ -407,7 +411,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
         for (int a = 0; a < FE; ++a)
 #pragma unroll
           for (int j = 0; j < NL; ++j)
-            acc[a][bf(j)] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.wb[bf(j)], f.xa[a], acc[a][bf(j)], 0, 0, 0);
+            acc[a][bf(j)] = mfma16<F16>(f.wb[bf(j)], f.xa[a], acc[a][bf(j)]);
       };
       // one LDS read after each MFMA while both last, then whichever is left
       auto interleave = [&]() {
@@ -491,7 +495,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
 #pragma unroll
           for (int j = 0; j < NL; ++j) {
             const int i = a * NL + j, b = bf(j);
-            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f1.wb[b], f1.xa[a], acc[a][b], 0, 0, 0);
+            acc[a][b] = mfma16<F16>(f1.wb[b], f1.xa[a], acc[a][b]);
             if (i < FE)
               f0.xa[i] = TA::frag(cons, i * C::FSM + wgrp_a, loff_a, 0);
             else if (i < FE + NL)
@@ -610,7 +614,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
     };
     [[maybe_unused]] auto row_scale = [&](int rt) -> float {
       if (!p.scale) return 1.0f;
-      return p.scale_f32 ? s_rowsc[par][rt + sc_sh] : bf2f(reinterpret_cast<const uint16_t*>(s_rowsc[par])[rt + sc_sh]);
+      return p.scale_f32 ? s_rowsc[par][rt + sc_sh] : X::one(reinterpret_cast<const uint16_t*>(s_rowsc[par])[rt + sc_sh]);
     };
     auto col_of = [&](int b, int g) { return b * C::FSN + wn * 32 + 8 * g + lcol; };  // tile column (write phase)
 #pragma unroll
@@ -647,7 +651,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
             const f32x16& v = acc[a][b];
-            if (p.aux) park_bf16(NSP, b, g, cvt_bf2(v[4 * g], v[4 * g + 1]), cvt_bf2(v[4 * g + 2], v[4 * g + 3]));
+            if (p.aux) park_bf16(NSP, b, g, X::pack2(v[4 * g], v[4 * g + 1]), X::pack2(v[4 * g + 2], v[4 * g + 3]));
             float v0, v1, v2, v3;
             if constexpr (C::BE == 1) {  // int8 weights: column scale first, then the row scale (two products)
               float ws[4];
@@ -660,7 +664,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
             if constexpr (EPI == EPI_STORE_F32)
               park_f32(0, b, g, make_float4(v0, v1, v2, v3));
             else
-              park_bf16(0, b, g, cvt_bf2(v0, v1), cvt_bf2(v2, v3));
+              park_bf16(0, b, g, X::pack2(v0, v1), X::pack2(v2, v3));
           }
         }
         drain(0, RB, ES, [&](int r, int tc, uint4 v) {
@@ -702,14 +706,14 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
                 us[t] *= wu[t];
               }
             }
-            const uint32_t gb0 = cvt_bf2(gs[0], gs[1]), gb1 = cvt_bf2(gs[2], gs[3]);
-            const uint32_t ub0 = cvt_bf2(us[0], us[1]), ub1 = cvt_bf2(us[2], us[3]);
-            const float gg[4] = {bf_lo(gb0), bf_hi(gb0), bf_lo(gb1), bf_hi(gb1)};
-            const float uu[4] = {bf_lo(ub0), bf_hi(ub0), bf_lo(ub1), bf_hi(ub1)};
-            // act = bf16(bf16(silu(g)) * u) with g, u the bf16-rounded projections
-            const uint32_t sl0 = cvt_bf2(silu_f(gg[0]), silu_f(gg[1])), sl1 = cvt_bf2(silu_f(gg[2]), silu_f(gg[3]));
-            park_bf16(0, b, g, cvt_bf2(bf_lo(sl0) * uu[0], bf_hi(sl0) * uu[1]),
-                      cvt_bf2(bf_lo(sl1) * uu[2], bf_hi(sl1) * uu[3]));
+            const uint32_t gb0 = X::pack2(gs[0], gs[1]), gb1 = X::pack2(gs[2], gs[3]);
+            const uint32_t ub0 = X::pack2(us[0], us[1]), ub1 = X::pack2(us[2], us[3]);
+            const float gg[4] = {X::lo(gb0), X::hi(gb0), X::lo(gb1), X::hi(gb1)};
+            const float uu[4] = {X::lo(ub0), X::hi(ub0), X::lo(ub1), X::hi(ub1)};
+            // act = R(R(silu(g)) * u) with g, u the rounded projections (R: to bf16, or fp16 with F16)
+            const uint32_t sl0 = X::pack2(silu_f(gg[0]), silu_f(gg[1])), sl1 = X::pack2(silu_f(gg[2]), silu_f(gg[3]));
+            park_bf16(0, b, g, X::pack2(X::lo(sl0) * uu[0], X::hi(sl0) * uu[1]),
+                      X::pack2(X::lo(sl1) * uu[2], X::hi(sl1) * uu[3]));
             if (p.aux) {
               park_bf16(NSP, b, g, gb0, gb1);
               park_bf16(2 * NSP, b, g, ub0, ub1);
@@ -833,9 +837,9 @@ static int num_cus() {
   return n;
 }
 
-template <class C, int MODE, bool A_MN, bool B_MN, int EPI, bool A_BLK = false>
+template <class C, int MODE, bool A_MN, bool B_MN, int EPI, bool A_BLK = false, bool F16 = false>
 static int launch(const GemmParams& p, int64_t tiles_upper, hipStream_t s) {
-  auto kern = grouped_gemm_kernel<C, MODE, A_MN, B_MN, EPI, A_BLK>;
+  auto kern = grouped_gemm_kernel<C, MODE, A_MN, B_MN, EPI, A_BLK, F16>;
   static std::atomic<bool> attr_set[64];  // per device: the (idempotent) attribute call is done
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return HMOE_ERR_DEVICE;
@@ -918,19 +922,37 @@ static bool pick_large_mgroup(int64_t tiles_large, int64_t ncols, int64_t K, boo
   return EPI == EPI_SWIGLU ? tiles_large * 2 >= cus * 5 : tiles_large * 8 >= cus * 5;
 }
 
-template <int MODE, bool A_MN, bool B_MN, int EPI, bool A_BLK = false>
+template <int MODE, bool A_MN, bool B_MN, int EPI, bool A_BLK = false, bool F16 = false>
 static int launch_mgroup(const GemmParams& p, int64_t ncols, hipStream_t s) {
   const int64_t tl = mgroup_tiles<CfgL, EPI>(p.M, p.E, ncols);
-  if (pick_large_mgroup<EPI>(tl, ncols, p.K, false)) return launch<CfgL, MODE, A_MN, B_MN, EPI, A_BLK>(p, tl, s);
-  return launch<CfgS, MODE, A_MN, B_MN, EPI, A_BLK>(p, mgroup_tiles<CfgS, EPI>(p.M, p.E, ncols), s);
+  if (pick_large_mgroup<EPI>(tl, ncols, p.K, false))
+    return launch<CfgL, MODE, A_MN, B_MN, EPI, A_BLK, F16>(p, tl, s);
+  return launch<CfgS, MODE, A_MN, B_MN, EPI, A_BLK, F16>(p, mgroup_tiles<CfgS, EPI>(p.M, p.E, ncols), s);
+}
+
+// the bf16 (f16 = false) or fp16 form of a forward launch
+template <int EPI, bool A_BLK = false>
+static int launch_fwd(const GemmParams& p, int64_t ncols, bool f16, hipStream_t s) {
+  return f16 ? launch_mgroup<MGROUP, false, true, EPI, A_BLK, true>(p, ncols, s)
+             : launch_mgroup<MGROUP, false, true, EPI, A_BLK, false>(p, ncols, s);
 }
 
 // int8 weights: the int8 tile configurations
-template <int EPI>
-static int launch_mgroup_i8(const GemmParams& p, int64_t ncols, hipStream_t s) {
+template <int EPI, bool F16 = false>
+static int launch_mgroup_i8_t(const GemmParams& p, int64_t ncols, hipStream_t s) {
   const int64_t tl = mgroup_tiles<CfgL8, EPI>(p.M, p.E, ncols);
-  if (pick_large_mgroup<EPI>(tl, ncols, p.K, true)) return launch<CfgL8, MGROUP, false, true, EPI>(p, tl, s);
-  return launch<CfgS8, MGROUP, false, true, EPI>(p, mgroup_tiles<CfgS8, EPI>(p.M, p.E, ncols), s);
+  if (pick_large_mgroup<EPI>(tl, ncols, p.K, true)) return launch<CfgL8, MGROUP, false, true, EPI, false, F16>(p, tl, s);
+  return launch<CfgS8, MGROUP, false, true, EPI, false, F16>(p, mgroup_tiles<CfgS8, EPI>(p.M, p.E, ncols), s);
+}
+template <int EPI>
+static int launch_mgroup_i8(const GemmParams& p, int64_t ncols, bool f16, hipStream_t s) {
+  return f16 ? launch_mgroup_i8_t<EPI, true>(p, ncols, s) : launch_mgroup_i8_t<EPI, false>(p, ncols, s);
+}
+
+// activation element type of the forward entry points: bf16 or fp16 (rc: HMOE_OK or HMOE_ERR_DTYPE)
+static inline bool act16(int dtype, int* rc) {
+  *rc = (dtype == HMOE_DT_BF16 || dtype == HMOE_DT_F16) ? HMOE_OK : HMOE_ERR_DTYPE;
+  return dtype == HMOE_DT_F16;
 }
 
 // Weight gradients: large tiles once they give every CU two tiles, unless they pad the (P, N) output area by more
@@ -993,11 +1015,12 @@ int hmoe_grouped_mm(const void* a, int64_t lda, int a_dtype, const void* w, int 
   if (rc) return rc;
   if (M == 0) return HMOE_OK;
   if (!a || !w || !y || K <= 0 || N <= 0) return HMOE_ERR_ARG;
-  if (a_dtype != HMOE_DT_BF16) return HMOE_ERR_DTYPE;
+  const bool f16 = act16(a_dtype, &rc);  // a, 16-bit w, a 16-bit scale and y share one type: bf16 or fp16
+  if (rc) return rc;
   const bool i8 = w_dtype == HMOE_DT_I8;
-  if (!i8 && w_dtype != HMOE_DT_BF16) return HMOE_ERR_DTYPE;
+  if (!i8 && w_dtype != a_dtype) return HMOE_ERR_DTYPE;
   if (i8 != (w_scale != nullptr)) return i8 ? HMOE_ERR_ARG : HMOE_ERR_DTYPE;  // int8 weights come with scales
-  if (scale && scale_dtype != HMOE_DT_BF16 && scale_dtype != HMOE_DT_F32) return HMOE_ERR_DTYPE;
+  if (scale && scale_dtype != a_dtype && scale_dtype != HMOE_DT_F32) return HMOE_ERR_DTYPE;
   if (K % 8 || N % 8 || lda % 8 || ldy % 8 || stride_wk % 8 || stride_we % 8) return HMOE_ERR_SHAPE;
   if (lda < K || ldy < N || stride_wk < N || !al16(a) || !al16(w) || !al16(y)) return HMOE_ERR_ARG;
   if (K > INT32_MAX || N > INT32_MAX || M > INT32_MAX) return HMOE_ERR_SHAPE;
@@ -1023,15 +1046,17 @@ int hmoe_grouped_mm(const void* a, int64_t lda, int a_dtype, const void* w, int 
     p.w_scale = w_scale;
     p.w_scale_f32 = w_scale_dtype == HMOE_DT_F32;
     p.ldws = N;
-    return launch_mgroup_i8<EPI_STORE>(p, N, s);
+    return launch_mgroup_i8<EPI_STORE>(p, N, f16, s);
   }
-  return launch_mgroup<MGROUP, false, true, EPI_STORE>(p, N, s);
+  return launch_fwd<EPI_STORE>(p, N, f16, s);
 }
 
 int hmoe_gate_up_swiglu(const void* x, int64_t ldx, const int32_t* a_idx, const void* wgu, int64_t E, int64_t d,
-                        int64_t h, const void* counts, int counts_dtype, int64_t M, void* act, void* gu,
+                        int64_t h, const void* counts, int counts_dtype, int64_t M, void* act, void* gu, int dtype,
                         hmoe_stream_t stream) {
   int rc = check_common(counts, counts_dtype, E, M);
+  if (rc) return rc;
+  const bool f16 = act16(dtype, &rc);
   if (rc) return rc;
   if (M == 0) return HMOE_OK;
   if (!x || !wgu || !act || d <= 0 || h <= 0) return HMOE_ERR_ARG;
@@ -1051,13 +1076,15 @@ int hmoe_gate_up_swiglu(const void* x, int64_t ldx, const int32_t* a_idx, const 
   p.C = act;
   p.ldc = h;
   p.aux = static_cast<uint16_t*>(gu);
-  return launch_mgroup<MGROUP, false, true, EPI_SWIGLU>(p, h, reinterpret_cast<hipStream_t>(stream));
+  return launch_fwd<EPI_SWIGLU>(p, h, f16, reinterpret_cast<hipStream_t>(stream));
 }
 
 int hmoe_gate_up_swiglu_tiles(const void* xs_tiles, const void* wgu, int64_t E, int64_t d, int64_t h,
-                              const void* counts, int counts_dtype, int64_t M, void* act, void* gu,
+                              const void* counts, int counts_dtype, int64_t M, void* act, void* gu, int dtype,
                               hmoe_stream_t stream) {
   int rc = check_common(counts, counts_dtype, E, M);
+  if (rc) return rc;
+  const bool f16 = act16(dtype, &rc);
   if (rc) return rc;
   if (M == 0) return HMOE_OK;
   if (!xs_tiles || !wgu || !act || d <= 0 || h <= 0) return HMOE_ERR_ARG;
@@ -1076,13 +1103,15 @@ int hmoe_gate_up_swiglu_tiles(const void* xs_tiles, const void* wgu, int64_t E, 
   p.C = act;
   p.ldc = h;
   p.aux = static_cast<uint16_t*>(gu);
-  return launch_mgroup<MGROUP, false, true, EPI_SWIGLU, true>(p, h, reinterpret_cast<hipStream_t>(stream));
+  return launch_fwd<EPI_SWIGLU, true>(p, h, f16, reinterpret_cast<hipStream_t>(stream));
 }
 
 int hmoe_down_scatter(const void* act, const void* wd, int64_t E, int64_t h, int64_t d, const void* counts,
                       int counts_dtype, int64_t M, const uint16_t* w_sorted, const int32_t* y_idx, void* y,
-                      void* yhat, hmoe_stream_t stream) {
+                      void* yhat, int dtype, hmoe_stream_t stream) {
   int rc = check_common(counts, counts_dtype, E, M);
+  if (rc) return rc;
+  const bool f16 = act16(dtype, &rc);
   if (rc) return rc;
   if (M == 0) return HMOE_OK;
   if (!act || !wd || !y || d <= 0 || h <= 0) return HMOE_ERR_ARG;
@@ -1103,13 +1132,15 @@ int hmoe_down_scatter(const void* act, const void* wd, int64_t E, int64_t h, int
   p.scale = w_sorted;
   p.scale_f32 = 0;
   p.aux = static_cast<uint16_t*>(yhat);
-  return launch_mgroup<MGROUP, false, true, EPI_STORE>(p, d, reinterpret_cast<hipStream_t>(stream));
+  return launch_fwd<EPI_STORE>(p, d, f16, reinterpret_cast<hipStream_t>(stream));
 }
 
 int hmoe_gate_up_swiglu_i8(const void* x, int64_t ldx, const int32_t* a_idx, const void* wgu_q, const void* wgu_s,
                            int wgu_s_dtype, int64_t E, int64_t d, int64_t h, const void* counts, int counts_dtype,
-                           int64_t M, void* act, hmoe_stream_t stream) {
+                           int64_t M, void* act, int dtype, hmoe_stream_t stream) {
   int rc = check_common(counts, counts_dtype, E, M);
+  if (rc) return rc;
+  const bool f16 = act16(dtype, &rc);
   if (rc) return rc;
   if (M == 0) return HMOE_OK;
   if (!x || !act || d <= 0 || h <= 0) return HMOE_ERR_ARG;
@@ -1132,13 +1163,15 @@ int hmoe_gate_up_swiglu_i8(const void* x, int64_t ldx, const int32_t* a_idx, con
   p.w_scale = wgu_s;
   p.w_scale_f32 = wgu_s_dtype == HMOE_DT_F32;
   p.ldws = 2 * h;
-  return launch_mgroup_i8<EPI_SWIGLU>(p, h, reinterpret_cast<hipStream_t>(stream));
+  return launch_mgroup_i8<EPI_SWIGLU>(p, h, f16, reinterpret_cast<hipStream_t>(stream));
 }
 
 int hmoe_down_scatter_i8(const void* act, const void* wd_q, const void* wd_s, int wd_s_dtype, int64_t E, int64_t h,
                          int64_t d, const void* counts, int counts_dtype, int64_t M, const uint16_t* w_sorted,
-                         const int32_t* y_idx, void* y, hmoe_stream_t stream) {
+                         const int32_t* y_idx, void* y, int dtype, hmoe_stream_t stream) {
   int rc = check_common(counts, counts_dtype, E, M);
+  if (rc) return rc;
+  const bool f16 = act16(dtype, &rc);
   if (rc) return rc;
   if (M == 0) return HMOE_OK;
   if (!act || !y || d <= 0 || h <= 0) return HMOE_ERR_ARG;
@@ -1162,7 +1195,7 @@ int hmoe_down_scatter_i8(const void* act, const void* wd_q, const void* wd_s, in
   p.w_scale = wd_s;
   p.w_scale_f32 = wd_s_dtype == HMOE_DT_F32;
   p.ldws = d;
-  return launch_mgroup_i8<EPI_STORE>(p, d, reinterpret_cast<hipStream_t>(stream));
+  return launch_mgroup_i8<EPI_STORE>(p, d, f16, reinterpret_cast<hipStream_t>(stream));
 }
 
 // Checks and parameters shared by the two down-dgrad entry points (rc: HMOE_OK, or the error to return).

@@ -201,11 +201,23 @@ struct MNTile {
   }
 };
 
+// MFMA on one k16 step of 16-bit fragments (8 elements per lane, bf16 or fp16 bits), fp32 accumulation
+template <bool F16>
+__device__ __forceinline__ f32x16 mfma16(bf16x8 a, bf16x8 b, f32x16 c) {
+  if constexpr (F16) {
+    typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                   0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+}
+
 // int8 MN-major operand (weights (K, N), N contiguous, as int8): 32 k-rows x ROWS columns = ROWS bytes per k-row.
 // Each 16-byte chunk holds 16 columns.  Logical chunk c = 4b + 2wn + h of a k-row (fragment b of wave column wn,
 // half h of its 32 columns) is stored at b + FN*((2wn + h) ^ (k & 3)), so the k-rows a transpose read touches spread
 // over the banks while fragment b stays a compile-time offset.
-template <int ROWS, int NWAVES, int FN>
+template <int ROWS, int NWAVES, int FN, bool F16 = false>
 struct MNTile8 {
   static constexpr int INSTR = ROWS * kBK / 1024;
   static constexpr int PER_WAVE = INSTR / NWAVES;
@@ -243,7 +255,7 @@ struct MNTile8 {
     const int h = (lane >> 4) & 1;
     return kr * ROWS + 16 * FN * ((2 * w32 + h) ^ (kr & 3)) + 8 * (lane & 1);
   }
-  // fragment b (columns b*FSN + 32 w32 + 0..31) x 16 k (ks*16 + ...), converted exactly to bf16
+  // fragment b (columns b*FSN + 32 w32 + 0..31) x 16 k (ks*16 + ...), converted exactly to bf16 (fp16 with F16)
   __device__ __forceinline__ static bf16x8 frag(const char* lds_tile, int grp64, int loff, int ks) {
     typedef int i32x2 __attribute__((ext_vector_type(2)));
     typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
@@ -259,24 +271,25 @@ struct MNTile8 {
       f[4 + j] = (float)(int8_t)(hi >> (8 * j));
     }
     typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-    const u32x4 w = {cvt_bf2(f[0], f[1]), cvt_bf2(f[2], f[3]), cvt_bf2(f[4], f[5]), cvt_bf2(f[6], f[7])};
+    using X = Elt<F16>;
+    const u32x4 w = {X::pack2(f[0], f[1]), X::pack2(f[2], f[3]), X::pack2(f[4], f[5]), X::pack2(f[6], f[7])};
     return __builtin_bit_cast(bf16x8, w);
   }
 };
 
-template <bool MN, int ROWS, int NWAVES, int ES = 2, int FN = 4>
+template <bool MN, int ROWS, int NWAVES, int ES = 2, int FN = 4, bool F16 = false>
 struct TileSel;
-template <int ROWS, int NWAVES, int FN>
-struct TileSel<false, ROWS, NWAVES, 2, FN> {
+template <int ROWS, int NWAVES, int FN, bool F16>
+struct TileSel<false, ROWS, NWAVES, 2, FN, F16> {
   using type = KTile<ROWS, NWAVES>;
 };
-template <int ROWS, int NWAVES, int FN>
-struct TileSel<true, ROWS, NWAVES, 2, FN> {
+template <int ROWS, int NWAVES, int FN, bool F16>
+struct TileSel<true, ROWS, NWAVES, 2, FN, F16> {
   using type = MNTile<ROWS, NWAVES>;
 };
-template <int ROWS, int NWAVES, int FN>
-struct TileSel<true, ROWS, NWAVES, 1, FN> {
-  using type = MNTile8<ROWS, NWAVES, FN>;
+template <int ROWS, int NWAVES, int FN, bool F16>
+struct TileSel<true, ROWS, NWAVES, 1, FN, F16> {
+  using type = MNTile8<ROWS, NWAVES, FN, F16>;
 };
 
 // Workgroup barrier that orders LDS only.  __syncthreads() is a workgroup release/acquire fence over all address
@@ -332,7 +345,7 @@ struct GemmParams {
   int64_t ldc, strideCe;
   int c_f32;                // EPI_WGRAD / EPI_STORE: fp32 output
   const int32_t* y_idx;     // EPI_STORE scatter
-  const void* scale;        // EPI_STORE / EPI_SWIGLU_BWD per-row scale
+  const void* scale;        // EPI_STORE / EPI_SWIGLU_BWD per-row scale: fp32, or the activations' 16-bit type
   int scale_f32;
   uint16_t* aux;            // EPI_STORE: yhat (unscaled, sorted); EPI_SWIGLU: gu store
   const uint16_t* gu_in;    // EPI_SWIGLU_BWD: [g | u]

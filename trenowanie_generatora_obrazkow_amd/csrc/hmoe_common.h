@@ -45,6 +45,32 @@ __device__ __forceinline__ uint32_t cvt_bf2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_hw));
 }
 
+// Two floats -> packed fp16 pair, round to nearest even (the conversion torch applies to fp16 tensors).
+typedef _Float16 f16x2_hw __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t cvt_h2(float lo, float hi) {
+  const f32x2_hw v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_hw));
+}
+__device__ __forceinline__ float h_lo(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu)); }
+__device__ __forceinline__ float h_hi(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16)); }
+
+// The 16-bit element type of activations, 16-bit weights, row scales and outputs: bf16 (F16 = false) or fp16.
+// pack2 rounds two floats to a packed pair (nearest even), lo / hi widen the halves of a pair exactly.
+template <bool F16>
+struct Elt {
+  __device__ __forceinline__ static uint32_t pack2(float lo, float hi) { return cvt_bf2(lo, hi); }
+  __device__ __forceinline__ static float lo(uint32_t w) { return bf_lo(w); }
+  __device__ __forceinline__ static float hi(uint32_t w) { return bf_hi(w); }
+  __device__ __forceinline__ static float one(uint16_t b) { return bf2f(b); }
+};
+template <>
+struct Elt<true> {
+  __device__ __forceinline__ static uint32_t pack2(float lo, float hi) { return cvt_h2(lo, hi); }
+  __device__ __forceinline__ static float lo(uint32_t w) { return h_lo(w); }
+  __device__ __forceinline__ static float hi(uint32_t w) { return h_hi(w); }
+  __device__ __forceinline__ static float one(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
+};
+
 // exp for x <= 0 by Cody-Waite reduction (Cephes split of ln 2) + degree-7 Taylor polynomial (Horner, fma) +
 // exponent scaling.  Bit-identical to the host restatement used by the tests: every step is an explicitly rounded
 // IEEE operation.  Arguments below -87 return 0 (results above that are normal floats).

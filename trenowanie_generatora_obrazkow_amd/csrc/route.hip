@@ -572,6 +572,16 @@ __global__ __launch_bounds__(kSgThreads) void route_sigmoid_kernel(const uint16_
 constexpr int kFPB = 256;        // flat rows per histogram block (one wave each: 128 waves at M = 32768)
 constexpr int kMaxEDispatch = 1024;
 
+// routing weight f of topk_w (fp32, bf16 or fp16) rounded to the activations' 16-bit type (fp16 when out_f16, else
+// bf16): the .to(x.dtype) of aurora/hf_compat.py:80; a weight already in that type is copied unchanged
+__device__ __forceinline__ uint16_t route_w16(const void* tw, int tw_dtype, int64_t f, int out_f16) {
+  const uint16_t raw = tw_dtype == HMOE_DT_F32 ? 0 : reinterpret_cast<const uint16_t*>(tw)[f];
+  if (tw_dtype == (out_f16 ? HMOE_DT_F16 : HMOE_DT_BF16)) return raw;
+  const float v = tw_dtype == HMOE_DT_F32 ? reinterpret_cast<const float*>(tw)[f]
+                  : tw_dtype == HMOE_DT_F16 ? Elt<true>::one(raw) : bf2f(raw);
+  return out_f16 ? __builtin_bit_cast(uint16_t, (_Float16)v) : (uint16_t)f2bf(v);
+}
+
 // an int64 id outside the int32 range becomes -1 (invalid) rather than wrapping onto a valid expert
 __device__ __forceinline__ int load_id(const void* ids, int is64, int64_t f) {
   if (is64) {
@@ -744,7 +754,8 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(int32_t* __restrict
 // lookups are in flight together (the per-token pass below visits a token's k rows one after another: at top-8 its
 // lookups are eight dependent round trips per wave).  Same values as the per-token pass.
 __global__ __launch_bounds__(256) void dispatch_index_kernel(const void* __restrict__ ids, int ids64,
-                                                             const void* __restrict__ tw, int tw_dtype, int64_t M,
+                                                             const void* __restrict__ tw, int tw_dtype, int ws_f16,
+                                                             int64_t M,
                                                              int k, int E, const int32_t* __restrict__ blkoff,
                                                              const int32_t* __restrict__ rank,
                                                              int32_t* __restrict__ order, int32_t* __restrict__ a_idx,
@@ -756,9 +767,7 @@ __global__ __launch_bounds__(256) void dispatch_index_kernel(const void* __restr
     if (pos >= 0) {
       order[pos] = (int32_t)f;
       if (a_idx) a_idx[pos] = (int32_t)(f / k);
-      if (w_sorted)
-        w_sorted[pos] = tw_dtype == HMOE_DT_F32 ? (uint16_t)f2bf(reinterpret_cast<const float*>(tw)[f])
-                                                : reinterpret_cast<const uint16_t*>(tw)[f];
+      if (w_sorted) w_sorted[pos] = route_w16(tw, tw_dtype, f, ws_f16);
     }
     if (inv_pos) inv_pos[f] = (int32_t)pos;
   }
@@ -767,7 +776,8 @@ __global__ __launch_bounds__(256) void dispatch_index_kernel(const void* __restr
 // one wave per token: sorted positions of its k rows, index arrays, then the row copies x[t] -> xs[pos_j] and into
 // the row-group tiles (64-byte pieces: slice s of row pos_j, its chunks swizzled as in the K-major LDS image)
 __global__ __launch_bounds__(256) void dispatch_scatter_kernel(
-    const void* __restrict__ ids, int ids64, const void* __restrict__ tw, int tw_dtype, int64_t T, int k, int E,
+    const void* __restrict__ ids, int ids64, const void* __restrict__ tw, int tw_dtype, int ws_f16, int64_t T, int k,
+    int E,
     const int32_t* __restrict__ blkoff, const int32_t* __restrict__ rank, const uint16_t* __restrict__ x,
     int64_t ldx, int64_t d, uint16_t* __restrict__ xs, int32_t* __restrict__ order, int32_t* __restrict__ a_idx,
     int32_t* __restrict__ inv_pos, uint16_t* __restrict__ w_sorted, char* __restrict__ xs_tiles,
@@ -798,14 +808,7 @@ __global__ __launch_bounds__(256) void dispatch_scatter_kernel(
         if (lane == j && pos[j] >= 0) {
           order[pos[j]] = (int32_t)f;
           if (a_idx) a_idx[pos[j]] = (int32_t)t;
-          if (w_sorted) {
-            uint32_t wb;
-            if (tw_dtype == HMOE_DT_F32)
-              wb = f2bf(reinterpret_cast<const float*>(tw)[f]);
-            else
-              wb = reinterpret_cast<const uint16_t*>(tw)[f];
-            w_sorted[pos[j]] = (uint16_t)wb;
-          }
+          if (w_sorted) w_sorted[pos[j]] = route_w16(tw, tw_dtype, f, ws_f16);
         }
         if (lane == j && inv_pos) inv_pos[f] = (int32_t)pos[j];
       }
@@ -875,7 +878,7 @@ __global__ __launch_bounds__(256) void make_schedule_kernel(const void* __restri
 // slot count at compile time: the thread issues its KT row loads before the first sum (KT = 0: a runtime loop).
 // Either way the slots are summed in order j = 0, 1, ..., so the result does not depend on KT.  With inv_pos, a slot
 // whose inv_pos is negative (an expert id outside [0, E): no GEMM wrote its row of y) is read as zeros.
-template <int KT>
+template <int KT, bool F16>
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ y,
                                                       const int32_t* __restrict__ inv_pos, int64_t T, int k,
                                                       int64_t d, const uint16_t* __restrict__ add,
@@ -886,20 +889,23 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
     const int64_t t = i / nvec, c = i - t * nvec;
     const uint4* src = reinterpret_cast<const uint4*>(y + t * k * d) + c;
     float s[8];
+    using X = Elt<F16>;
+    // round to the element type: torch's bf16 rule (NaN -> 0x7fc0) for bf16, nearest even for fp16
+    auto pack = [](float lo, float hi) { return F16 ? cvt_h2(lo, hi) : pack_bf2(lo, hi); };
     auto first = [&](const uint4 v) {
       const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        s[2 * q] = bf_lo(w[q]);
-        s[2 * q + 1] = bf_hi(w[q]);
+        s[2 * q] = X::lo(w[q]);
+        s[2 * q + 1] = X::hi(w[q]);
       }
     };
     auto accum = [&](const uint4 v) {
       const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        s[2 * q] += bf_lo(w[q]);
-        s[2 * q + 1] += bf_hi(w[q]);
+        s[2 * q] += X::lo(w[q]);
+        s[2 * q + 1] += X::hi(w[q]);
       }
     };
     const uint4 a = add ? reinterpret_cast<const uint4*>(add + t * d)[c] : make_uint4(0, 0, 0, 0);
@@ -918,16 +924,16 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
       for (int j = 1; j < k; ++j) accum(row(j));
     }
     uint4 o;
-    o.x = pack_bf2(s[0], s[1]);
-    o.y = pack_bf2(s[2], s[3]);
-    o.z = pack_bf2(s[4], s[5]);
-    o.w = pack_bf2(s[6], s[7]);
+    o.x = pack(s[0], s[1]);
+    o.y = pack(s[2], s[3]);
+    o.z = pack(s[4], s[5]);
+    o.w = pack(s[6], s[7]);
     if (add) {
       const uint32_t av[4] = {a.x, a.y, a.z, a.w};
       uint32_t ov[4] = {o.x, o.y, o.z, o.w};
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        ov[q] = pack_bf2(__fadd_rn(bf_lo(ov[q]), bf_lo(av[q])), __fadd_rn(bf_hi(ov[q]), bf_hi(av[q])));
+        ov[q] = pack(__fadd_rn(X::lo(ov[q]), X::lo(av[q])), __fadd_rn(X::hi(ov[q]), X::hi(av[q])));
       o = make_uint4(ov[0], ov[1], ov[2], ov[3]);
     }
     reinterpret_cast<uint4*>(out + t * d)[c] = o;
@@ -1412,11 +1418,12 @@ static inline int grid_for(int64_t work, int per_block, int cap = 8192) {
 
 static inline bool al16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+template <bool F16>
 static void combine_launch(const uint16_t* y, const int32_t* inv_pos, int64_t T, int k, int64_t d,
                            const uint16_t* add, uint16_t* out, int64_t work, hipStream_t s) {
   const dim3 grid(grid_for(work, 256, 65536));
 #define HMOE_COMBINE(KT) \
-  hipLaunchKernelGGL((combine_kernel<KT>), grid, dim3(256), 0, s, y, inv_pos, T, k, d, add, out)
+  hipLaunchKernelGGL((combine_kernel<KT, F16>), grid, dim3(256), 0, s, y, inv_pos, T, k, d, add, out)
   switch (k) {
     case 1: HMOE_COMBINE(1); break;
     case 2: HMOE_COMBINE(2); break;
@@ -1512,12 +1519,14 @@ static int dispatch_impl(const void* topk_ids, int ids_dtype, const void* topk_w
                          const void* x, int64_t ldx, int64_t d, void* xs, void* xs_tiles, int32_t* counts,
                          int64_t* counts64, int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos,
                          uint16_t* w_sorted, int32_t* n_invalid, void* workspace, size_t workspace_bytes,
-                         hipStream_t s) {
+                         int dtype, hipStream_t s) {
   if (T < 0 || k <= 0 || E <= 0) return HMOE_ERR_ARG;
   if (E > kMaxEDispatch || k > kMaxK) return HMOE_ERR_SHAPE;
   if (!counts || !starts) return HMOE_ERR_ARG;
   if (ids_dtype != HMOE_DT_I32 && ids_dtype != HMOE_DT_I64) return HMOE_ERR_DTYPE;
-  if (topk_w && w_dtype != HMOE_DT_F32 && w_dtype != HMOE_DT_BF16) return HMOE_ERR_DTYPE;
+  if (topk_w && w_dtype != HMOE_DT_F32 && w_dtype != HMOE_DT_BF16 && w_dtype != HMOE_DT_F16) return HMOE_ERR_DTYPE;
+  if (dtype != HMOE_DT_BF16 && dtype != HMOE_DT_F16) return HMOE_ERR_DTYPE;
+  const bool f16 = dtype == HMOE_DT_F16;
   if (w_sorted && !topk_w) return HMOE_ERR_ARG;
   const int64_t M = T * k;
   if (M > INT32_MAX) return HMOE_ERR_SHAPE;
@@ -1546,14 +1555,14 @@ static int dispatch_impl(const void* topk_ids, int ids_dtype, const void* topk_w
   HMOE_CHECK_LAUNCH();
   if (M > 0 && (xs || xs_tiles)) {
     const int grid = grid_for(T, 4, 8192);
-    hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(grid), dim3(256), 0, s, topk_ids, ids64, topk_w, w_dtype, T, k,
-                       E, hist, rank, static_cast<const uint16_t*>(x), ldx, d, static_cast<uint16_t*>(xs), order,
+    hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(grid), dim3(256), 0, s, topk_ids, ids64, topk_w, w_dtype,
+                       (int)f16, T, k, E, hist, rank, static_cast<const uint16_t*>(x), ldx, d, static_cast<uint16_t*>(xs), order,
                        a_idx, inv_pos, w_sorted,
                        static_cast<char*>(xs_tiles), starts, gstart);
     HMOE_CHECK_LAUNCH();
   } else if (M > 0) {
     hipLaunchKernelGGL(dispatch_index_kernel, dim3(grid_for(M, 256, 8192)), dim3(256), 0, s, topk_ids, ids64, topk_w,
-                       w_dtype, M, k, E, hist, rank, order, a_idx, inv_pos, w_sorted);
+                       w_dtype, (int)f16, M, k, E, hist, rank, order, a_idx, inv_pos, w_sorted);
     HMOE_CHECK_LAUNCH();
   }
   return HMOE_OK;
@@ -1655,9 +1664,9 @@ size_t hmoe_dispatch_workspace_size(int64_t T, int k, int E) { return dispatch_w
 int hmoe_dispatch(const void* topk_ids, int ids_dtype, const void* topk_w, int w_dtype, int64_t T, int k, int E,
                   const void* x, int64_t ldx, int64_t d, void* xs, int32_t* counts, int64_t* counts64,
                   int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos, uint16_t* w_sorted,
-                  int32_t* n_invalid, void* workspace, size_t workspace_bytes, hmoe_stream_t stream) {
+                  int32_t* n_invalid, void* workspace, size_t workspace_bytes, int dtype, hmoe_stream_t stream) {
   return dispatch_impl(topk_ids, ids_dtype, topk_w, w_dtype, T, k, E, x, ldx, d, xs, nullptr, counts, counts64, starts,
-                       order, a_idx, inv_pos, w_sorted, n_invalid, workspace, workspace_bytes,
+                       order, a_idx, inv_pos, w_sorted, n_invalid, workspace, workspace_bytes, dtype,
                        reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -1668,17 +1677,17 @@ size_t hmoe_xs_tiles_bytes(int64_t M, int E, int64_t d) {
 int hmoe_dispatch_tiles(const void* topk_ids, int ids_dtype, const void* topk_w, int w_dtype, int64_t T, int k, int E,
                         const void* x, int64_t ldx, int64_t d, void* xs, void* xs_tiles, int32_t* counts,
                         int64_t* counts64, int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos,
-                        uint16_t* w_sorted, int32_t* n_invalid, void* workspace, size_t workspace_bytes,
+                        uint16_t* w_sorted, int32_t* n_invalid, void* workspace, size_t workspace_bytes, int dtype,
                         hmoe_stream_t stream) {
   return dispatch_impl(topk_ids, ids_dtype, topk_w, w_dtype, T, k, E, x, ldx, d, xs, xs_tiles, counts, counts64,
-                       starts, order, a_idx, inv_pos, w_sorted, n_invalid, workspace, workspace_bytes,
+                       starts, order, a_idx, inv_pos, w_sorted, n_invalid, workspace, workspace_bytes, dtype,
                        reinterpret_cast<hipStream_t>(stream));
 }
 
 int hmoe_dispatch_noalloc(const void* topk_ids, int ids_dtype, const void* topk_w, int w_dtype, int64_t T, int k,
                           int E, const void* x, int64_t ldx, int64_t d, void* xs, int32_t* counts, int64_t* counts64,
                           int32_t* starts, int32_t* order, int32_t* a_idx, int32_t* inv_pos, uint16_t* w_sorted,
-                          int32_t* n_invalid, hmoe_stream_t stream) {
+                          int32_t* n_invalid, int dtype, hmoe_stream_t stream) {
   if (T < 0 || k <= 0 || E <= 0) return HMOE_ERR_ARG;
   if (E > kMaxEDispatch || k > kMaxK) return HMOE_ERR_SHAPE;
   if (T > INT32_MAX / k || dispatch_ws_bytes(T, k, E) > kDispatchScratchBytes) return HMOE_ERR_TOO_LARGE;
@@ -1686,7 +1695,7 @@ int hmoe_dispatch_noalloc(const void* topk_ids, int ids_dtype, const void* topk_
   void* ws = dispatch_scratch(&rc);
   if (rc) return rc;
   return dispatch_impl(topk_ids, ids_dtype, topk_w, w_dtype, T, k, E, x, ldx, d, xs, nullptr, counts, counts64, starts,
-                       order, a_idx, inv_pos, w_sorted, n_invalid, ws, kDispatchScratchBytes,
+                       order, a_idx, inv_pos, w_sorted, n_invalid, ws, kDispatchScratchBytes, dtype,
                        reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -1703,27 +1712,38 @@ int hmoe_make_schedule(const void* counts, int counts_dtype, int E, int64_t M, i
   return HMOE_OK;
 }
 
-int hmoe_combine(const void* y, const int32_t* inv_pos, int64_t T, int k, int64_t d, void* out,
+int hmoe_combine(const void* y, const int32_t* inv_pos, int64_t T, int k, int64_t d, void* out, int dtype,
                  hmoe_stream_t stream) {
   if (T < 0 || k <= 0 || d <= 0) return HMOE_ERR_ARG;
+  if (dtype != HMOE_DT_BF16 && dtype != HMOE_DT_F16) return HMOE_ERR_DTYPE;
   if (T == 0) return HMOE_OK;
   if (!y || !out || d % 8 || !al16(y) || !al16(out)) return HMOE_ERR_ARG;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int64_t work = T * (d / 8);
-  combine_launch(static_cast<const uint16_t*>(y), inv_pos, T, k, d, nullptr, static_cast<uint16_t*>(out), work, s);
+  if (dtype == HMOE_DT_F16)
+    combine_launch<true>(static_cast<const uint16_t*>(y), inv_pos, T, k, d, nullptr, static_cast<uint16_t*>(out), work,
+                         s);
+  else
+    combine_launch<false>(static_cast<const uint16_t*>(y), inv_pos, T, k, d, nullptr, static_cast<uint16_t*>(out), work,
+                          s);
   HMOE_CHECK_LAUNCH();
   return HMOE_OK;
 }
 
 int hmoe_combine_add(const void* y, const int32_t* inv_pos, int64_t T, int k, int64_t d, const void* add, void* out,
-                     hmoe_stream_t stream) {
+                     int dtype, hmoe_stream_t stream) {
   if (T < 0 || k <= 0 || d <= 0) return HMOE_ERR_ARG;
+  if (dtype != HMOE_DT_BF16 && dtype != HMOE_DT_F16) return HMOE_ERR_DTYPE;
   if (T == 0) return HMOE_OK;
   if (!y || !add || !out || d % 8 || !al16(y) || !al16(add) || !al16(out)) return HMOE_ERR_ARG;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int64_t work = T * (d / 8);
-  combine_launch(static_cast<const uint16_t*>(y), inv_pos, T, k, d, static_cast<const uint16_t*>(add),
-                 static_cast<uint16_t*>(out), work, s);
+  if (dtype == HMOE_DT_F16)
+    combine_launch<true>(static_cast<const uint16_t*>(y), inv_pos, T, k, d, static_cast<const uint16_t*>(add),
+                         static_cast<uint16_t*>(out), work, s);
+  else
+    combine_launch<false>(static_cast<const uint16_t*>(y), inv_pos, T, k, d, static_cast<const uint16_t*>(add),
+                          static_cast<uint16_t*>(out), work, s);
   HMOE_CHECK_LAUNCH();
   return HMOE_OK;
 }

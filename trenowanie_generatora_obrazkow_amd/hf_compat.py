@@ -74,11 +74,12 @@ def _self_test(fn, device, dtype, quant=False):
 
 
 def _pick_mode(device, dtype):
-    """aurora/hf_compat.py:124-139, with one mode: "hip" on a ROCm GPU once the known-answer test passes."""
+    """aurora/hf_compat.py:124-139, with one mode: "hip" on a ROCm GPU once the known-answer tests pass in the
+    activations' dtype (bf16 or fp16)."""
     if device.type != "cuda":
         raise RuntimeError("hmoe fused MoE needs a ROCm GPU device (the kernels have no CPU path)")
-    if dtype != torch.bfloat16:
-        raise TypeError(f"hmoe fused MoE runs bf16 activations (got {dtype})")
+    if dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"hmoe fused MoE runs bf16 or fp16 activations (got {dtype})")
     fn = lambda a, w, s, c: grouped_mm(a, w, c, w_scale=s)
     if not (_self_test(fn, device, dtype) and _self_test(fn, device, dtype, quant=True)):
         raise RuntimeError("hmoe grouped_mm failed its known-answer self-test on this device")

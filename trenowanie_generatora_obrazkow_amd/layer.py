@@ -13,7 +13,8 @@ Backward:
   the k slots) + router input gradient.
 
 The kernels compute in bf16 with fp32 accumulation.  fp32 weights (master weights) are rounded to bf16 for the
-products, as torch.autocast does for the reference's nn.Linear layers, and receive fp32 gradients.
+products, as torch.autocast does for the reference's nn.Linear layers, and receive fp32 gradients; fp16 weights
+are rounded to bf16 the same way and receive their fp32 gradients rounded once to fp16.
 """
 from __future__ import annotations
 
@@ -22,7 +23,17 @@ import torch.nn as nn
 
 from . import ops
 
-_WDTYPES = (torch.bfloat16, torch.float32)
+_WDTYPES = (torch.bfloat16, torch.float32, torch.float16)
+
+
+def _grad_dtype(param_dtype):
+    """dtype a weight gradient is computed in: the parameter's own for bf16 / fp32, fp32 for fp16 parameters (the
+    kernels write bf16 or fp32; the fp32 sum is then rounded once to fp16)."""
+    return torch.float32 if param_dtype == torch.float16 else param_dtype
+
+
+def _to_param(g, param_dtype):
+    return g if g is None or g.dtype == param_dtype else g.to(param_dtype)
 
 
 def _check_layer_args(x, wr, wgu, wd, bias, k):
@@ -39,7 +50,7 @@ def _check_layer_args(x, wr, wgu, wd, bias, k):
         if tuple(t.shape) != shape:
             raise ValueError(f"{name}: shape {tuple(t.shape)}, expected {shape} (E={E}, d={d}, h={h})")
         if t.dtype not in _WDTYPES:
-            raise TypeError(f"{name}: dtype {t.dtype}; the layer takes bf16 or fp32 weights")
+            raise TypeError(f"{name}: dtype {t.dtype}; the layer takes bf16, fp32 or fp16 weights")
     if bias is not None and tuple(bias.shape) != (E,):
         raise ValueError(f"logit_bias: shape {tuple(bias.shape)}, expected ({E},)")
     if not 1 <= k <= E:
@@ -94,16 +105,17 @@ class _MoEFunction(torch.autograd.Function):
         dys, _ = ops.combine_bwd(dout, None, disp, k)
         dwd = dwgu = None
         if ctx.needs_input_grad[3]:
-            dwd = ops.grouped_wgrad(act, dys, counts, E, dtype=wd_dt)
+            dwd = _to_param(ops.grouped_wgrad(act, dys, counts, E, dtype=_grad_dtype(wd_dt)), wd_dt)
         # dgu, and the routing-weight gradient <dout[t], act[r] @ wd[e]> from the same fp32 product
         dgu, dtw = ops.down_dgrad_swiglu_dw(dout, wd, counts, M, gu, order, k, a_idx=a_idx, w_sorted=w_sorted)
         if dtw_out is not None:  # the returned routing weights are outputs too: their gradient joins the combine's
             dtw = dtw + dtw_out.to(torch.float32)
         if ctx.needs_input_grad[2]:
-            dwgu = ops.grouped_wgrad(xs, dgu, counts, E, dtype=wgu_dt)
+            dwgu = _to_param(ops.grouped_wgrad(xs, dgu, counts, E, dtype=_grad_dtype(wgu_dt)), wgu_dt)
         dxs = ops.gate_up_dgrad(dgu, wgu, counts, M)
-        dl, dwr = ops.router_bwd(logits, ids, dtw, x, renorm=ctx.renorm, dwr_dtype=wr_dt,
+        dl, dwr = ops.router_bwd(logits, ids, dtw, x, renorm=ctx.renorm, dwr_dtype=_grad_dtype(wr_dt),
                                  want_dwr=ctx.needs_input_grad[1])
+        dwr = _to_param(dwr, wr_dt)
         dx = ops.unpermute_bwd(dxs, inv_pos, T, k, dlogits=dl, wr=wr) if ctx.needs_input_grad[0] else None
         return dx, dwr, dwgu, dwd, None, None, None
 
@@ -111,8 +123,8 @@ class _MoEFunction(torch.autograd.Function):
 def moe_swiglu(x, router_weight, w_gu, w_d, top_k, logit_bias=None, renorm=True):
     """Functional form: x (T, d) bf16 -> (out (T, d) bf16, topk_ids (T, k) int32, topk_weight (T, k) fp32).
 
-    router_weight (E, d), w_gu (E, d, 2h) = [gate | up], w_d (E, h, d): bf16, or fp32 (rounded to bf16 for the
-    products, gradients in fp32).  logit_bias (E,) fp32 is added to the router logits (no gradient).  Gradients reach
+    router_weight (E, d), w_gu (E, d, 2h) = [gate | up], w_d (E, h, d): bf16, or fp32 / fp16 (rounded to bf16 for
+    the products, gradients in the weights' dtype).  logit_bias (E,) fp32 is added to the router logits (no gradient).  Gradients reach
     x and the three weights from `out` and from `topk_weight` (softmax + renormalisation Jacobian)."""
     return _MoEFunction.apply(x, router_weight, w_gu, w_d, logit_bias, top_k, renorm)
 

@@ -35,14 +35,16 @@ def grouped_mm(a: torch.Tensor, w: torch.Tensor, counts: torch.Tensor, sched=Non
     names the row to read --, w (E, K, N) with contiguous rows, counts (E,) rows per expert (sum = M) -> (M, N) of
     a.dtype.  scale[r] multiplies output row r; y_idx[r] is where row r is written.  `sched` (make_schedule's
     output) is accepted for call compatibility; the kernel derives its own tile map from `counts` on the device.
-    w may be int8 with w_scale (E, N) (aurora/moe_triton.py:44-51): the integers enter the bf16 products exactly and
-    the per-column scale multiplies the fp32 sum, before `scale`."""
+    a is bf16 or fp16 (the products run on the matching MFMA, the output has a's type); w has a's type, or is int8
+    with w_scale (E, N) (aurora/moe_triton.py:44-51): the integers enter the 16-bit products exactly and the
+    per-column scale multiplies the fp32 sum, before `scale`."""
     M = a_idx.numel() if a_idx is not None else a.shape[0]
     assert w.stride(2) == 1, "w must be (E, K, N) with contiguous rows"
-    if a.dtype != torch.bfloat16 or w.dtype not in (torch.bfloat16, torch.int8):
-        raise TypeError(f"hmoe grouped_mm supports bf16 a and bf16 or int8 w (got {a.dtype}, {w.dtype})")
+    if a.dtype not in (torch.bfloat16, torch.float16) or w.dtype not in (a.dtype, torch.int8):
+        raise TypeError(f"hmoe grouped_mm supports bf16 or fp16 a with w of a's type or int8 (got {a.dtype}, "
+                        f"{w.dtype})")
     if (w.dtype == torch.int8) != (w_scale is not None):
-        raise ValueError("int8 weights need w_scale (E, N); bf16 weights take none")
+        raise ValueError("int8 weights need w_scale (E, N); 16-bit weights take none")
     a = a.contiguous()
     if a_idx is not None and a_idx.dtype != torch.int32:
         a_idx = a_idx.to(torch.int32)

@@ -77,7 +77,16 @@ def _need(t, name, shape=None, dtypes=None, contig=True, min_rows=None):
 
 
 _BF16 = (torch.bfloat16,)
+_H16 = (torch.bfloat16, torch.float16)  # the activation types of the forward kernels
 _I32 = (torch.int32,)
+
+
+def _act_dtype(t, name):
+    """The 16-bit activation type of a forward call (bf16 or fp16), as the C code of the entry points' dtype."""
+    if t.dtype not in _H16:
+        raise TypeError(f"{name}: the hmoe forward kernels take bf16 or fp16 activations (got {t.dtype})")
+    return L.dt(t)
+
 
 
 def _rows_index(idx, name, M):
@@ -151,11 +160,12 @@ class Dispatch:
 
 
 def dispatch(topk_ids: torch.Tensor, E: int, topk_w=None, x=None, want_counts64=False, want_inv=True,
-             want_xs=True, want_tiles=False) -> Dispatch:
+             want_xs=True, want_tiles=False, dtype=None) -> Dispatch:
     """Stable counting sort of the flat routed rows (aurora/hf_compat.py:69-72, 78, 80) and optionally, with x, the
     row permutation xs = x[a_idx] (want_xs) and the same rows as row-group tiles for gate_up_swiglu_tiles
     (want_tiles).  Expert ids outside [0, E) route nowhere (inv_pos -1, counted in no expert); their number is left
-    on the device in n_invalid, read without a host sync only when the caller asks."""
+    on the device in n_invalid, read without a host sync only when the caller asks.  The sorted routing weights (and
+    the copied rows) have x's type, bf16 or fp16 (dtype without x; bf16 by default)."""
     T, k = topk_ids.shape
     M = T * k
     dev = topk_ids.device
@@ -165,33 +175,39 @@ def dispatch(topk_ids: torch.Tensor, E: int, topk_w=None, x=None, want_counts64=
         if tuple(topk_w.shape) != (T, k):
             raise ValueError(f"topk_weight: shape {tuple(topk_w.shape)}, expected {(T, k)}")
         topk_w = _contig(topk_w, "topk_weight")
-        if topk_w.dtype not in (torch.float32, torch.bfloat16):
+        if topk_w.dtype not in (torch.float32, torch.bfloat16, torch.float16):
             topk_w = topk_w.float()
+    if x is not None:
+        dtype = x.dtype
+    dtype = torch.bfloat16 if dtype is None else dtype
+    if dtype not in _H16:
+        raise TypeError(f"dispatch: activations must be bf16 or fp16 (got {dtype})")
     counts = torch.empty(E, device=dev, dtype=torch.int32)
     counts64 = torch.empty(E, device=dev, dtype=torch.int64) if want_counts64 else None
     starts = torch.empty(E + 1, device=dev, dtype=torch.int32)
     order = torch.empty(M, device=dev, dtype=torch.int32)
     a_idx = torch.empty(M, device=dev, dtype=torch.int32)
     inv = torch.empty(M, device=dev, dtype=torch.int32) if want_inv else None
-    w_sorted = torch.empty(M, device=dev, dtype=torch.bfloat16) if topk_w is not None else None
+    w_sorted = torch.empty(M, device=dev, dtype=dtype) if topk_w is not None else None
     n_invalid = torch.empty(1, device=dev, dtype=torch.int32)
     xs = tiles = None
     d = 0
     ldx = 0
     if x is not None:
-        _need(x, "x", (T, None), _BF16, contig=False)  # xs = x[a_idx] reads rows a_idx < T
+        _need(x, "x", (T, None), _H16, contig=False)  # xs = x[a_idx] reads rows a_idx < T
         d = x.shape[1]
         ldx = x.stride(0)
         if want_xs:
-            xs = torch.empty(M, d, device=dev, dtype=torch.bfloat16)
+            xs = torch.empty(M, d, device=dev, dtype=dtype)
         if want_tiles:
-            tiles = torch.empty(L.lib().hmoe_xs_tiles_bytes(M, E, d) // 2, device=dev, dtype=torch.bfloat16)
+            tiles = torch.empty(L.lib().hmoe_xs_tiles_bytes(M, E, d) // 2, device=dev, dtype=dtype)
     ws_bytes = L.lib().hmoe_dispatch_workspace_size(T, k, E)
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
     with _Probe("dispatch"):
         L.call("hmoe_dispatch_tiles", L.ptr(ids), L.dt(ids), L.ptr(topk_w), L.dt(topk_w) if topk_w is not None else 0,
                T, k, E, L.ptr(x), ldx, d, L.ptr(xs), L.ptr(tiles), L.ptr(counts), L.ptr(counts64), L.ptr(starts),
-               L.ptr(order), L.ptr(a_idx), L.ptr(inv), L.ptr(w_sorted), L.ptr(n_invalid), L.ptr(ws), ws_bytes, s)
+               L.ptr(order), L.ptr(a_idx), L.ptr(inv), L.ptr(w_sorted), L.ptr(n_invalid), L.ptr(ws), ws_bytes,
+               L.dt(dtype), s)
     return Dispatch(counts, counts64, starts, order, a_idx, inv, w_sorted, xs, tiles, n_invalid)
 
 
@@ -218,10 +234,11 @@ def _counts(counts, E):
 def grouped_mm(a, w, counts, M, a_idx=None, y_idx=None, scale=None, w_scale=None, out=None):
     """y[y_idx[r] or r] = (a[a_idx[r] or r] @ w[e(r)]) * w_scale[e(r)] * scale[r], y (M, N) bf16.  The index
     values are trusted (in range: a_idx < rows of a, y_idx < M); everything else is checked here."""
-    if w.dim() != 3 or w.dtype not in (torch.bfloat16, torch.int8):
-        raise TypeError(f"w must be an (E, K, N) bf16 or int8 stack (got {tuple(w.shape)} {w.dtype})")
+    if w.dim() != 3 or w.dtype not in (a.dtype, torch.int8):
+        raise TypeError(f"w must be an (E, K, N) stack of a's type or int8 (got {tuple(w.shape)} {w.dtype})")
     E, K, N = w.shape
     s = _dev_stream(a)
+    _act_dtype(a, "a")
     counts = _counts(counts, E)
     if a.stride(1) != 1:
         a = a.contiguous()
@@ -229,7 +246,7 @@ def grouped_mm(a, w, counts, M, a_idx=None, y_idx=None, scale=None, w_scale=None
         w = w.contiguous()
     a_idx = _rows_index(a_idx, "a_idx", M)
     y_idx = _rows_index(y_idx, "y_idx", M)
-    _need(a, "a", (None, K), _BF16, contig=False, min_rows=min(1, M) if a_idx is not None else M)
+    _need(a, "a", (None, K), _H16, contig=False, min_rows=min(1, M) if a_idx is not None else M)
     if a_idx is not None and a.shape[0] * a.stride(0) * 2 >= 2 ** 31:
         raise ValueError("a gathered through a_idx must span less than 2 GiB (32-bit row offsets)")
     if w_scale is not None:
@@ -237,11 +254,11 @@ def grouped_mm(a, w, counts, M, a_idx=None, y_idx=None, scale=None, w_scale=None
         if w_scale.shape != (E, N):
             raise ValueError(f"w_scale must be (E, N) = {(E, N)}, got {tuple(w_scale.shape)}")
     if out is not None:
-        _need(out, "out", (M, N), _BF16, contig=False)
+        _need(out, "out", (M, N), (a.dtype,), contig=False)
     y = out if out is not None else torch.empty(M, N, device=a.device, dtype=a.dtype)
     if scale is not None:
         scale = _contig(scale, "scale")
-        if scale.dtype not in (torch.bfloat16, torch.float32):
+        if scale.dtype not in (a.dtype, torch.float32):
             scale = scale.float()
         _need(scale, "scale", (M,))
     with _Probe("grouped_mm"):
@@ -266,46 +283,49 @@ def _w_scale(w, w_s, n):
 def gate_up_swiglu(x, wgu, counts, M, a_idx=None, keep_gu=False, wgu_s=None):
     """act = bf16(bf16(silu(g)) * u) for [g | u] = x[a_idx] @ wgu[e]; wgu bf16, or int8 with per-column scales
     wgu_s (E, 2h) (inference only: no gu)."""
-    if wgu.dim() != 3 or wgu.dtype not in (torch.bfloat16, torch.int8) or wgu.shape[2] % 2:
-        raise TypeError(f"wgu must be an (E, d, 2h) bf16 or int8 stack (got {tuple(wgu.shape)} {wgu.dtype})")
+    if wgu.dim() != 3 or wgu.dtype not in (x.dtype, torch.int8) or wgu.shape[2] % 2:
+        raise TypeError(f"wgu must be an (E, d, 2h) stack of x's type or int8 (got {tuple(wgu.shape)} {wgu.dtype})")
     E, d, h2 = wgu.shape
     h = h2 // 2
     s = _dev_stream(x)
+    dt = _act_dtype(x, "x")
     wgu = _contig(wgu, "wgu")
     counts = _counts(counts, E)
     wgu_s = _w_scale(wgu, wgu_s, h2)
     a_idx = _rows_index(a_idx, "a_idx", M)
-    _need(x, "x", (None, d), _BF16, contig=False, min_rows=min(1, M) if a_idx is not None else M)
-    act = torch.empty(M, h, device=x.device, dtype=torch.bfloat16)
+    _need(x, "x", (None, d), _H16, contig=False, min_rows=min(1, M) if a_idx is not None else M)
+    act = torch.empty(M, h, device=x.device, dtype=x.dtype)
     if wgu_s is not None:
         if keep_gu:
             raise ValueError("int8 weights are inference only (no gu kept)")
         with _Probe("gate_up_swiglu"):
             L.call("hmoe_gate_up_swiglu_i8", L.ptr(x), x.stride(0), L.ptr(a_idx), L.ptr(wgu), L.ptr(wgu_s),
-                   L.dt(wgu_s), E, d, h, L.ptr(counts), L.dt(counts), M, L.ptr(act), s)
+                   L.dt(wgu_s), E, d, h, L.ptr(counts), L.dt(counts), M, L.ptr(act), dt, s)
         return act, None
-    gu = torch.empty(M, h2, device=x.device, dtype=torch.bfloat16) if keep_gu else None
+    gu = torch.empty(M, h2, device=x.device, dtype=x.dtype) if keep_gu else None
     with _Probe("gate_up_swiglu"):
         L.call("hmoe_gate_up_swiglu", L.ptr(x), x.stride(0), L.ptr(a_idx), L.ptr(wgu), E, d, h, L.ptr(counts),
-               L.dt(counts), M, L.ptr(act), L.ptr(gu), s)
+               L.dt(counts), M, L.ptr(act), L.ptr(gu), dt, s)
     return act, gu
 
 
 def gate_up_swiglu_tiles(xs_tiles, wgu, counts, M, keep_gu=False):
-    """gate_up_swiglu on the row-group tiles a dispatch(want_tiles=True) wrote (bf16 weights): identical act / gu."""
-    if wgu.dim() != 3 or wgu.dtype != torch.bfloat16 or wgu.shape[2] % 2:
-        raise TypeError(f"wgu must be an (E, d, 2h) bf16 stack (got {tuple(wgu.shape)} {wgu.dtype})")
+    """gate_up_swiglu on the row-group tiles a dispatch(want_tiles=True) wrote (16-bit weights of the tiles' type):
+    identical act / gu."""
+    if wgu.dim() != 3 or wgu.dtype != xs_tiles.dtype or wgu.shape[2] % 2:
+        raise TypeError(f"wgu must be an (E, d, 2h) stack of the tiles' type (got {tuple(wgu.shape)} {wgu.dtype})")
     E, d, h2 = wgu.shape
     h = h2 // 2
     s = _dev_stream(xs_tiles)
+    dt = _act_dtype(xs_tiles, "xs_tiles")
     wgu = _contig(wgu, "wgu")
     counts = _counts(counts, E)
-    _need(xs_tiles, "xs_tiles", (L.lib().hmoe_xs_tiles_bytes(M, E, d) // 2,), _BF16)
-    act = torch.empty(M, h, device=xs_tiles.device, dtype=torch.bfloat16)
-    gu = torch.empty(M, h2, device=xs_tiles.device, dtype=torch.bfloat16) if keep_gu else None
+    _need(xs_tiles, "xs_tiles", (L.lib().hmoe_xs_tiles_bytes(M, E, d) // 2,), _H16)
+    act = torch.empty(M, h, device=xs_tiles.device, dtype=xs_tiles.dtype)
+    gu = torch.empty(M, h2, device=xs_tiles.device, dtype=xs_tiles.dtype) if keep_gu else None
     with _Probe("gate_up_swiglu"):
         L.call("hmoe_gate_up_swiglu_tiles", L.ptr(xs_tiles), L.ptr(wgu), E, d, h, L.ptr(counts), L.dt(counts), M,
-               L.ptr(act), L.ptr(gu), s)
+               L.ptr(act), L.ptr(gu), dt, s)
     return act, gu
 
 
@@ -325,10 +345,10 @@ def routed_gate_up(x, ids, E, wgu, topk_w=None, wgu_s=None, keep_gu=False, want_
     M = T * k
     d = x.shape[1]
     h = wgu.shape[2] // 2
-    tiles = (wgu_s is None and wgu.dtype == torch.bfloat16 and h >= TILES_MIN_H
+    tiles = (wgu_s is None and wgu.dtype == x.dtype and h >= TILES_MIN_H
              and L.lib().hmoe_xs_tiles_bytes(M, E, d) < (1 << 31))
     disp = dispatch(ids, E, topk_w=topk_w, x=x if (tiles or want_xs) else None, want_inv=want_inv, want_xs=want_xs,
-                    want_tiles=tiles)
+                    want_tiles=tiles, dtype=x.dtype)
     if tiles:
         act, gu = gate_up_swiglu_tiles(disp.xs_tiles, wgu, disp.counts, M, keep_gu=keep_gu)
         disp.xs_tiles = None  # read once: not kept alive with the dispatch
@@ -341,29 +361,30 @@ def routed_gate_up(x, ids, E, wgu, topk_w=None, wgu_s=None, keep_gu=False, want_
 
 def down_scatter(act, wd, counts, M, w_sorted, y_idx, keep_yhat=False, wd_s=None):
     """y[y_idx[r]] = bf16(act[r] @ wd[e] * w_sorted[r]); wd bf16, or int8 with per-column scales wd_s (E, d)."""
-    if wd.dim() != 3 or wd.dtype not in (torch.bfloat16, torch.int8):
-        raise TypeError(f"wd must be an (E, h, d) bf16 or int8 stack (got {tuple(wd.shape)} {wd.dtype})")
+    if wd.dim() != 3 or wd.dtype not in (act.dtype, torch.int8):
+        raise TypeError(f"wd must be an (E, h, d) stack of act's type or int8 (got {tuple(wd.shape)} {wd.dtype})")
     E, h, d = wd.shape
     s = _dev_stream(act)
+    dt = _act_dtype(act, "act")
     wd = _contig(wd, "wd")
     counts = _counts(counts, E)
     wd_s = _w_scale(wd, wd_s, d)
-    _need(act, "act", (M, h), _BF16)
+    _need(act, "act", (M, h), _H16)
     y_idx = _rows_index(y_idx, "y_idx", M)
     if w_sorted is not None:
-        _need(w_sorted, "w_sorted", (M,), _BF16)
-    y = torch.empty(M, d, device=act.device, dtype=torch.bfloat16)
+        _need(w_sorted, "w_sorted", (M,), (act.dtype,))
+    y = torch.empty(M, d, device=act.device, dtype=act.dtype)
     if wd_s is not None:
         if keep_yhat:
             raise ValueError("int8 weights are inference only (no yhat kept)")
         with _Probe("down_scatter"):
             L.call("hmoe_down_scatter_i8", L.ptr(act), L.ptr(wd), L.ptr(wd_s), L.dt(wd_s), E, h, d, L.ptr(counts),
-                   L.dt(counts), M, L.ptr(w_sorted), L.ptr(y_idx), L.ptr(y), s)
+                   L.dt(counts), M, L.ptr(w_sorted), L.ptr(y_idx), L.ptr(y), dt, s)
         return y, None
-    yhat = torch.empty(M, d, device=act.device, dtype=torch.bfloat16) if keep_yhat else None
+    yhat = torch.empty(M, d, device=act.device, dtype=act.dtype) if keep_yhat else None
     with _Probe("down_scatter"):
         L.call("hmoe_down_scatter", L.ptr(act), L.ptr(wd), E, h, d, L.ptr(counts), L.dt(counts), M, L.ptr(w_sorted),
-               L.ptr(y_idx), L.ptr(y), L.ptr(yhat), s)
+               L.ptr(y_idx), L.ptr(y), L.ptr(yhat), dt, s)
     return y, yhat
 
 
@@ -371,17 +392,18 @@ def combine(y, T, k, add=None, inv_pos=None):
     """out[t] = bf16(sum_j y[t*k + j]) (+ add[t], rounded once more: bf16 + bf16).  inv_pos (T*k,) from the dispatch:
     slots routed nowhere (inv_pos < 0: an expert id outside [0, E)) add zeros instead of their unwritten rows."""
     d = y.shape[1]
-    _need(y, "y", (T * k, d), _BF16)
+    _need(y, "y", (T * k, d), _H16)
+    dt = _act_dtype(y, "y")
     inv_pos = _rows_index(inv_pos, "inv_pos", T * k)
     out = torch.empty(T, d, device=y.device, dtype=y.dtype)
     with _Probe("combine"):
         if add is None:
-            L.call("hmoe_combine", L.ptr(_contig(y, "y")), L.ptr(inv_pos), T, k, d, L.ptr(out), _dev_stream(y))
+            L.call("hmoe_combine", L.ptr(_contig(y, "y")), L.ptr(inv_pos), T, k, d, L.ptr(out), dt, _dev_stream(y))
         else:
-            if add.shape != (T, d) or add.dtype != torch.bfloat16:
-                raise ValueError(f"add must be bf16 of shape {(T, d)}")
+            if add.shape != (T, d) or add.dtype != y.dtype:
+                raise ValueError(f"add must be {y.dtype} of shape {(T, d)}")
             L.call("hmoe_combine_add", L.ptr(_contig(y, "y")), L.ptr(inv_pos), T, k, d, L.ptr(_contig(add, "add")),
-                   L.ptr(out), _dev_stream(y))
+                   L.ptr(out), dt, _dev_stream(y))
     return out
 
 
