@@ -738,34 +738,53 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
           });
         }
       } else if constexpr (EPI == EPI_SWIGLU_BWD) {
-        // sub-planes: dg [0, NSP), du [NSP, 2 NSP), then the pass's forward [g | u] inputs: g [2 NSP, 3 NSP),
-        // u [3 NSP, 4 NSP), in the same layout park_bf16 writes (so a lane reads its accumulator-shaped 8 bytes back)
+        // Two staging buffers per wave, in the layout park_bf16 writes (so a lane reads its accumulator-shaped 8
+        // bytes back): buffer q holds a pass's forward g in sub-planes [2q NSP, (2q+1) NSP) and u in
+        // [(2q+1) NSP, (2q+2) NSP).  The pass's dg and du are parked over its g and u (each lane overwrites exactly
+        // the bytes it has just read), then drained.  Pass a uses buffer a & 1: the [g | u] of pass a + 1 load while
+        // pass a computes and drains, and those of pass a + 2 are issued once pass a's drain has read its buffer.
         constexpr int RB = C::FN * 32 * 2, NSP = (RB + 127) / 128;
-        static_assert(4 * NSP * 4096 <= 8 * CH, "SwiGLU backward staging: dg, du, g, u sub-planes");
+        constexpr int LG = 2 * NSP * 4;  // direct loads per pass of [g | u]
+        static_assert(4 * NSP * 4096 <= 8 * CH, "SwiGLU backward staging: two buffers of g and u sub-planes");
         const float sc = row_scale(rbase + lrow);
-        // this pass's g and u rows copied into their sub-planes with direct loads: instruction (array, sp, i) fills
-        // rows 8i..8i+7 of a sub-plane, lane l row 8i + l/8, physical chunk l%8 = logical chunk (l%8) ^ (l/8)
+        // pass pa's g and u rows copied into buffer pa & 1 with direct loads: instruction (array, sp, i) fills rows
+        // 8i..8i+7 of a sub-plane, lane l row 8i + l/8, physical chunk l%8 = logical chunk (l%8) ^ (l/8).  The
+        // descriptor starts at the pass's first row and its range ends at the expert's last row, so rows past it
+        // read zeros; a lane's columns past N use an out-of-range offset; the row and array parts of each address
+        // are uniform (the scalar offset), so a lane holds one offset per sub-plane.
         auto issue_gu = [&](int pa) {
           const int rb = pa * C::FSM + wm * 32;
-          i32x4 rs = make_rsrc(p.gu_in + row0 * (int64_t)(2 * p.h));
+          const int64_t prow = row0 + rb;
+          i32x4 rs = make_rsrc(p.gu_in + prow * (int64_t)(2 * p.h));
+          const int64_t live = row_end > prow ? (row_end - prow) * (int64_t)(2 * p.h) * 2 : 0;
+          rs.z = __builtin_amdgcn_readfirstlane((int)min(live, (int64_t)0x7FFFFFF0));
           const int rl = lane >> 3, cl = (lane & 7) ^ rl;
 #pragma unroll
-          for (int arr = 0; arr < 2; ++arr)
+          for (int sp = 0; sp < NSP; ++sp) {
+            const int cw = sp * 64 + 8 * cl;  // column within the wave's FN*32
+            const int tc = (cw / 32) * C::FSN + wn * 32 + cw % 32;
+            const bool ok = n0 + tc < p.N && sp * 128 + cl * 16 < RB;
+            const uint32_t vo = ok ? (uint32_t)((rl * (2 * p.h) + n0 + tc) * 2) : kOOB;
 #pragma unroll
-            for (int sp = 0; sp < NSP; ++sp)
+            for (int arr = 0; arr < 2; ++arr)
 #pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                const int r = 8 * i + rl;
-                const int cw = sp * 64 + 8 * cl;  // column within the wave's FN*32
-                const int tc = (cw / 32) * C::FSN + wn * 32 + cw % 32;
-                const bool ok = row0 + rb + r < row_end && n0 + tc < p.N && sp * 128 + cl * 16 < RB;
-                const uint32_t vo = ok ? (uint32_t)(((rb + r) * (2 * p.h) + arr * p.h + n0 + tc) * 2) : kOOB;
-                buf2lds(vo, rs, 0u, sp_addr((2 + arr) * NSP + sp, 8 * i, 0));
-              }
+              for (int i = 0; i < 4; ++i)
+                buf2lds(vo, rs, (uint32_t)((8 * i * (2 * p.h) + arr * p.h) * 2),
+                        sp_addr((2 * (pa & 1) + arr) * NSP + sp, 8 * i, 0));
+          }
         };
-        if (a == 0) issue_gu(0);
-        wait_vm<0>();  // this pass's [g | u] (and the previous pass's stores: in-order counter)
+        if (a == 0) {
+          issue_gu(0);
+          if (fe_rows > 1) issue_gu(1);
+        }
+        // this pass's [g | u]: the direct loads are counted in issue order with the stores, and the only memory
+        // operations issued after them are the next pass's LG loads (every one issued: absent lanes load kOOB)
+        if (a + 1 < fe_rows)
+          wait_vm<LG>();
+        else
+          wait_vm<0>();
         asm volatile("" ::: "memory");
+        const int gsp = 2 * (a & 1) * NSP, usp = gsp + NSP;
         // With dw_part: the routing-weight gradient of the lane's row, sum over its columns of the unscaled product
         // (dy @ wd^T) times the forward's act = bf16(bf16(silu(g)) * u), in a fixed order (b, g, t).
         float dwl = 0.0f;
@@ -775,27 +794,32 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
             const int byte = (b * 32 + 8 * g + lcol) * 2;
-            const uint2 gl = *reinterpret_cast<const uint2*>(sp_addr(2 * NSP + byte / 128, lrow, byte % 128));
-            const uint2 ul = *reinterpret_cast<const uint2*>(sp_addr(3 * NSP + byte / 128, lrow, byte % 128));
-            const float gg[4] = {bf_lo(gl.x), bf_hi(gl.x), bf_lo(gl.y), bf_hi(gl.y)};
-            const float uu[4] = {bf_lo(ul.x), bf_hi(ul.x), bf_lo(ul.y), bf_hi(ul.y)};
-            float dg[4], du[4];
+            const uint2 gl = *reinterpret_cast<const uint2*>(sp_addr(gsp + byte / 128, lrow, byte % 128));
+            const uint2 ul = *reinterpret_cast<const uint2*>(sp_addr(usp + byte / 128, lrow, byte % 128));
+            const uint32_t gw[2] = {gl.x, gl.y}, uw[2] = {ul.x, ul.y};
+            uint32_t dgw[2], duw[2];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              const float da = acc[a][b][4 * g + t] * sc;
-              const float sig = sigmoid_f(gg[t]);
-              const float sl = gg[t] * sig;
-              // du uses the forward's stored factor bf16(silu(g)); silu_f(g) = g * sig
-              const float slb = bf_lo(cvt_bf2(sl, sl));
-              du[t] = da * slb;
-              dg[t] = da * uu[t] * sig * (1.0f + gg[t] * (1.0f - sig));
+            for (int tp = 0; tp < 2; ++tp) {  // element pairs (t, t + 1), t = 2 tp
+              const float g0 = bf_lo(gw[tp]), g1 = bf_hi(gw[tp]), u0 = bf_lo(uw[tp]), u1 = bf_hi(uw[tp]);
+              const float s0 = sigmoid_f(g0), s1 = sigmoid_f(g1);
+              const float l0 = g0 * s0, l1 = g1 * s1;  // silu_f(g), as the forward computes it
+              // du uses the forward's stored factor bf16(silu(g))
+              const uint32_t sb = cvt_bf2(l0, l1);
+              const float b0 = bf_lo(sb), b1 = bf_hi(sb);
+              const float a0 = acc[a][b][4 * g + 2 * tp], a1 = acc[a][b][4 * g + 2 * tp + 1];
+              const float da0 = a0 * sc, da1 = a1 * sc;
+              duw[tp] = cvt_bf2(da0 * b0, da1 * b1);
+              // silu'(g) = sig (1 + g (1 - sig)) = sig + silu(g) (1 - sig)
+              dgw[tp] = cvt_bf2((da0 * u0) * __builtin_fmaf(l0, 1.0f - s0, s0),
+                                (da1 * u1) * __builtin_fmaf(l1, 1.0f - s1, s1));
               if (p.dw_part) {
-                const float av = slb * uu[t];
-                dwl = __builtin_fmaf(acc[a][b][4 * g + t], bf_lo(cvt_bf2(av, av)), dwl);
+                const uint32_t av = cvt_bf2(b0 * u0, b1 * u1);
+                dwl = __builtin_fmaf(a0, bf_lo(av), dwl);
+                dwl = __builtin_fmaf(a1, bf_hi(av), dwl);
               }
             }
-            park_bf16(0, b, g, cvt_bf2(dg[0], dg[1]), cvt_bf2(dg[2], dg[3]));
-            park_bf16(NSP, b, g, cvt_bf2(du[0], du[1]), cvt_bf2(du[2], du[3]));
+            *reinterpret_cast<uint2*>(sp_addr(gsp + byte / 128, lrow, byte % 128)) = make_uint2(dgw[0], dgw[1]);
+            *reinterpret_cast<uint2*>(sp_addr(usp + byte / 128, lrow, byte % 128)) = make_uint2(duw[0], duw[1]);
           }
         }
         if (p.dw_part) {  // lanes l and l + 32 hold the two column halves of one row
@@ -803,19 +827,19 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
           const int64_t row = row0 + rbase + lrow;
           if (lane < 32 && row < row_end) p.dw_part[(int64_t)(2 * nb + wn) * p.M + row] = dwl;  // (partial, row)
         }
-        // the next pass's inputs load while this pass drains (its g / u sub-planes have been read above)
-        if (a + 1 < fe_rows) issue_gu(a + 1);
-        drain(0, RB, 2, [&](int rr, int tc, uint4 v) {
+        drain(gsp, RB, 2, [&](int rr, int tc, uint4 v) {
           const int64_t row = row0 + rbase + rr;
           const int j = n0 + tc;
           if (row < row_end && j < p.N) *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p.C) + row * (int64_t)(2 * p.h) + j) = v;
         });
-        drain(NSP, RB, 2, [&](int rr, int tc, uint4 v) {
+        drain(usp, RB, 2, [&](int rr, int tc, uint4 v) {
           const int64_t row = row0 + rbase + rr;
           const int j = n0 + tc;
           if (row < row_end && j < p.N)
             *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p.C) + row * (int64_t)(2 * p.h) + p.h + j) = v;
         });
+        // the drain's LDS reads have returned (the stores above consumed them): the buffer takes pass a + 2's rows
+        if (a + 2 < fe_rows) issue_gu(a + 2);
       }
     }
   }
