@@ -351,6 +351,58 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
       }
     }
 
+    const int nk = (kvalid + kBK - 1) / kBK;  // k-slices of this tile
+
+    // ---- epilogue staging (defined here: the SwiGLU backward starts loading its first pass inside the loop) ----
+    // The sub-planes live in the ring bytes this wave's own direct loads fill (its A and B parts of each stage),
+    // which no other wave writes.  Chunk q is part q & 1 of stage q >> 1 (bf16 weights; int8: the A part of stage
+    // q), the stage rotated by srot: the SwiGLU backward's first staging buffer (stages srot, srot + 1) is then the
+    // pair of stages whose slices (nk - 4, nk - 3) every wave has read by the barrier of iteration nk - 2.
+    const int lrow = lane & 31;
+    const int lcol = 4 * (lane >> 5);
+    constexpr int CH = C::A_BYTES / C::NWAVES;  // bytes per ring part filled by one wave
+    static_assert(CH >= 1024 && 4096 % CH == 0 && (C::BE == 1 || C::A_BYTES == C::B_BYTES), "staging chunks");
+    const int srot = EPI == EPI_SWIGLU_BWD ? (nk & (kNStage - 1)) : 0;
+    auto chunk = [&](int q) -> char* {
+      if constexpr (C::BE == 1) return smem + q * C::STAGE_BYTES + wave * CH;
+      return smem + (((q >> 1) + srot) & (kNStage - 1)) * C::STAGE_BYTES + (q & 1) * C::A_BYTES + wave * CH;
+    };
+    // sub-plane sp, row r (0..31), byte offset within the 128-byte row; 16-byte chunks XOR-swizzled by r & 7
+    auto sp_addr = [&](int sp, int r, int byte) -> char* {
+      const int lin = r * 128;
+      return chunk(sp * (4096 / CH) + lin / CH) + lin % CH + ((((byte >> 4) ^ r) & 7) << 4) + (byte & 15);
+    };
+    // SwiGLU backward: pass pa's forward [g | u] rows into staging buffer pa & 1 (g in sub-planes
+    // [2 (pa & 1) NSP, (2 (pa & 1) + 1) NSP), u in the next NSP) with direct loads: instruction (array, sp, i) fills
+    // rows 8i..8i+7 of a sub-plane, lane l row 8i + l/8, physical chunk l%8 = logical chunk (l%8) ^ (l/8).  The
+    // descriptor starts at the pass's first row and its range ends at the expert's last row, so rows past it read
+    // zeros; a lane's columns past N use an out-of-range offset; the row and array parts of each address are
+    // uniform (the scalar offset), so a lane holds one offset per sub-plane.
+    constexpr int GU_RB = C::FN * 32 * 2, GU_NSP = (GU_RB + 127) / 128;
+    [[maybe_unused]] auto issue_gu = [&](int pa) {
+      const int rb = pa * C::FSM + wm * 32;
+      const int64_t prow = row0 + rb;
+      i32x4 rs = make_rsrc(p.gu_in + prow * (int64_t)(2 * p.h));
+      const int64_t live = row_end > prow ? (row_end - prow) * (int64_t)(2 * p.h) * 2 : 0;
+      rs.z = __builtin_amdgcn_readfirstlane((int)min(live, (int64_t)0x7FFFFFF0));
+      const int rl = lane >> 3, cl = (lane & 7) ^ rl;
+#pragma unroll
+      for (int sp = 0; sp < GU_NSP; ++sp) {
+        const int cw = sp * 64 + 8 * cl;  // column within the wave's FN*32
+        const int tc = (cw / 32) * C::FSN + wn * 32 + cw % 32;
+        const bool ok = n0 + tc < p.N && sp * 128 + cl * 16 < GU_RB;
+        const uint32_t vo = ok ? (uint32_t)((rl * (2 * p.h) + n0 + tc) * 2) : kOOB;
+#pragma unroll
+        for (int arr = 0; arr < 2; ++arr)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            buf2lds(vo, rs, (uint32_t)((8 * i * (2 * p.h) + arr * p.h) * 2),
+                    sp_addr((2 * (pa & 1) + arr) * GU_NSP + sp, 8 * i, 0));
+      }
+    };
+    // SwiGLU backward: pass 0's rows are loaded from the barrier of iteration nk - 2 on (nk >= 2)
+    const bool gu_early = EPI == EPI_SWIGLU_BWD && nk >= 2;
+
     // ---- main loop: NSTAGE-deep ring of k-slices ----
     f32x16 acc[C::FM][C::FN];
 #pragma unroll
@@ -361,7 +413,6 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
         for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
 
     constexpr int LOADS = decltype(ta)::PER_WAVE + decltype(tb)::PER_WAVE;  // direct loads per thread per slice
-    const int nk = (kvalid + kBK - 1) / kBK;
     char* const ring_end = smem + C::LDS_BYTES;
     char* fill = smem;        // next ring slot to fill
     const char* cons = smem;  // ring slot consumed by the current slice
@@ -461,10 +512,13 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
             wait_vm<2 * LOADS>();
           else if (ahead == 1)
             wait_vm<LOADS>();
-          else
-            wait_vm<0>();
+          else if (!gu_early || kt + 1 < nk)  // the last iteration has no next slice to wait for: pass 0's [g | u]
+            wait_vm<0>();                      // stay in flight
         }
         lds_barrier();
+        if constexpr (EPI == EPI_SWIGLU_BWD) {
+          if (kt == nk - 2) issue_gu(0);  // slices nk - 4 and nk - 3 have been read by every wave
+        }
         // Second half: MFMAs on the ks1 fragments, the next slice's ks0 fragment reads and the refill of slice
         // kt's slot with slice kt+4 (fill == cons here), one step per MFMA so the reads and copies issue in its
         // shadow (in both modes: the weight gradients measured 6% faster than with the copies issued together).
@@ -561,15 +615,6 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
     // 8-byte pieces.  The sub-planes live in the ring bytes this wave's own direct loads fill (its A and B parts of
     // each stage), which no other wave writes: the epilogue needs no barrier, and the wave's next-tile loads are
     // issued after its last read in program order.
-    const int lrow = lane & 31;
-    const int lcol = 4 * (lane >> 5);
-    constexpr int CH = C::A_BYTES / C::NWAVES;  // bytes per ring part filled by one wave
-    static_assert(CH >= 1024 && 4096 % CH == 0 && (C::BE == 1 || C::A_BYTES == C::B_BYTES), "staging chunks");
-    // chunk q: the A and B parts of each stage (bf16 weights), or the A parts only (int8 weights: smaller B parts)
-    auto chunk = [&](int q) -> char* {
-      if constexpr (C::BE == 1) return smem + q * C::STAGE_BYTES + wave * CH;
-      return smem + (q >> 1) * C::STAGE_BYTES + (q & 1) * C::A_BYTES + wave * CH;
-    };
     // column scale of int8 weights for tile column tc (1 for bf16 weights)
     [[maybe_unused]] auto col_scale4 = [&](int tc, float* ws) {
       if constexpr (C::BE == 1) {
@@ -583,11 +628,6 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
       } else {
         ws[0] = ws[1] = ws[2] = ws[3] = 1.0f;
       }
-    };
-    // sub-plane sp, row r (0..31), byte offset within the 128-byte row; 16-byte chunks XOR-swizzled by r & 7
-    auto sp_addr = [&](int sp, int r, int byte) -> char* {
-      const int lin = r * 128;
-      return chunk(sp * (4096 / CH) + lin / CH) + lin % CH + ((((byte >> 4) ^ r) & 7) << 4) + (byte & 15);
     };
     // park the 4 values of fragment (a, b), group g (rows lrow) into a bf16 / fp32 array starting at sub-plane sp0
     auto park_bf16 = [&](int sp0, int b, int g, uint32_t lo, uint32_t hi) {
@@ -743,38 +783,12 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
         // [(2q+1) NSP, (2q+2) NSP).  The pass's dg and du are parked over its g and u (each lane overwrites exactly
         // the bytes it has just read), then drained.  Pass a uses buffer a & 1: the [g | u] of pass a + 1 load while
         // pass a computes and drains, and those of pass a + 2 are issued once pass a's drain has read its buffer.
-        constexpr int RB = C::FN * 32 * 2, NSP = (RB + 127) / 128;
+        constexpr int RB = GU_RB, NSP = GU_NSP;
         constexpr int LG = 2 * NSP * 4;  // direct loads per pass of [g | u]
         static_assert(4 * NSP * 4096 <= 8 * CH, "SwiGLU backward staging: two buffers of g and u sub-planes");
         const float sc = row_scale(rbase + lrow);
-        // pass pa's g and u rows copied into buffer pa & 1 with direct loads: instruction (array, sp, i) fills rows
-        // 8i..8i+7 of a sub-plane, lane l row 8i + l/8, physical chunk l%8 = logical chunk (l%8) ^ (l/8).  The
-        // descriptor starts at the pass's first row and its range ends at the expert's last row, so rows past it
-        // read zeros; a lane's columns past N use an out-of-range offset; the row and array parts of each address
-        // are uniform (the scalar offset), so a lane holds one offset per sub-plane.
-        auto issue_gu = [&](int pa) {
-          const int rb = pa * C::FSM + wm * 32;
-          const int64_t prow = row0 + rb;
-          i32x4 rs = make_rsrc(p.gu_in + prow * (int64_t)(2 * p.h));
-          const int64_t live = row_end > prow ? (row_end - prow) * (int64_t)(2 * p.h) * 2 : 0;
-          rs.z = __builtin_amdgcn_readfirstlane((int)min(live, (int64_t)0x7FFFFFF0));
-          const int rl = lane >> 3, cl = (lane & 7) ^ rl;
-#pragma unroll
-          for (int sp = 0; sp < NSP; ++sp) {
-            const int cw = sp * 64 + 8 * cl;  // column within the wave's FN*32
-            const int tc = (cw / 32) * C::FSN + wn * 32 + cw % 32;
-            const bool ok = n0 + tc < p.N && sp * 128 + cl * 16 < RB;
-            const uint32_t vo = ok ? (uint32_t)((rl * (2 * p.h) + n0 + tc) * 2) : kOOB;
-#pragma unroll
-            for (int arr = 0; arr < 2; ++arr)
-#pragma unroll
-              for (int i = 0; i < 4; ++i)
-                buf2lds(vo, rs, (uint32_t)((8 * i * (2 * p.h) + arr * p.h) * 2),
-                        sp_addr((2 * (pa & 1) + arr) * NSP + sp, 8 * i, 0));
-          }
-        };
         if (a == 0) {
-          issue_gu(0);
+          if (!gu_early) issue_gu(0);
           if (fe_rows > 1) issue_gu(1);
         }
         // this pass's [g | u]: the direct loads are counted in issue order with the stores, and the only memory
