@@ -25,6 +25,11 @@
 
 namespace hmoe {
 
+// byte offsets of a lane's four epilogue drain rows (-1: no row)
+struct RowOffs {
+  int64_t o[4];
+};
+
 // ----------------------------------------------------------------------------------------------------------------
 // The kernel
 // ----------------------------------------------------------------------------------------------------------------
@@ -615,18 +620,14 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
     // 8-byte pieces.  The sub-planes live in the ring bytes this wave's own direct loads fill (its A and B parts of
     // each stage), which no other wave writes: the epilogue needs no barrier, and the wave's next-tile loads are
     // issued after its last read in program order.
-    // column scale of int8 weights for tile column tc (1 for bf16 weights)
-    [[maybe_unused]] auto col_scale4 = [&](int tc, float* ws) {
-      if constexpr (C::BE == 1) {
-        if (p.w_scale_f32) {
-          const float4 v = *reinterpret_cast<const float4*>(&s_colsc[par][tc]);
-          ws[0] = v.x; ws[1] = v.y; ws[2] = v.z; ws[3] = v.w;
-        } else {
-          const uint2 v = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(s_colsc[par]) + tc);
-          ws[0] = bf_lo(v.x); ws[1] = bf_hi(v.x); ws[2] = bf_lo(v.y); ws[3] = bf_hi(v.y);
-        }
+    // the 4 column scales of int8 weights from tile column tc: fp32 (scf_tag true) or bf16 values
+    [[maybe_unused]] auto col_scale4 = [&](auto scf_tag, int tc, float* ws) {
+      if constexpr (decltype(scf_tag)::value) {
+        const float4 v = *reinterpret_cast<const float4*>(&s_colsc[par][tc]);
+        ws[0] = v.x; ws[1] = v.y; ws[2] = v.z; ws[3] = v.w;
       } else {
-        ws[0] = ws[1] = ws[2] = ws[3] = 1.0f;
+        const uint2 v = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(s_colsc[par]) + tc);
+        ws[0] = bf_lo(v.x); ws[1] = bf_hi(v.x); ws[2] = bf_lo(v.y); ws[3] = bf_hi(v.y);
       }
     };
     // park the 4 values of fragment (a, b), group g (rows lrow) into a bf16 / fp32 array starting at sub-plane sp0
@@ -638,19 +639,52 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
       const int byte = (b * 32 + 8 * g + lcol) * 4;
       *reinterpret_cast<float4*>(sp_addr(sp0 + byte / 128, lrow, byte % 128)) = v;
     };
-    // read back an array of rowbytes bytes per row (es bytes per element) from sub-plane sp0 on: calls
-    // st(r, tile_col, uint4) for each of the lane's 16-byte pieces (row r of the wave's 32, tile column of its first
-    // element)
-    auto drain = [&](int sp0, int rowbytes, int es, auto&& st) {
-      for (int sp = 0; sp * 128 < rowbytes; ++sp)
+    // Read back NSPX sub-planes from sp0 (an array of rowbytes bytes per row, es bytes per element) and store them.
+    // Lane l holds the 16-byte piece l % 8 of every sub-plane in the wave's rows 8 j + l / 8 (j = 0..3); rows.o[j]
+    // is the byte offset from base of its row j's column 0, or -1 for a row past the tile's rows, and a piece goes
+    // to base + rows.o[j] + (n0 + tile column) * es when that column is below ncols.  The reads of two sub-planes
+    // are issued before their stores, so a pass waits for LDS once per sub-plane pair, not once per store.
+    auto drain_rows = [&](auto nsp_tag, int sp0, int rowbytes, int es, char* base, const RowOffs rows, int ncols) {
+      constexpr int NSPX = decltype(nsp_tag)::value;
+      const int c = lane & 7;
+      auto read4 = [&](int sp, uint4* v) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int idx = j * 64 + lane, r = idx >> 3, c = idx & 7;
-          if (sp * 128 + c * 16 >= rowbytes) continue;  // a narrow array fills only part of its last sub-plane
-          const uint4 v = *reinterpret_cast<const uint4*>(sp_addr(sp0 + sp, r, c * 16));
-          const int cw = (sp * 128 + c * 16) / es;  // column within the wave's FN*32
-          st(r, (cw / 32) * C::FSN + wn * 32 + cw % 32, v);
-        }
+        for (int j = 0; j < 4; ++j)
+          v[j] = *reinterpret_cast<const uint4*>(sp_addr(sp0 + sp, 8 * j + (lane >> 3), c * 16));
+      };
+      auto store4 = [&](int sp, const uint4* v) {
+        const int cw = (sp * 128 + c * 16) / es;  // column within the wave's FN*32
+        const int n = n0 + (cw / 32) * C::FSN + wn * 32 + cw % 32;
+        const bool cok = sp * 128 + c * 16 < rowbytes && n < ncols;  // a narrow array fills part of a sub-plane
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (cok && rows.o[j] >= 0) *reinterpret_cast<uint4*>(base + rows.o[j] + (int64_t)n * es) = v[j];
+      };
+#pragma unroll
+      for (int sp = 0; sp + 1 < NSPX; sp += 2) {
+        uint4 va[4], vb[4];
+        read4(sp, va);
+        read4(sp + 1, vb);
+        store4(sp, va);
+        store4(sp + 1, vb);
+      }
+      if constexpr (NSPX & 1) {
+        uint4 va[4];
+        read4(NSPX - 1, va);
+        store4(NSPX - 1, va);
+      }
+    };
+    // the lane's drain rows of pass rbase (tile rows rbase + 8 j + lane / 8): o[j] = off(tile row, sorted row), or -1
+    // past the tile's rows
+    [[maybe_unused]] auto rows_of = [&](int rbase, auto&& off) {
+      RowOffs r;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int rt = rbase + 8 * j + (lane >> 3);
+        const int64_t row = row0 + rt;
+        r.o[j] = row < row_end ? off(rt, row) : (int64_t)-1;
+      }
+      return r;
     };
     [[maybe_unused]] auto row_scale = [&](int rt) -> float {
       if (!p.scale) return 1.0f;
@@ -662,120 +696,146 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
       if (a >= fe_rows) break;  // no tile rows in this or later passes (partial m-tile)
       const int rbase = a * C::FSM + wm * 32;  // tile row of the wave's row 0 in this pass
       if constexpr (EPI == EPI_WGRAD) {
+        auto park_all = [&](auto f32_tag) {
 #pragma unroll
-        for (int b = 0; b < C::FN; ++b) {
-          pin_agpr(acc[a][b]);
+          for (int b = 0; b < C::FN; ++b) {
+            pin_agpr(acc[a][b]);
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const f32x16& v = acc[a][b];
-            if (p.c_f32)
-              park_f32(0, b, g, make_float4(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]));
-            else
-              park_bf16(0, b, g, cvt_bf2(v[4 * g], v[4 * g + 1]), cvt_bf2(v[4 * g + 2], v[4 * g + 3]));
+            for (int g = 0; g < 4; ++g) {
+              const f32x16& v = acc[a][b];
+              if constexpr (decltype(f32_tag)::value)
+                park_f32(0, b, g, make_float4(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]));
+              else
+                park_bf16(0, b, g, cvt_bf2(v[4 * g], v[4 * g + 1]), cvt_bf2(v[4 * g + 2], v[4 * g + 3]));
+            }
           }
-        }
+        };
         const int es = p.c_f32 ? 4 : 2;
-        drain(0, C::FN * 32 * es, es, [&](int r, int tc, uint4 v) {
-          const int i = i0 + rbase + r, n = n0 + tc;
-          if (i < p.P && n < p.N)
-            *reinterpret_cast<uint4*>(reinterpret_cast<char*>(p.C) +
-                                      ((int64_t)e * p.strideCe + (int64_t)i * p.ldc + n) * es) = v;
-        });
+        RowOffs rows;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int i = i0 + rbase + 8 * j + (lane >> 3);
+          rows.o[j] = i < p.P ? ((int64_t)e * p.strideCe + (int64_t)i * p.ldc) * es : (int64_t)-1;
+        }
+        char* const base = reinterpret_cast<char*>(p.C);
+        if (p.c_f32) {
+          park_all(std::true_type{});
+          drain_rows(std::integral_constant<int, C::FN * 32 * 4 / 128>{}, 0, C::FN * 32 * 4, 4, base, rows, p.N);
+        } else {
+          park_all(std::false_type{});
+          drain_rows(std::integral_constant<int, C::FN * 32 * 2 / 128>{}, 0, C::FN * 32 * 2, 2, base, rows, p.N);
+        }
       } else if constexpr (EPI == EPI_STORE || EPI == EPI_STORE_F32) {
         constexpr int ES = EPI == EPI_STORE_F32 ? 4 : 2;
         constexpr int RB = C::FN * 32 * ES, NSP = (RB + 127) / 128;  // y's row bytes, sub-planes; yhat (bf16) follows
         const float sc = row_scale(rbase + lrow);   // 1 without a scale: the product is then exact
+        // aux: also park yhat (bf16 weights only); scf_tag: fp32 int8 column scales, chosen once per pass so that the
+        // int8 column scales of a fragment's four groups are read together
+        auto park_all = [&](bool aux, auto scf_tag) {
 #pragma unroll
-        for (int b = 0; b < C::FN; ++b) {
-          pin_agpr(acc[a][b]);
+          for (int b = 0; b < C::FN; ++b) {
+            pin_agpr(acc[a][b]);
+            [[maybe_unused]] float ws[4][4];
+            if constexpr (C::BE == 1) {
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const f32x16& v = acc[a][b];
-            if (p.aux) park_bf16(NSP, b, g, X::pack2(v[4 * g], v[4 * g + 1]), X::pack2(v[4 * g + 2], v[4 * g + 3]));
-            float v0, v1, v2, v3;
-            if constexpr (C::BE == 1) {  // int8 weights: column scale first, then the row scale (two products)
-              float ws[4];
-              col_scale4(col_of(b, g), ws);
-              v0 = (v[4 * g] * ws[0]) * sc, v1 = (v[4 * g + 1] * ws[1]) * sc;
-              v2 = (v[4 * g + 2] * ws[2]) * sc, v3 = (v[4 * g + 3] * ws[3]) * sc;
-            } else {
-              v0 = v[4 * g] * sc, v1 = v[4 * g + 1] * sc, v2 = v[4 * g + 2] * sc, v3 = v[4 * g + 3] * sc;
+              for (int g = 0; g < 4; ++g) col_scale4(scf_tag, col_of(b, g), ws[g]);
             }
-            if constexpr (EPI == EPI_STORE_F32)
-              park_f32(0, b, g, make_float4(v0, v1, v2, v3));
-            else
-              park_bf16(0, b, g, X::pack2(v0, v1), X::pack2(v2, v3));
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              const f32x16& v = acc[a][b];
+              if (C::BE == 2 && aux)
+                park_bf16(NSP, b, g, X::pack2(v[4 * g], v[4 * g + 1]), X::pack2(v[4 * g + 2], v[4 * g + 3]));
+              float v0, v1, v2, v3;
+              if constexpr (C::BE == 1) {  // int8 weights: column scale first, then the row scale (two products)
+                v0 = (v[4 * g] * ws[g][0]) * sc, v1 = (v[4 * g + 1] * ws[g][1]) * sc;
+                v2 = (v[4 * g + 2] * ws[g][2]) * sc, v3 = (v[4 * g + 3] * ws[g][3]) * sc;
+              } else {
+                v0 = v[4 * g] * sc, v1 = v[4 * g + 1] * sc, v2 = v[4 * g + 2] * sc, v3 = v[4 * g + 3] * sc;
+              }
+              if constexpr (EPI == EPI_STORE_F32)
+                park_f32(0, b, g, make_float4(v0, v1, v2, v3));
+              else
+                park_bf16(0, b, g, X::pack2(v0, v1), X::pack2(v2, v3));
+            }
           }
-        }
-        drain(0, RB, ES, [&](int r, int tc, uint4 v) {
-          const int rt = rbase + r;
-          const int64_t row = row0 + rt;
-          const int n = n0 + tc;
-          if (row < row_end && n < p.N) {
-            const int64_t yr = p.y_idx ? (int64_t)s_rowy[par][rt + y_sh] : row;
-            *reinterpret_cast<uint4*>(reinterpret_cast<char*>(p.C) + (yr * p.ldc + n) * ES) = v;
-          }
+        };
+        // the int8 entry points keep no yhat (aux is NULL with int8 weights)
+        const bool aux = C::BE == 2 && p.aux;
+        if (C::BE == 1 && p.w_scale_f32)
+          park_all(aux, std::true_type{});
+        else
+          park_all(aux, std::false_type{});
+        const RowOffs rows = rows_of(rbase, [&](int rt, int64_t row) {
+          return (p.y_idx ? (int64_t)s_rowy[par][rt + y_sh] : row) * p.ldc * ES;
         });
-        if (p.aux)
-          drain(NSP, C::FN * 32 * 2, 2, [&](int r, int tc, uint4 v) {
-            const int64_t row = row0 + rbase + r;
-            const int n = n0 + tc;
-            if (row < row_end && n < p.N) *reinterpret_cast<uint4*>(p.aux + row * p.ldc + n) = v;
-          });
+        drain_rows(std::integral_constant<int, NSP>{}, 0, RB, ES, reinterpret_cast<char*>(p.C), rows, p.N);
+        if constexpr (C::BE == 2) {
+          if (aux)
+            drain_rows(std::integral_constant<int, (C::FN * 32 * 2 + 127) / 128>{}, NSP, C::FN * 32 * 2, 2,
+                       reinterpret_cast<char*>(p.aux),
+                       rows_of(rbase, [&](int, int64_t row) { return row * p.ldc * 2; }), p.N);
+        }
       } else if constexpr (EPI == EPI_SWIGLU) {
         // fragments b < FN/2 hold gate columns, b + FN/2 the matching up columns (tile columns + BN/2); the wave's
         // activation columns are b*32 + ... for b < FN/2: sub-plane 0 = act, 1 = g, 2 = u (one each for FN = 4)
         constexpr int RB = C::FN / 2 * 32 * 2, NSP = (RB + 127) / 128;  // row bytes and sub-planes of each array
+        // aux: also park [g | u] (bf16 weights only); scf_tag: fp32 int8 column scales (chosen once per pass)
+        auto park_all = [&](bool aux, auto scf_tag) {
 #pragma unroll
-        for (int b = 0; b < C::FN / 2; ++b) {
-          pin_agpr(acc[a][b]);
-          pin_agpr(acc[a][b + C::FN / 2]);
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const f32x16& gv = acc[a][b];
-            const f32x16& uv = acc[a][b + C::FN / 2];
-            float gs[4] = {gv[4 * g], gv[4 * g + 1], gv[4 * g + 2], gv[4 * g + 3]};
-            float us[4] = {uv[4 * g], uv[4 * g + 1], uv[4 * g + 2], uv[4 * g + 3]};
+          for (int b = 0; b < C::FN / 2; ++b) {
+            pin_agpr(acc[a][b]);
+            pin_agpr(acc[a][b + C::FN / 2]);
+            [[maybe_unused]] float wg[4][4], wu[4][4];
             if constexpr (C::BE == 1) {  // int8 weights: per-column scales of the gate and up columns
-              float wg[4], wu[4];
-              col_scale4(col_of(b, g), wg);
-              col_scale4(col_of(b + C::FN / 2, g), wu);
 #pragma unroll
-              for (int t = 0; t < 4; ++t) {
-                gs[t] *= wg[t];
-                us[t] *= wu[t];
+              for (int g = 0; g < 4; ++g) {
+                col_scale4(scf_tag, col_of(b, g), wg[g]);
+                col_scale4(scf_tag, col_of(b + C::FN / 2, g), wu[g]);
               }
             }
-            const uint32_t gb0 = X::pack2(gs[0], gs[1]), gb1 = X::pack2(gs[2], gs[3]);
-            const uint32_t ub0 = X::pack2(us[0], us[1]), ub1 = X::pack2(us[2], us[3]);
-            const float gg[4] = {X::lo(gb0), X::hi(gb0), X::lo(gb1), X::hi(gb1)};
-            const float uu[4] = {X::lo(ub0), X::hi(ub0), X::lo(ub1), X::hi(ub1)};
-            // act = R(R(silu(g)) * u) with g, u the rounded projections (R: to bf16, or fp16 with F16)
-            const uint32_t sl0 = X::pack2(silu_f(gg[0]), silu_f(gg[1])), sl1 = X::pack2(silu_f(gg[2]), silu_f(gg[3]));
-            park_bf16(0, b, g, X::pack2(X::lo(sl0) * uu[0], X::hi(sl0) * uu[1]),
-                      X::pack2(X::lo(sl1) * uu[2], X::hi(sl1) * uu[3]));
-            if (p.aux) {
-              park_bf16(NSP, b, g, gb0, gb1);
-              park_bf16(2 * NSP, b, g, ub0, ub1);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              const f32x16& gv = acc[a][b];
+              const f32x16& uv = acc[a][b + C::FN / 2];
+              float gs[4] = {gv[4 * g], gv[4 * g + 1], gv[4 * g + 2], gv[4 * g + 3]};
+              float us[4] = {uv[4 * g], uv[4 * g + 1], uv[4 * g + 2], uv[4 * g + 3]};
+              if constexpr (C::BE == 1) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                  gs[t] *= wg[g][t];
+                  us[t] *= wu[g][t];
+                }
+              }
+              const uint32_t gb0 = X::pack2(gs[0], gs[1]), gb1 = X::pack2(gs[2], gs[3]);
+              const uint32_t ub0 = X::pack2(us[0], us[1]), ub1 = X::pack2(us[2], us[3]);
+              const float gg[4] = {X::lo(gb0), X::hi(gb0), X::lo(gb1), X::hi(gb1)};
+              const float uu[4] = {X::lo(ub0), X::hi(ub0), X::lo(ub1), X::hi(ub1)};
+              // act = R(R(silu(g)) * u) with g, u the rounded projections (R: to bf16, or fp16 with F16)
+              const uint32_t sl0 = X::pack2(silu_f(gg[0]), silu_f(gg[1])), sl1 = X::pack2(silu_f(gg[2]), silu_f(gg[3]));
+              park_bf16(0, b, g, X::pack2(X::lo(sl0) * uu[0], X::hi(sl0) * uu[1]),
+                        X::pack2(X::lo(sl1) * uu[2], X::hi(sl1) * uu[3]));
+              if (C::BE == 2 && aux) {
+                park_bf16(NSP, b, g, gb0, gb1);
+                park_bf16(2 * NSP, b, g, ub0, ub1);
+              }
             }
           }
-        }
-        drain(0, RB, 2, [&](int r, int tc, uint4 v) {
-          const int64_t row = row0 + rbase + r;
-          const int j = n0 + tc;
-          if (row < row_end && j < p.N) *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p.C) + row * p.ldc + j) = v;
-        });
-        if (p.aux) {
-          drain(NSP, RB, 2, [&](int r, int tc, uint4 v) {
-            const int64_t row = row0 + rbase + r;
-            const int j = n0 + tc;
-            if (row < row_end && j < p.N) *reinterpret_cast<uint4*>(p.aux + row * (int64_t)(2 * p.h) + j) = v;
-          });
-          drain(2 * NSP, RB, 2, [&](int r, int tc, uint4 v) {
-            const int64_t row = row0 + rbase + r;
-            const int j = n0 + tc;
-            if (row < row_end && j < p.N) *reinterpret_cast<uint4*>(p.aux + row * (int64_t)(2 * p.h) + p.h + j) = v;
-          });
+        };
+        // the int8 entry point keeps no [g | u] (aux is NULL with int8 weights)
+        const bool aux = C::BE == 2 && p.aux;
+        if (C::BE == 1 && p.w_scale_f32)
+          park_all(aux, std::true_type{});
+        else
+          park_all(aux, std::false_type{});
+        drain_rows(std::integral_constant<int, NSP>{}, 0, RB, 2, reinterpret_cast<char*>(p.C),
+                   rows_of(rbase, [&](int, int64_t row) { return row * p.ldc * 2; }), p.N);
+        if constexpr (C::BE == 2) {
+          if (aux) {
+            const RowOffs rows = rows_of(rbase, [&](int, int64_t row) { return row * (int64_t)(2 * p.h) * 2; });
+            drain_rows(std::integral_constant<int, NSP>{}, NSP, RB, 2, reinterpret_cast<char*>(p.aux), rows, p.N);
+            drain_rows(std::integral_constant<int, NSP>{}, 2 * NSP, RB, 2, reinterpret_cast<char*>(p.aux + p.h), rows,
+                       p.N);
+          }
         }
       } else if constexpr (EPI == EPI_SWIGLU_BWD) {
         // Two staging buffers per wave, in the layout park_bf16 writes (so a lane reads its accumulator-shaped 8
@@ -841,17 +901,20 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
           const int64_t row = row0 + rbase + lrow;
           if (lane < 32 && row < row_end) p.dw_part[(int64_t)(2 * nb + wn) * p.M + row] = dwl;  // (partial, row)
         }
-        drain(gsp, RB, 2, [&](int rr, int tc, uint4 v) {
-          const int64_t row = row0 + rbase + rr;
-          const int j = n0 + tc;
-          if (row < row_end && j < p.N) *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p.C) + row * (int64_t)(2 * p.h) + j) = v;
-        });
-        drain(usp, RB, 2, [&](int rr, int tc, uint4 v) {
-          const int64_t row = row0 + rbase + rr;
-          const int j = n0 + tc;
-          if (row < row_end && j < p.N)
-            *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p.C) + row * (int64_t)(2 * p.h) + p.h + j) = v;
-        });
+        // (one piece read, one stored: fewer live registers than the batched drain, and as fast here)
+        for (int q = 0; q < 2; ++q)
+          for (int sp = 0; sp < NSP; ++sp)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int idx = j * 64 + lane, rr = idx >> 3, c = idx & 7;
+              if (sp * 128 + c * 16 >= RB) continue;
+              const uint4 v = *reinterpret_cast<const uint4*>(sp_addr((q ? usp : gsp) + sp, rr, c * 16));
+              const int cw = (sp * 128 + c * 16) / 2;
+              const int64_t row = row0 + rbase + rr;
+              const int jc = n0 + (cw / 32) * C::FSN + wn * 32 + cw % 32;
+              if (row < row_end && jc < p.N)
+                *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.C) + row * (int64_t)(2 * p.h) + q * p.h + jc) = v;
+            }
         // the drain's LDS reads have returned (the stores above consumed them): the buffer takes pass a + 2's rows
         if (a + 2 < fe_rows) issue_gu(a + 2);
       }
