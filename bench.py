@@ -76,11 +76,14 @@ def zipf_bias(E, seed=0, s=1.2, n_empty=2):
     return b
 
 
+PROBE_STRIDE = 4
+
+
 def time_steps(step, steps, warmup, graph, probe_kernel, probe_every=1, probe_first=0):
     """The timed region.  graph: the step is captured once as a HIP graph (graphs.StepGraph, after the warm-ups) and
     the timed region replays it `steps` times; an eager pass of the same number of steps follows, with events
-    around the probe kernel's launches on its stream (its average launch time, for the roofline) and its own wall
-    time (eager_ms).  Without graph the timed region is that eager pass.  Returns (ms per step, eager ms per step,
+    around the probe kernel's launches on its stream in every PROBE_STRIDE-th step (its average launch time, for the
+    roofline) and its own wall time (eager_ms).  Without graph the timed region is that eager pass.  Returns (ms per step, eager ms per step,
     probe kernel ms per launch)."""
     import torch
 
@@ -102,13 +105,17 @@ def time_steps(step, steps, warmup, graph, probe_kernel, probe_every=1, probe_fi
         torch.cuda.synchronize()
         ms = (time.perf_counter() - t0) * 1e3 / steps
         del g
-    ops.probe = {probe_kernel: []}
+    # the probe's two event records cost the stream a few microseconds each, so every PROBE_STRIDE-th step carries
+    # them (the first step always)
+    probes = {probe_kernel: []}
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(steps):
+    for i in range(steps):
+        ops.probe = probes if i % PROBE_STRIDE == 0 else None
         step()
     torch.cuda.synchronize()
     eager_ms = (time.perf_counter() - t0) * 1e3 / steps
+    ops.probe = probes
     # every probe_every-th launch of the probe kernel from launch probe_first on (the BailingMoeV2 block launches it
     # twice per step: for the shared expert and the routed experts)
     dom = [a.elapsed_time(b) for a, b in ops.probe[probe_kernel][probe_first::probe_every]]
