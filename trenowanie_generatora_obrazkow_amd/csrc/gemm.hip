@@ -41,14 +41,17 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
   static_assert(!F16 || EPI == EPI_STORE || EPI == EPI_SWIGLU, "fp16: forward epilogues only");
   using X = Elt<F16>;
   extern __shared__ __attribute__((aligned(1024))) char smem[];
-  __shared__ int64_t s_rstart[kMaxEGemm + 1];
+  __shared__ int s_rstart[kMaxEGemm + 1];  // row starts (M < 2^31: checked on the host)
   __shared__ int s_tstart[kMaxEGemm + 1];  // MGROUP: prefix of ceil(count / BM); KGROUP: one m-tile per expert
   __shared__ int s_gstart[A_BLK ? kMaxEGemm + 1 : 1];  // A_BLK: prefix of ceil(count / 128) (row groups)
   // per-row epilogue inputs of the tile (scatter index, routing weight), double-buffered by tile parity: a wave
-  // that has finished its epilogue may already fill the next tile's while others still read this one
-  // (2 KB each: 256 rows plus up to 3 leading rows, since the copy starts at the 16-byte boundary below row0)
-  __shared__ __attribute__((aligned(16))) int s_rowy[2][512];
-  __shared__ __attribute__((aligned(16))) float s_rowsc[2][512];
+  // that has finished its epilogue may already fill the next tile's while others still read this one.  The copy
+  // starts at the 16-byte boundary below row0 (up to 7 leading 2-byte elements) and writes whole 1 KB blocks: one
+  // for 128-row tiles, two for 256-row tiles (whose rows reach past the first 1 KB).  The smaller buffers keep the
+  // static LDS of the 128-row kernels low enough for two workgroups per CU.
+  constexpr int RDW = C::BM > 128 ? 512 : 256;
+  __shared__ __attribute__((aligned(16))) int s_rowy[2][RDW];
+  __shared__ __attribute__((aligned(16))) float s_rowsc[2][RDW];
   // int8 weights: the tile's per-column weight scales (bf16 or fp32), by tile parity like the row data
   __shared__ __attribute__((aligned(16))) float s_colsc[2][256];
 
@@ -93,7 +96,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
       if (e < E) {
         int64_t c = read_count(p.counts, p.counts64, e);
         c = c < 0 ? 0 : (c > p.M ? p.M : c);
-        s_rstart[e] = r0;
+        s_rstart[e] = (int)min(r0, p.M);  // (garbage counts can sum past M)
         s_tstart[e] = t0;
         r0 += c;
         t0 += MODE == MGROUP ? (int)((c + C::BM - 1) / C::BM) : 1;
@@ -104,7 +107,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
       }
     }
     if (lane == 63) {
-      s_rstart[E] = irs;
+      s_rstart[E] = (int)min(irs, p.M);
       s_tstart[E] = its;
     }
   }
@@ -191,7 +194,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
       }
       e = lo;
       row0 = s_rstart[e] + (int64_t)(mt - s_tstart[e]) * C::BM;
-      row_end = min(s_rstart[e + 1], p.M);
+      row_end = min((int64_t)s_rstart[e + 1], p.M);
       if (half >= 0) {
         row0 += half * (C::BM / 2);
         row_end = min(row_end, row0 + C::BM / 2);
@@ -204,7 +207,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
       e = mt / nb_i;
       i0 = (mt - e * nb_i) * C::BM;
       kstart = s_rstart[e];
-      const int64_t kend = min(s_rstart[e + 1], p.M);
+      const int64_t kend = min((int64_t)s_rstart[e + 1], p.M);
       kvalid = (int)max((int64_t)0, kend - kstart);
     }
     const int n0 = nb * (EPI == EPI_SWIGLU ? C::BN / 2 : C::BN);
@@ -310,8 +313,8 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
     const int par = tile_iter & 1;
     constexpr bool ROWDATA = MODE == MGROUP && (EPI == EPI_STORE || EPI == EPI_STORE_F32 || EPI == EPI_SWIGLU_BWD);
     static_assert(!ROWDATA || C::BM <= 256, "row data buffers hold 256 rows");
-    // The copies start at the 16-byte boundary at or below row0 (the direct loads move aligned 16-byte chunks) and
-    // take two instructions (1 KB + 16 bytes) so that the shifted 256 rows are always covered.
+    // The copies start at the 16-byte boundary at or below row0 (the direct loads move aligned 16-byte chunks); a
+    // 256-row tile takes two instructions (1 KB + 16 bytes of data) so that its shifted rows are always covered.
     [[maybe_unused]] int y_sh = 0, sc_sh = 0;  // leading rows in front of row0
     if constexpr (ROWDATA) {
       auto copy_rows = [&](const void* arr, int esz, char* dst) -> int {
@@ -326,7 +329,7 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
           i32x4 rs = make_rsrc(reinterpret_cast<const void*>(base));
           rs.z = __builtin_amdgcn_readfirstlane((int)min(bytes, (int64_t)0x7FFFFFF0));
           buf2lds((uint32_t)lane * 16u, rs, 0u, dst);
-          buf2lds(lane == 0 ? 1024u : kOOB, rs, 0u, dst + 1024);
+          if constexpr (C::BM > 128) buf2lds(lane == 0 ? 1024u : kOOB, rs, 0u, dst + 1024);
         }
         return sh;
       };
@@ -1097,7 +1100,7 @@ static GemmParams base_params(const void* counts, int counts_dtype, int64_t E, i
 
 static int check_common(const void* counts, int counts_dtype, int64_t E, int64_t M) {
   if (!counts || E <= 0 || M < 0) return HMOE_ERR_ARG;
-  if (E > kMaxEGemm) return HMOE_ERR_SHAPE;
+  if (E > kMaxEGemm || M > INT32_MAX) return HMOE_ERR_SHAPE;
   if (counts_dtype != HMOE_DT_I32 && counts_dtype != HMOE_DT_I64) return HMOE_ERR_DTYPE;
   return HMOE_OK;
 }
