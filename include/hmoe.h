@@ -143,6 +143,7 @@ int hmoe_make_schedule(const void* counts, int counts_dtype, int E, int64_t M, i
 
 /* ---------------------------------------------------------------------------------------------------------------
  * Grouped GEMMs (bf16 MFMA, fp32 accumulation, persistent tile scheduler over ragged expert groups)
+ * Every grouped GEMM takes E <= 1024 experts and M < 2^31 sorted rows (HMOE_ERR_SHAPE otherwise).
  * ------------------------------------------------------------------------------------------------------------- */
 
 /* grouped_mm: replaces aurora/moe_triton.py:65-90 (_grouped_kernel :22-56).

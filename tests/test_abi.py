@@ -117,6 +117,9 @@ def test_argument_validation_codes(lib):
     # direct-load offsets beyond 2^31 bytes
     assert L.hmoe_gate_up_swiglu(P, 4096, P, P, 3, 4096, 65536, P, 4, 1 << 20, P, None, 0, None) == -2
     assert L.hmoe_down_scatter(P, P, 3, 64, 64, P, 4, 48, P, P, P, None, 4, None) == -3  # int64 activations
+    # 2^31 routed rows or more (the GEMMs keep row starts in 32 bits)
+    assert L.hmoe_down_scatter(P, P, 3, 64, 64, P, 4, 1 << 31, P, P, P, None, 0, None) == -2
+    assert L.hmoe_grouped_wgrad(P, 64, P, 64, 3, 64, 64, P, 4, 1 << 31, P, 2, None) == -2
     # wgrad: output dtype, shapes
     assert L.hmoe_grouped_wgrad(P, 64, P, 64, 3, 64, 64, P, 4, 48, P, 3, None) == -3
     assert L.hmoe_grouped_wgrad(P, 64, P, 64, 3, 60, 64, P, 4, 48, P, 2, None) == -2
