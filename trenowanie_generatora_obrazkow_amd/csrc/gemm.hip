@@ -647,8 +647,12 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
     // is the byte offset from base of its row j's column 0, or -1 for a row past the tile's rows, and a piece goes
     // to base + rows.o[j] + (n0 + tile column) * es when that column is below ncols.  The reads of two sub-planes
     // are issued before their stores, so a pass waits for LDS once per sub-plane pair, not once per store.
-    auto drain_rows = [&](auto nsp_tag, int sp0, int rowbytes, int es, char* base, const RowOffs rows, int ncols) {
+    // PAIRED false: each piece's read just ahead of its store instead (what the bf16 forward epilogues measured
+    // fastest, by 1%)
+    auto drain_rows = [&](auto nsp_tag, int sp0, int rowbytes, int es, char* base, const RowOffs rows, int ncols,
+                          auto paired_tag) {
       constexpr int NSPX = decltype(nsp_tag)::value;
+      constexpr bool PAIRED = decltype(paired_tag)::value;
       const int c = lane & 7;
       auto read4 = [&](int sp, uint4* v) {
 #pragma unroll
@@ -663,18 +667,32 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
         for (int j = 0; j < 4; ++j)
           if (cok && rows.o[j] >= 0) *reinterpret_cast<uint4*>(base + rows.o[j] + (int64_t)n * es) = v[j];
       };
+      if constexpr (PAIRED) {
 #pragma unroll
-      for (int sp = 0; sp + 1 < NSPX; sp += 2) {
-        uint4 va[4], vb[4];
-        read4(sp, va);
-        read4(sp + 1, vb);
-        store4(sp, va);
-        store4(sp + 1, vb);
-      }
-      if constexpr (NSPX & 1) {
-        uint4 va[4];
-        read4(NSPX - 1, va);
-        store4(NSPX - 1, va);
+        for (int sp = 0; sp + 1 < NSPX; sp += 2) {
+          uint4 va[4], vb[4];
+          read4(sp, va);
+          read4(sp + 1, vb);
+          store4(sp, va);
+          store4(sp + 1, vb);
+        }
+        if constexpr (NSPX & 1) {
+          uint4 va[4];
+          read4(NSPX - 1, va);
+          store4(NSPX - 1, va);
+        }
+      } else {
+#pragma unroll
+        for (int sp = 0; sp < NSPX; ++sp) {
+          const int cw = (sp * 128 + c * 16) / es;
+          const int n = n0 + (cw / 32) * C::FSN + wn * 32 + cw % 32;
+          const bool cok = sp * 128 + c * 16 < rowbytes && n < ncols;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint4 v = *reinterpret_cast<const uint4*>(sp_addr(sp0 + sp, 8 * j + (lane >> 3), c * 16));
+            if (cok && rows.o[j] >= 0) *reinterpret_cast<uint4*>(base + rows.o[j] + (int64_t)n * es) = v;
+          }
+        }
       }
     };
     // the lane's drain rows of pass rbase (tile rows rbase + 8 j + lane / 8): o[j] = off(tile row, sorted row), or -1
@@ -723,10 +741,12 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
         char* const base = reinterpret_cast<char*>(p.C);
         if (p.c_f32) {
           park_all(std::true_type{});
-          drain_rows(std::integral_constant<int, C::FN * 32 * 4 / 128>{}, 0, C::FN * 32 * 4, 4, base, rows, p.N);
+          drain_rows(std::integral_constant<int, C::FN * 32 * 4 / 128>{}, 0, C::FN * 32 * 4, 4, base, rows, p.N,
+                     std::true_type{});
         } else {
           park_all(std::false_type{});
-          drain_rows(std::integral_constant<int, C::FN * 32 * 2 / 128>{}, 0, C::FN * 32 * 2, 2, base, rows, p.N);
+          drain_rows(std::integral_constant<int, C::FN * 32 * 2 / 128>{}, 0, C::FN * 32 * 2, 2, base, rows, p.N,
+                     std::true_type{});
         }
       } else if constexpr (EPI == EPI_STORE || EPI == EPI_STORE_F32) {
         constexpr int ES = EPI == EPI_STORE_F32 ? 4 : 2;
@@ -771,12 +791,13 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
         const RowOffs rows = rows_of(rbase, [&](int rt, int64_t row) {
           return (p.y_idx ? (int64_t)s_rowy[par][rt + y_sh] : row) * p.ldc * ES;
         });
-        drain_rows(std::integral_constant<int, NSP>{}, 0, RB, ES, reinterpret_cast<char*>(p.C), rows, p.N);
+        constexpr std::bool_constant<C::BE == 1> paired{};  // int8 weights: paired reads (bf16: one by one)
+        drain_rows(std::integral_constant<int, NSP>{}, 0, RB, ES, reinterpret_cast<char*>(p.C), rows, p.N, paired);
         if constexpr (C::BE == 2) {
           if (aux)
             drain_rows(std::integral_constant<int, (C::FN * 32 * 2 + 127) / 128>{}, NSP, C::FN * 32 * 2, 2,
                        reinterpret_cast<char*>(p.aux),
-                       rows_of(rbase, [&](int, int64_t row) { return row * p.ldc * 2; }), p.N);
+                       rows_of(rbase, [&](int, int64_t row) { return row * p.ldc * 2; }), p.N, paired);
         }
       } else if constexpr (EPI == EPI_SWIGLU) {
         // fragments b < FN/2 hold gate columns, b + FN/2 the matching up columns (tile columns + BN/2); the wave's
@@ -830,14 +851,16 @@ __global__ __launch_bounds__(C::NT, 1) void grouped_gemm_kernel(GemmParams p) {
           park_all(aux, std::true_type{});
         else
           park_all(aux, std::false_type{});
+        constexpr std::bool_constant<C::BE == 1> paired{};  // int8 weights: paired reads (bf16: one by one)
         drain_rows(std::integral_constant<int, NSP>{}, 0, RB, 2, reinterpret_cast<char*>(p.C),
-                   rows_of(rbase, [&](int, int64_t row) { return row * p.ldc * 2; }), p.N);
+                   rows_of(rbase, [&](int, int64_t row) { return row * p.ldc * 2; }), p.N, paired);
         if constexpr (C::BE == 2) {
           if (aux) {
             const RowOffs rows = rows_of(rbase, [&](int, int64_t row) { return row * (int64_t)(2 * p.h) * 2; });
-            drain_rows(std::integral_constant<int, NSP>{}, NSP, RB, 2, reinterpret_cast<char*>(p.aux), rows, p.N);
+            drain_rows(std::integral_constant<int, NSP>{}, NSP, RB, 2, reinterpret_cast<char*>(p.aux), rows, p.N,
+                       paired);
             drain_rows(std::integral_constant<int, NSP>{}, 2 * NSP, RB, 2, reinterpret_cast<char*>(p.aux + p.h), rows,
-                       p.N);
+                       p.N, paired);
           }
         }
       } else if constexpr (EPI == EPI_SWIGLU_BWD) {
