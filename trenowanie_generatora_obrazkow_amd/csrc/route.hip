@@ -775,6 +775,8 @@ __global__ __launch_bounds__(256) void dispatch_index_kernel(const void* __restr
 
 // one wave per token: sorted positions of its k rows, index arrays, then the row copies x[t] -> xs[pos_j] and into
 // the row-group tiles (64-byte pieces: slice s of row pos_j, its chunks swizzled as in the K-major LDS image)
+// KT: the slot count k when it is 1, 2, 4 or 8 (0: any k up to kMaxK), so the per-slot arrays hold only k entries
+template <int KT>
 __global__ __launch_bounds__(256) void dispatch_scatter_kernel(
     const void* __restrict__ ids, int ids64, const void* __restrict__ tw, int tw_dtype, int ws_f16, int64_t T, int k,
     int E,
@@ -782,15 +784,29 @@ __global__ __launch_bounds__(256) void dispatch_scatter_kernel(
     int64_t ldx, int64_t d, uint16_t* __restrict__ xs, int32_t* __restrict__ order, int32_t* __restrict__ a_idx,
     int32_t* __restrict__ inv_pos, uint16_t* __restrict__ w_sorted, char* __restrict__ xs_tiles,
     const int32_t* __restrict__ starts, const int32_t* __restrict__ gstart) {
+  constexpr int KA = KT > 0 ? KT : kMaxK;
+  if constexpr (KT > 0) k = KT;
   const int lane = threadIdx.x & 63;
   const int nwaves = blockDim.x >> 6;
   const int64_t nvec = d / 8;
+  // rows of up to 2048 elements: the lane's (at most 4) chunks of the token's row are loaded first, since their
+  // address needs no lookup, and stay in registers while the positions are looked up
+  const bool pre = (xs || xs_tiles) && nvec <= 256;
   for (int64_t t = (int64_t)blockIdx.x * nwaves + (threadIdx.x >> 6); t < T; t += (int64_t)gridDim.x * nwaves) {
-    int64_t pos[kMaxK];
-    int64_t tpos[kMaxK];  // tiles: byte offset of the row's slice 0 (its group's slice 0 + 64 * row in group)
-    int tsw[kMaxK];       // tiles: the row's chunk swizzle
+    const uint4* src = reinterpret_cast<const uint4*>(x + t * ldx);
+    uint4 xv[4];
+    if (pre) {
 #pragma unroll
-    for (int j = 0; j < kMaxK; ++j) {
+      for (int i = 0; i < 4; ++i) {
+        const int64_t c = lane + 64 * i;
+        xv[i] = c < nvec ? src[c] : make_uint4(0, 0, 0, 0);
+      }
+    }
+    int64_t pos[KA];
+    int64_t tpos[KA];  // tiles: byte offset of the row's slice 0 (its group's slice 0 + 64 * row in group)
+    int tsw[KA];       // tiles: the row's chunk swizzle
+#pragma unroll
+    for (int j = 0; j < KA; ++j) {
       pos[j] = -1;
       tpos[j] = 0;
       tsw[j] = 0;
@@ -814,11 +830,9 @@ __global__ __launch_bounds__(256) void dispatch_scatter_kernel(
       }
     }
     if (xs || xs_tiles) {
-      const uint4* src = reinterpret_cast<const uint4*>(x + t * ldx);
-      for (int64_t c = lane; c < nvec; c += 64) {
-        const uint4 v = src[c];
+      auto put = [&](int64_t c, const uint4 v) {
 #pragma unroll
-        for (int j = 0; j < kMaxK; ++j)
+        for (int j = 0; j < KA; ++j)
           if (j < k && pos[j] >= 0) {
             if (xs) reinterpret_cast<uint4*>(xs + pos[j] * d)[c] = v;
             if (xs_tiles) {  // chunk c: slice c / 4, logical chunk c % 4 of the row's 64 bytes
@@ -826,6 +840,13 @@ __global__ __launch_bounds__(256) void dispatch_scatter_kernel(
               *reinterpret_cast<uint4*>(xs_tiles + off) = v;
             }
           }
+      };
+      if (pre) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (lane + 64 * i < nvec) put(lane + 64 * i, xv[i]);
+      } else {
+        for (int64_t c = lane; c < nvec; c += 64) put(c, src[c]);
       }
     }
   }
@@ -1555,10 +1576,22 @@ static int dispatch_impl(const void* topk_ids, int ids_dtype, const void* topk_w
   HMOE_CHECK_LAUNCH();
   if (M > 0 && (xs || xs_tiles)) {
     const int grid = grid_for(T, 4, 8192);
-    hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(grid), dim3(256), 0, s, topk_ids, ids64, topk_w, w_dtype,
-                       (int)f16, T, k, E, hist, rank, static_cast<const uint16_t*>(x), ldx, d, static_cast<uint16_t*>(xs), order,
-                       a_idx, inv_pos, w_sorted,
-                       static_cast<char*>(xs_tiles), starts, gstart);
+#define HMOE_SCAT(KT)                                                                                              \
+  hipLaunchKernelGGL(dispatch_scatter_kernel<KT>, dim3(grid), dim3(256), 0, s, topk_ids, ids64, topk_w, w_dtype,      \
+                     (int)f16, T, k, E, hist, rank, static_cast<const uint16_t*>(x), ldx, d,                        \
+                     static_cast<uint16_t*>(xs), order, a_idx, inv_pos, w_sorted, static_cast<char*>(xs_tiles),      \
+                     starts, gstart)
+    if (k == 1)
+      HMOE_SCAT(1);
+    else if (k == 2)
+      HMOE_SCAT(2);
+    else if (k == 4)
+      HMOE_SCAT(4);
+    else if (k == 8)
+      HMOE_SCAT(8);
+    else
+      HMOE_SCAT(0);
+#undef HMOE_SCAT
     HMOE_CHECK_LAUNCH();
   } else if (M > 0) {
     hipLaunchKernelGGL(dispatch_index_kernel, dim3(grid_for(M, 256, 8192)), dim3(256), 0, s, topk_ids, ids64, topk_w,
