@@ -1409,9 +1409,20 @@ __global__ __launch_bounds__(256) void unpermute_bwd_kernel(const void* __restri
           }
         };
         if constexpr (EMAX > 0) {
-          // experts past E have zero weight columns (wreg), so their (clamped, finite) router gradient adds 0
+          if (E == EMAX) {  // the token's whole gradient row in four 16-byte (scalar) loads
+            float g[EMAX];
 #pragma unroll
-          for (int e = 0; e < EMAX; ++e) fma_row(dlogits[t * E + min(e, E - 1)], wreg[e]);
+            for (int q = 0; q < EMAX / 4; ++q) {
+              const float4 v = reinterpret_cast<const float4*>(dlogits + t * EMAX)[q];
+              g[4 * q] = v.x; g[4 * q + 1] = v.y; g[4 * q + 2] = v.z; g[4 * q + 3] = v.w;
+            }
+#pragma unroll
+            for (int e = 0; e < EMAX; ++e) fma_row(g[e], wreg[e]);
+          } else {
+            // experts past E have zero weight columns (wreg), so their (clamped, finite) router gradient adds 0
+#pragma unroll
+            for (int e = 0; e < EMAX; ++e) fma_row(dlogits[t * E + min(e, E - 1)], wreg[e]);
+          }
         } else {
           for (int e = 0; e < E; ++e)
             fma_row(dlogits[t * E + e], active ? *reinterpret_cast<const uint4*>(wr + (int64_t)e * d + col)
