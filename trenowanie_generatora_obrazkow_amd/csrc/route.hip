@@ -1441,35 +1441,6 @@ __global__ __launch_bounds__(256) void unpermute_bwd_kernel(const void* __restri
   }
 }
 
-// Workgroups of `kern` (threads each, no dynamic LDS) resident on the whole device at once, or 0 if the runtime
-// cannot tell.  Cached per (device, kernel, block size): the un-permute asks for two kernels and a few block sizes.
-static int resident_blocks(const void* kern, int threads) {
-  struct Entry {
-    std::atomic<const void*> k{nullptr};
-    std::atomic<int> key{-1}, n{0};  // key = device * 4096 + threads, set before k is published
-  };
-  static Entry cache[32];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  const int key = dev * 4096 + threads;
-  for (auto& c : cache)
-    if (c.k.load(std::memory_order_acquire) == kern && c.key.load(std::memory_order_relaxed) == key)
-      return c.n.load(std::memory_order_relaxed);
-  int per_cu = 0, cus = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, 0) != hipSuccess || per_cu <= 0) return 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 0;
-  const int n = per_cu * cus;
-  for (auto& c : cache) {  // first free entry (a race may fill two entries with the same answer: harmless)
-    int free_key = -1;
-    if (c.key.compare_exchange_strong(free_key, key, std::memory_order_relaxed)) {
-      c.n.store(n, std::memory_order_relaxed);
-      c.k.store(kern, std::memory_order_release);
-      break;
-    }
-  }
-  return n;
-}
-
 static inline int grid_for(int64_t work, int per_block, int cap = 8192) {
   int64_t g = (work + per_block - 1) / per_block;
   if (g < 1) g = 1;
@@ -1899,19 +1870,13 @@ int hmoe_unpermute_bwd(const void* dxs, int dxs_dtype, const int32_t* inv_pos, c
   const int64_t vec = d / 8;
   const int threads = (int)(vec >= 256 ? 256 : ((vec + 63) / 64) * 64);
   const unsigned slabs = (unsigned)((vec + threads - 1) / threads);
+  const unsigned tgrid = (unsigned)((T + 1) / 2 < 4096 ? (T + 1) / 2 : 4096);
   const uint16_t* wp = static_cast<const uint16_t*>(wr);
   uint16_t* dxp = static_cast<uint16_t*>(dx);
   const bool regs = dlogits == nullptr || E <= 16;
-  // one round of resident workgroups walks all the tokens: a workgroup loads its router-weight columns once, and a
-  // second round would only repeat that (at C5: 48 -> 42 us against 4096 workgroups)
-#define HMOE_UNPERM(F, EM)                                                                                           \
-  do {                                                                                                               \
-    auto kern = unpermute_bwd_kernel<F, EM>;                                                                         \
-    const int64_t res = resident_blocks(reinterpret_cast<const void*>(kern), threads) / (int64_t)slabs;              \
-    const int64_t cap = res > 0 ? res : 4096;                                                                        \
-    const unsigned tgrid = (unsigned)((T + 1) / 2 < cap ? (T + 1) / 2 : cap);                                        \
-    hipLaunchKernelGGL(kern, dim3(tgrid, slabs), dim3(threads), 0, s, dxs, inv_pos, dlogits, wp, T, k, d, E, dxp); \
-  } while (0)
+#define HMOE_UNPERM(F, EM)                                                                                         \
+  hipLaunchKernelGGL((unpermute_bwd_kernel<F, EM>), dim3(tgrid, slabs), dim3(threads), 0, s, dxs, inv_pos, dlogits, \
+                     wp, T, k, d, E, dxp)
   if (dxs_dtype == HMOE_DT_F32) {
     if (regs)
       HMOE_UNPERM(true, 16);
