@@ -89,7 +89,7 @@ def test_fuse_moe_int8_buffers():
     """quant="int8" (aurora/hf_compat.py:159-162): int8 stacked weights with (E, out) bf16 scales that dequantise
     to within half a step of the stacked bf16 weights."""
     torch.manual_seed(1)
-    d, h, E = 32, 24, 5
+    d, h, E = 32, 48, 5
     blk = _Block(d, h, E)
     wgu = torch.stack([torch.cat([e.gate_proj.weight, e.up_proj.weight]).t() for e in blk.experts]).detach()
     wd = torch.stack([e.down_proj.weight.t() for e in blk.experts]).detach()
@@ -103,6 +103,62 @@ def test_fuse_moe_int8_buffers():
         assert ((deq - w).abs() <= s.float().unsqueeze(1) * (0.5 + 127 * 2.0 ** -8) * 1.01).all()
     with pytest.raises(RuntimeError, match="GPU"):
         blk.moe_infer(torch.randn(4, d), torch.zeros(4, 2, dtype=torch.long), torch.ones(4, 2))
+
+
+@pytest.mark.parametrize("quant,gr", [("", 8), ("int8", 16)])
+def test_fuse_moe_pads_off_granule_widths(quant, gr):
+    """Widths off the kernels' copy granule: the stacks are zero-padded to it once, the real block sits in place
+    ([gate | pad | up | pad] along the output axis), int8 values and scales of the real columns are those of the
+    unpadded stack bit for bit, and the padded layer computed in float64 equals the unpadded one on the d columns
+    (padded hidden columns are silu(0) * 0 and meet zero down rows)."""
+    torch.manual_seed(3)
+    d, h, E = 36, 20, 3
+    blk = _Block(d, h, E)
+    wgu = torch.stack([torch.cat([e.gate_proj.weight, e.up_proj.weight]).t() for e in blk.experts]).detach()
+    wd = torch.stack([e.down_proj.weight.t() for e in blk.experts]).detach()
+    assert hf_compat.fuse_moe(nn.Sequential(blk), quant=quant) == 1
+    dp, hp = -(-d // gr) * gr, -(-h // gr) * gr
+    assert blk._wgu.shape == (E, dp, 2 * hp) and blk._wd.shape == (E, hp, dp)
+    cols = list(range(h)) + list(range(hp, hp + h))
+    if quant:
+        q_gu, s_gu = hf_compat._quant_int8(wgu)
+        q_d, s_d = hf_compat._quant_int8(wd)
+        assert torch.equal(blk._wgu[:, :d, cols], q_gu) and torch.equal(blk._wgu_s[:, cols], s_gu)
+        assert torch.equal(blk._wd[:, :h, :d], q_d) and torch.equal(blk._wd_s[:, :d], s_d)
+        gu_p, d_p = hf_compat._dequant(blk._wgu, blk._wgu_s, torch.float64), hf_compat._dequant(blk._wd, blk._wd_s,
+                                                                                                  torch.float64)
+        gu_r, d_r = hf_compat._dequant(q_gu, s_gu, torch.float64), hf_compat._dequant(q_d, s_d, torch.float64)
+    else:
+        assert torch.equal(blk._wgu[:, :d, cols], wgu) and torch.equal(blk._wd[:, :h, :d], wd)
+        gu_p, d_p, gu_r, d_r = blk._wgu.double(), blk._wd.double(), wgu.double(), wd.double()
+    pad_mask = torch.ones(E, dp, 2 * hp, dtype=torch.bool)
+    pad_mask[:, :d, cols] = False
+    assert (gu_p[pad_mask] == 0).all() and d_p[:, h:].abs().sum() == 0 and d_p[:, :, d:].abs().sum() == 0
+    x = torch.randn(7, d, dtype=torch.float64)
+    xp = torch.nn.functional.pad(x, (0, dp - d))
+    for e in range(E):
+        gp = xp @ gu_p[e]
+        yp = (torch.nn.functional.silu(gp[:, :hp]) * gp[:, hp:]) @ d_p[e]
+        g = x @ gu_r[e]
+        y = (torch.nn.functional.silu(g[:, :h]) * g[:, h:]) @ d_r[e]
+        torch.testing.assert_close(yp[:, :d], y, rtol=1e-12, atol=1e-12)
+
+
+def test_pad_operands_for_grouped_mm():
+    """moe_triton.pad_operands: K to a multiple of 8, N to 8 (16-bit weights) or 16 (int8), zeros in the padding,
+    aligned shapes passed through as the same tensors."""
+    a, w = torch.randn(10, 13).bfloat16(), torch.randn(3, 13, 7).bfloat16()
+    ap, wp, sp = moe_triton.pad_operands(a, w)
+    assert ap.shape == (10, 16) and wp.shape == (3, 16, 8) and sp is None
+    assert torch.equal(ap[:, :13], a) and (ap[:, 13:] == 0).all()
+    assert torch.equal(wp[:, :13, :7], w) and wp[:, 13:].abs().sum() == 0 and wp[:, :, 7:].abs().sum() == 0
+    q, s = torch.randint(-127, 128, (3, 16, 20), dtype=torch.int8), torch.rand(3, 20).bfloat16()
+    a16 = torch.randn(4, 16).bfloat16()
+    ap, qp, sp = moe_triton.pad_operands(a16, q, s)
+    assert ap is a16 and qp.shape == (3, 16, 32) and sp.shape == (3, 32)
+    assert torch.equal(qp[:, :, :20], q) and (qp[:, :, 20:] == 0).all() and torch.equal(sp[:, :20], s)
+    w8 = torch.randn(2, 16, 8).bfloat16()
+    assert moe_triton.pad_operands(a16, w8)[1] is w8
 
 
 def test_quant_int8_matches_reference_rule():

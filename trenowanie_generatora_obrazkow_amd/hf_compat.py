@@ -18,22 +18,37 @@ def _fused_moe_infer(self, x, topk_ids, topk_weight):
     """aurora/hf_compat.py:63-82 (the fused branch): stable sort of the flat routed rows by expert, gate/up GEMM
     over gathered token rows with the SwiGLU fused into its epilogue, down GEMM scaled by the bf16-rounded routing
     weight and scattered back to (token, slot) order, sum over the k slots.  Layers fused with quant="int8" run the
-    int8-weight forms of the two GEMMs (per-column scales applied to the fp32 sums).  An expert id outside [0, E)
+    int8-weight forms of the two GEMMs (per-column scales applied to the fp32 sums).  Blocks whose act_fn is not
+    silu run the two grouped GEMMs with the module's act_fn applied to g, times u, in between (the reference's
+    order of operations).  Widths fuse_moe padded are padded on x and cut from the output.  An expert id outside [0, E)
     in topk_ids routes its slot nowhere: the slot adds nothing to the output, and the count of such ids is kept on
     the device in self._n_invalid (read by invalid_expert_ids, which is the only place that synchronises)."""
     n, k = topk_ids.shape
-    E = self._wgu.shape[0]
+    E, dp = self._wgu.shape[0], self._wgu.shape[1]
     if self._mode is None:  # decided on the device the weights ended up on
         self._mode = _pick_mode(x.device, x.dtype)
-    if self._act is not torch.nn.functional.silu and not isinstance(self._act, torch.nn.SiLU):
-        raise NotImplementedError("the hmoe SwiGLU epilogue implements silu(g) * u only")
-    x = x.contiguous()
-    disp, act, _ = ops.routed_gate_up(x, topk_ids.contiguous(), E, self._wgu, topk_w=topk_weight.contiguous(),
-                                      wgu_s=self._wgu_s, want_inv=True)
+    d = x.shape[-1]
+    x = x.contiguous() if dp == d else torch.nn.functional.pad(x, (0, dp - d))  # stacks padded by fuse_moe
     M = n * k
-    y, _ = ops.down_scatter(act, self._wd, disp.counts, M, disp.w_sorted, disp.order, wd_s=self._wd_s)
+    if _is_silu(self._act):
+        disp, act, _ = ops.routed_gate_up(x, topk_ids.contiguous(), E, self._wgu, topk_w=topk_weight.contiguous(),
+                                          wgu_s=self._wgu_s, want_inv=True)
+        y, _ = ops.down_scatter(act, self._wd, disp.counts, M, disp.w_sorted, disp.order, wd_s=self._wd_s)
+    else:
+        # any other activation: the module's own act_fn between the two grouped GEMMs, as the reference's fused
+        # branch applies it (aurora/hf_compat.py:79-81); gathered rows in, routing weight and scatter in the down GEMM
+        disp = ops.dispatch(topk_ids.contiguous(), E, topk_w=topk_weight.contiguous(), want_xs=False, dtype=x.dtype)
+        g, u = ops.grouped_mm(x, self._wgu, disp.counts, M, a_idx=disp.a_idx, w_scale=self._wgu_s).chunk(2, dim=-1)
+        y = ops.grouped_mm((self._act(g) * u).contiguous(), self._wd, disp.counts, M, y_idx=disp.order,
+                           scale=disp.w_sorted, w_scale=self._wd_s)
     self._n_invalid = disp.n_invalid
-    return ops.combine(y, n, k, inv_pos=disp.inv_pos)
+    out = ops.combine(y, n, k, inv_pos=disp.inv_pos)
+    return out if dp == d else out[:, :d].contiguous()
+
+
+def _is_silu(act):
+    """The activations the fused SwiGLU epilogue computes: silu(g) * u (torch's functional silu or an nn.SiLU)."""
+    return act is torch.nn.functional.silu or isinstance(act, torch.nn.SiLU)
 
 
 def invalid_expert_ids(model) -> int:
@@ -46,6 +61,26 @@ def invalid_expert_ids(model) -> int:
         if isinstance(n, torch.Tensor):
             total += int(n.item())
     return total
+
+
+def _pad_stacks(wgu, wd, granule):
+    """Zero-pad the stacked (E, d, 2h) gate|up and (E, h, d) down weights so that d and h are multiples of `granule`
+    (8 for 16-bit weights, 16 for int8: the GEMMs' copy granule; the reference's Triton kernel masks any width).
+    Padded gate and up columns give g = u = 0, so the padded hidden columns are act(0) * 0 = 0, and the down
+    weights' padded rows are zero as well: the first d output columns are those of the unpadded layer, exactly (the
+    extra k terms add exact zeros to the fp32 sums).  int8 scales of the padded columns come out at the floor value
+    and multiply zeros."""
+    E, d, h2 = wgu.shape
+    h = h2 // 2
+    dp, hp = -(-d // granule) * granule, -(-h // granule) * granule
+    if (dp, hp) == (d, h):
+        return wgu, wd
+    gu = wgu.new_zeros(E, dp, 2 * hp)
+    gu[:, :d, :h] = wgu[:, :, :h]
+    gu[:, :d, hp:hp + h] = wgu[:, :, h:]
+    dn = wd.new_zeros(E, hp, dp)
+    dn[:, :h, :d] = wd
+    return gu, dn
 
 
 def _dequant(w, scale, dtype):
@@ -102,6 +137,7 @@ def fuse_moe(model, quant=""):
         # device or dtype carries them along
         wgu = torch.stack([torch.cat([e.gate_proj.weight, e.up_proj.weight]).t() for e in experts]).contiguous()
         wd = torch.stack([e.down_proj.weight.t() for e in experts]).contiguous()
+        wgu, wd = _pad_stacks(wgu, wd, 16 if quant else 8)
         for name, w in (("_wgu", wgu), ("_wd", wd)):
             w, sc = _quant_int8(w) if quant else (w, None)
             mod.register_buffer(name, w, persistent=False)

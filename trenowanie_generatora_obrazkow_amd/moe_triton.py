@@ -37,7 +37,8 @@ def grouped_mm(a: torch.Tensor, w: torch.Tensor, counts: torch.Tensor, sched=Non
     output) is accepted for call compatibility; the kernel derives its own tile map from `counts` on the device.
     a is bf16 or fp16 (the products run on the matching MFMA, the output has a's type); w has a's type, or is int8
     with w_scale (E, N) (aurora/moe_triton.py:44-51): the integers enter the 16-bit products exactly and the
-    per-column scale multiplies the fp32 sum, before `scale`."""
+    per-column scale multiplies the fp32 sum, before `scale`.  K and N need not be multiples of the copy granule:
+    such operands are zero-padded on the device first (pad_operands)."""
     M = a_idx.numel() if a_idx is not None else a.shape[0]
     assert w.stride(2) == 1, "w must be (E, K, N) with contiguous rows"
     if a.dtype not in (torch.bfloat16, torch.float16) or w.dtype not in (a.dtype, torch.int8):
@@ -50,5 +51,26 @@ def grouped_mm(a: torch.Tensor, w: torch.Tensor, counts: torch.Tensor, sched=Non
         a_idx = a_idx.to(torch.int32)
     if y_idx is not None and y_idx.dtype != torch.int32:
         y_idx = y_idx.to(torch.int32)
-    return ops.grouped_mm(a, w, counts, M, a_idx=a_idx.contiguous() if a_idx is not None else None,
-                          y_idx=y_idx.contiguous() if y_idx is not None else None, scale=scale, w_scale=w_scale)
+    N = w.shape[2]
+    a, w, w_scale = pad_operands(a, w, w_scale)
+    y = ops.grouped_mm(a, w, counts, M, a_idx=a_idx.contiguous() if a_idx is not None else None,
+                       y_idx=y_idx.contiguous() if y_idx is not None else None, scale=scale, w_scale=w_scale)
+    return y if y.shape[1] == N else y[:, :N].contiguous()
+
+
+def pad_operands(a, w, w_scale=None):
+    """Zero-pad K and N up to the kernels' copy granule (aurora/moe_triton.py:43-44,56 masks any K and N; the direct
+    global -> LDS copies here move 16-byte pieces): K to a multiple of 8, N to 8 (16-bit weights) or 16 (int8
+    weights, whose padded scale columns are zero).  Zero k terms add exact zeros to the fp32 sums and padded output
+    columns are dropped, so the N valid columns are what the unpadded product gives.  Shapes already aligned pass
+    through untouched; the padding is a device copy of a and w on each call (fuse_moe pads its stacks once)."""
+    K, N = w.shape[1], w.shape[2]
+    Kp = -(-K // 8) * 8
+    Np = -(-N // (16 if w.dtype == torch.int8 else 8)) * (16 if w.dtype == torch.int8 else 8)
+    if Kp != K:
+        a = torch.nn.functional.pad(a, (0, Kp - K))
+    if (Kp, Np) != (K, N):
+        w = torch.nn.functional.pad(w, (0, Np - N, 0, Kp - K))
+        if w_scale is not None:
+            w_scale = torch.nn.functional.pad(w_scale, (0, Np - N))
+    return a, w, w_scale
