@@ -449,116 +449,304 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restr
   }
 }
 
-// ---------------------------------------------------------------------------------------------------------------
-// BailingMoeV2 (sigmoid, group-limited) router.  A workgroup of 8 waves routes 8 x kSgTW tokens (two per wave: four
-// waves per SIMD at T = 8192, where four tokens per wave left two and measured 25% slower).  The router weight
-// and the workgroup's token values stream through LDS in chunks of 64 elements (double-buffered): weight rows as
-// bf16 with a row pitch of kSgPitch bytes (the lanes' 16-byte reads of 64 consecutive rows fall on distinct banks),
-// token values widened to fp32 once when staged and read back as wave-uniform broadcasts.  Lane l owns experts l,
-// l + 64, ...; each logit is the sequential fma sum over the row in element order (x[0]*w[0] first), and each
-// 8-element piece of weight widened to fp32 once serves the wave's kSgTW tokens.
-// ---------------------------------------------------------------------------------------------------------------
-constexpr int kSgTW = 2, kSgChunk = 64, kSgPitch = 144;
-constexpr int kSgWaves = 8, kSgThreads = 64 * kSgWaves;
-constexpr int kSgTok = kSgWaves * kSgTW;             // tokens per workgroup
-constexpr int kSgXBytes = kSgTok * kSgChunk * 4;     // fp32 token values per chunk buffer
+// Selection of the sigmoid, group-limited router for four tokens per wave: the 16-lane segment q of the wave takes
+// one token, lane j of it holds experts i * 16 + j (i < EPS).  The steps and orders are route_select<true>'s (scores,
+// routing values, group values as the sum of the two largest with multiplicity, topk_group groups by descending value
+// with ties to the lower group, then the k largest routing values among the kept groups with ties to the lower
+// expert, weights = the selected scores over their sum in selection order plus 1e-20, times scaling), with the
+// reductions over the segment's 16 lanes (row-local DPP exchanges) and the winner's score carried through them.
+// Every lane runs the same instructions (dead tokens included, with live false), so the exchanges see every lane.
+template <int S>
+__device__ __forceinline__ void seg_argmax_step(float& bv, int& be, float& bp) {
+  const float ov = lane_xor<S>(bv), op = lane_xor<S>(bp);
+  const int oe = lane_xor_i<S>(be);
+  if (oe != 0x7fffffff && (be == 0x7fffffff || ov > bv || (ov == bv && oe < be))) {
+    bv = ov;
+    be = oe;
+    bp = op;
+  }
+}
 
-template <int EPL>
-__global__ __launch_bounds__(kSgThreads) void route_sigmoid_kernel(const uint16_t* __restrict__ x, int64_t ldx,
-                                                            const uint16_t* __restrict__ wr,
-                                                            const float* __restrict__ bias, int T, int d, int E,
-                                                            int k, float scaling, float* __restrict__ scores,
-                                                            int32_t* __restrict__ ids, float* __restrict__ wout,
-                                                            int n_group, int topk_group) {
+template <int EPS>
+__device__ __forceinline__ void route_select_sig16(const float (&lg)[EPS], const float (&bsv)[EPS], bool has_bias,
+                                                   int64_t t, bool live, int lane, int E, int k, float scaling,
+                                                   float* __restrict__ scores, int32_t* __restrict__ ids,
+                                                   float* __restrict__ wout, int n_group, int topk_group) {
 #pragma clang fp contract(off)
-  // [2][EPL * 64][kSgPitch] bf16 weight rows, then [2][kSgTok][kSgChunk] fp32 token values
-  extern __shared__ __attribute__((aligned(16))) char s_w[];
-  constexpr int ER = EPL * 64;       // expert rows staged (rows past E are zero)
-  constexpr int PIECES = ER * 8;     // 16-byte weight pieces per chunk
-  constexpr int PPT = PIECES / kSgThreads;  // weight pieces per thread
-  char* const s_x = s_w + 2 * ER * kSgPitch;
+  const int j16 = lane & 15;
+  float num[EPS], key[EPS];
+#pragma unroll
+  for (int i = 0; i < EPS; ++i) {
+    const int e = i * 16 + j16;
+    num[i] = 0.0f;
+    key[i] = -__builtin_inff();
+    if (e < E) {
+      num[i] = __fdiv_rn(1.0f, __fadd_rn(1.0f, hexp(-lg[i])));
+      key[i] = has_bias ? __fadd_rn(num[i], bsv[i]) : num[i];
+      if (live && scores) scores[t * E + e] = num[i];
+    }
+  }
+  if (topk_group < n_group) {
+    const int eg = E / n_group;  // a power of two in [2, 64] (checked on the host)
+    float m1[EPS], m2[EPS];
+#pragma unroll
+    for (int i = 0; i < EPS; ++i) {
+      m1[i] = key[i];
+      m2[i] = -__builtin_inff();
+    }
+    // the two largest values (with multiplicity) of each run of min(eg, 16) lanes
+    auto fold = [&](auto sc) {
+      constexpr int SS = decltype(sc)::value;
+      if (SS < eg) {
+#pragma unroll
+        for (int i = 0; i < EPS; ++i) {
+          const float o1 = lane_xor<SS>(m1[i]), o2 = lane_xor<SS>(m2[i]);
+          const float n2 = fmaxf(fminf(m1[i], o1), fmaxf(m2[i], o2));
+          m1[i] = fmaxf(m1[i], o1);
+          m2[i] = n2;
+        }
+      }
+    };
+    fold(std::integral_constant<int, 1>());
+    fold(std::integral_constant<int, 2>());
+    fold(std::integral_constant<int, 4>());
+    fold(std::integral_constant<int, 8>());
+    // groups of 32 or 64 experts span 2 or 4 consecutive slots: merge their pairs in the lane
+    auto merge = [&](auto nc) {
+      constexpr int NS = decltype(nc)::value;
+      if constexpr (NS <= EPS) {
+#pragma unroll
+        for (int b = 0; b < EPS; b += NS) {
+          float a1 = m1[b], a2 = m2[b];
+#pragma unroll
+          for (int i = b + 1; i < b + NS; ++i) {
+            const float n2 = fmaxf(fminf(a1, m1[i]), fmaxf(a2, m2[i]));
+            a1 = fmaxf(a1, m1[i]);
+            a2 = n2;
+          }
+#pragma unroll
+          for (int i = b; i < b + NS; ++i) {
+            m1[i] = a1;
+            m2[i] = a2;
+          }
+        }
+      }
+    };
+    if (eg == 32) merge(std::integral_constant<int, 2>());
+    if (eg == 64) merge(std::integral_constant<int, 4>());
+    float gs[EPS];
+    bool gsel[EPS];
+#pragma unroll
+    for (int i = 0; i < EPS; ++i) {
+      gs[i] = __fadd_rn(m1[i], m2[i]);
+      gsel[i] = false;
+    }
+    for (int jj = 0; jj < topk_group; ++jj) {
+      float bv = 0.0f, bp = 0.0f;
+      int be = 0x7fffffff;
+#pragma unroll
+      for (int i = 0; i < EPS; ++i) {
+        const int e = i * 16 + j16;
+        if (e < E && !gsel[i]) argmax_take(bv, be, gs[i], e / eg);
+      }
+      seg_argmax_step<8>(bv, be, bp);
+      seg_argmax_step<4>(bv, be, bp);
+      seg_argmax_step<2>(bv, be, bp);
+      seg_argmax_step<1>(bv, be, bp);
+#pragma unroll
+      for (int i = 0; i < EPS; ++i)
+        if ((i * 16 + j16) / eg == be) gsel[i] = true;
+    }
+#pragma unroll
+    for (int i = 0; i < EPS; ++i)
+      if (!gsel[i]) key[i] = -__builtin_inff();
+  }
+  bool taken[EPS];
+#pragma unroll
+  for (int i = 0; i < EPS; ++i) taken[i] = false;
+  float ssum = 0.0f, my_p = 0.0f;
+  int my_e = 0;
+  for (int jj = 0; jj < k; ++jj) {
+    float bv = 0.0f, bp = 0.0f;
+    int be = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < EPS; ++i) {
+      const int e = i * 16 + j16;
+      if (e < E && !taken[i] && (be == 0x7fffffff || key[i] > bv)) {
+        bv = key[i];
+        be = e;
+        bp = num[i];
+      }
+    }
+    seg_argmax_step<8>(bv, be, bp);
+    seg_argmax_step<4>(bv, be, bp);
+    seg_argmax_step<2>(bv, be, bp);
+    seg_argmax_step<1>(bv, be, bp);
+#pragma unroll
+    for (int i = 0; i < EPS; ++i)
+      if (be == i * 16 + j16) taken[i] = true;
+    ssum = jj == 0 ? bp : __fadd_rn(ssum, bp);
+    if (j16 == jj) {
+      my_e = be;
+      my_p = bp;
+    }
+  }
+  if (live && j16 < k) {
+    const float den = __fadd_rn(ssum, 1e-20f);
+    ids[t * k + j16] = my_e;
+    wout[t * k + j16] = __fmul_rn(__fdiv_rn(my_p, den), scaling);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// BailingMoeV2 (sigmoid, group-limited) router on the fp32 matrix cores.  v_mfma_f32_16x16x4_f32 forms each output
+// as four fused multiply-adds in k order, acc = fma(a3, b3, fma(a2, b2, fma(a1, b1, fma(a0, b0, acc)))), each
+// rounded once with denormals kept (an in-bounds probe of 4.2 M outputs -- cancelling sums, products in the denormal
+// range, denormal inputs -- matched that chain bit for bit and no other summation order), so handing step s of a
+// chained accumulator the elements 4s .. 4s + 3 of a row gives the sequential fma sum over the row in element order
+// (x[0] * w[0] first): the logits of the C oracle, bit for bit.  The instruction's operands: lane l holds
+// A = x[token l % 16][4s + l / 16] and B = w[expert l % 16][4s + l / 16]; the 16 x 16 output block leaves tokens
+// 4 (l / 16) + 0..3 of expert l % 16 in lane l.
+// A workgroup of NW waves routes 16 TT tokens; wave w owns the expert blocks w NB .. w NB + NB - 1 (16 experts
+// each).  Token rows and weight rows stream through LDS in chunks of 128 elements (double-buffered through
+// registers; a chunk's products cover the next chunk's load latency), stored de-interleaved by element mod 4: k-lane
+// q's 32 elements of a row (4s + q, s = 0..31) sit at bytes 64q .. 64q + 63, so a lane reads its 32 values of a row
+// with four 16-byte reads, and with a row pitch of 272 bytes the 16 rows one read touches fall on distinct banks.
+// Past d the token values are -0 and the weights +0: fma(-0, +0, acc) = acc for every acc (including either zero),
+// so the padded steps change nothing.  The logits then go through LDS to the selection, four tokens per wave
+// (route_select_sig16).
+// ---------------------------------------------------------------------------------------------------------------
+constexpr int kSmChunk = 128, kSmPitch = 272;
+
+template <int NW, int NB, int TT>
+__global__ __launch_bounds__(64 * NW) void route_sigmoid_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                 const uint16_t* __restrict__ wr,
+                                                                 const float* __restrict__ bias, int T, int d,
+                                                                 int E, int k, float scaling,
+                                                                 float* __restrict__ scores,
+                                                                 int32_t* __restrict__ ids, float* __restrict__ wout,
+                                                                 int n_group, int topk_group) {
+#pragma clang fp contract(off)
+  constexpr int NT = 64 * NW;
+  constexpr int TB = 16 * TT;                 // tokens per workgroup
+  constexpr int ER = 16 * NB * NW;            // weight rows staged (rows past E are zero)
+  constexpr int PIECES = (TB + ER) * 16;      // 16-byte pieces per chunk: token rows first, then weight rows
+  constexpr int PPT = (PIECES + NT - 1) / NT;
+  constexpr int STAGE = (TB + ER) * kSmPitch;
+  constexpr int LP = ER + 16;                 // row pitch (floats) of the logits handed to the selection
+  static_assert(TB * LP * 4 <= 2 * STAGE, "the logits reuse the staging buffers");
+  extern __shared__ __attribute__((aligned(16))) char s_m[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int tblk = blockIdx.x * kSgTok;  // the workgroup's first token
-  const int nch = (d + kSgChunk - 1) / kSgChunk;
+  const int tblk = blockIdx.x * TB;
+  const int nch = (d + kSmChunk - 1) / kSmChunk;
   uint4 stage[PPT];
-  uint4 xstage;  // threads 0..127: 8 token values (token tid / 8, elements 8 * (tid % 8) + 0..7 of the chunk)
   auto load_chunk = [&](int c) {
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
-      const int pc = tid + kSgThreads * j, e = pc >> 3, el = c * kSgChunk + (pc & 7) * 8;
-      stage[j] = (e < E && el < d) ? *reinterpret_cast<const uint4*>(wr + (int64_t)e * d + el) : make_uint4(0, 0, 0, 0);
-    }
-    if (tid < kSgTok * 8) {
-      const int t = min(tblk + (tid >> 3), T - 1), el = c * kSgChunk + (tid & 7) * 8;
-      xstage = el < d ? *reinterpret_cast<const uint4*>(x + (int64_t)t * ldx + el) : make_uint4(0, 0, 0, 0);
+      const int pc = tid + NT * j, row = pc >> 4, el = c * kSmChunk + (pc & 15) * 8;
+      if (row < TB) {
+        const int t = tblk + row;
+        stage[j] = (t < T && el < d) ? *reinterpret_cast<const uint4*>(x + (int64_t)t * ldx + el)
+                                     : make_uint4(0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u);
+      } else {
+        const int e = row - TB;
+        stage[j] = (pc < PIECES && e < E && el < d) ? *reinterpret_cast<const uint4*>(wr + (int64_t)e * d + el)
+                                                    : make_uint4(0, 0, 0, 0);
+      }
     }
   };
+  // piece p of a row holds elements 8p .. 8p + 7: k-lane q receives 8p + q and 8p + q + 4, its positions 2p, 2p + 1
   auto store_chunk = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
-      const int pc = tid + kSgThreads * j;
-      *reinterpret_cast<uint4*>(s_w + (buf * ER + (pc >> 3)) * kSgPitch + (pc & 7) * 16) = stage[j];
-    }
-    if (tid < kSgTok * 8) {
-      float* xd = reinterpret_cast<float*>(s_x + buf * kSgXBytes) + (tid >> 3) * kSgChunk + (tid & 7) * 8;
-      *reinterpret_cast<float4*>(xd) = make_float4(bf_lo(xstage.x), bf_hi(xstage.x), bf_lo(xstage.y), bf_hi(xstage.y));
-      *reinterpret_cast<float4*>(xd + 4) =
-          make_float4(bf_lo(xstage.z), bf_hi(xstage.z), bf_lo(xstage.w), bf_hi(xstage.w));
+      const int pc = tid + NT * j;
+      if (PIECES % NT == 0 || pc < PIECES) {
+        const uint4 v = stage[j];
+        uint32_t* dst = reinterpret_cast<uint32_t*>(s_m + buf * STAGE + (pc >> 4) * kSmPitch) + (pc & 15);
+        dst[0] = (v.x & 0xFFFFu) | (v.z << 16);
+        dst[16] = (v.x >> 16) | (v.z & 0xFFFF0000u);
+        dst[32] = (v.y & 0xFFFFu) | (v.w << 16);
+        dst[48] = (v.y >> 16) | (v.w & 0xFFFF0000u);
+      }
     }
   };
-  float acc[kSgTW][EPL];
+  // a lane's 32 values (positions 0..31 of its k-lane) of LDS row `row`: four 16-byte pieces of 8 bf16
+  auto read_row = [&](const char* base, int row, uint4 (&u)[4]) {
+    const uint4* src = reinterpret_cast<const uint4*>(base + row * kSmPitch + (lane >> 4) * 64);
 #pragma unroll
-  for (int q = 0; q < kSgTW; ++q)
+    for (int h = 0; h < 4; ++h) u[h] = src[h];
+  };
+  auto widen = [&](const uint4& u, float (&f)[8]) {
+    f[0] = bf_lo(u.x); f[1] = bf_hi(u.x); f[2] = bf_lo(u.y); f[3] = bf_hi(u.y);
+    f[4] = bf_lo(u.z); f[5] = bf_hi(u.z); f[6] = bf_lo(u.w); f[7] = bf_hi(u.w);
+  };
+  f32x4 acc[TT][NB];
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) acc[q][i] = 0.0f;
+  for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[tt][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float bsv[ER / 16];  // the selection bias of this lane's experts (i * 16 + lane % 16)
+#pragma unroll
+  for (int i = 0; i < ER / 16; ++i) {
+    const int e = i * 16 + (lane & 15);
+    bsv[i] = bias && e < E ? bias[e] : 0.0f;
+  }
+  const bool live = wave * NB * 16 < E;  // a wave whose experts all lie past E skips the products
+  const int r = lane & 15;
   load_chunk(0);
   store_chunk(0);
   __syncthreads();
   for (int c = 0; c < nch; ++c) {
     if (c + 1 < nch) load_chunk(c + 1);
-    const char* wbuf = s_w + (c & 1) * ER * kSgPitch;
-    const float* xbuf = reinterpret_cast<const float*>(s_x + (c & 1) * kSgXBytes) + wave * kSgTW * kSgChunk;
-    const int npc = min(8, (d - c * kSgChunk) / 8);  // 8-element pieces of this chunk (the last may be short)
-#pragma unroll 2
-    for (int pcs = 0; pcs < npc; ++pcs) {
-      float xv[kSgTW][8];
+    const char* base = s_m + (c & 1) * STAGE;
+    if (live) {
+      // every read of the chunk is issued before the first product (the LDS latency is paid once per chunk)
+      uint4 ua[TT][4], ub[NB][4];
 #pragma unroll
-      for (int q = 0; q < kSgTW; ++q) {
-        const float4 a = *reinterpret_cast<const float4*>(xbuf + q * kSgChunk + pcs * 8);
-        const float4 b = *reinterpret_cast<const float4*>(xbuf + q * kSgChunk + pcs * 8 + 4);
-        xv[q][0] = a.x; xv[q][1] = a.y; xv[q][2] = a.z; xv[q][3] = a.w;
-        xv[q][4] = b.x; xv[q][5] = b.y; xv[q][6] = b.z; xv[q][7] = b.w;
-      }
+      for (int tt = 0; tt < TT; ++tt) read_row(base, tt * 16 + r, ua[tt]);
 #pragma unroll
-      for (int i = 0; i < EPL; ++i) {
-        const uint4 wv = *reinterpret_cast<const uint4*>(wbuf + (i * 64 + lane) * kSgPitch + pcs * 16);
-        const uint32_t w4[4] = {wv.x, wv.y, wv.z, wv.w};
-        float wf[8];
+      for (int nb = 0; nb < NB; ++nb) read_row(base, TB + (wave * NB + nb) * 16 + r, ub[nb]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          wf[2 * j] = bf_lo(w4[j]);
-          wf[2 * j + 1] = bf_hi(w4[j]);
-        }
+      for (int h = 0; h < 4; ++h) {
+        float a[TT][8], b[NB][8];
 #pragma unroll
-        for (int q = 0; q < kSgTW; ++q)
+        for (int tt = 0; tt < TT; ++tt) widen(ua[tt][h], a[tt]);
 #pragma unroll
-          for (int j = 0; j < 8; ++j) acc[q][i] = __builtin_fmaf(xv[q][j], wf[j], acc[q][i]);
+        for (int nb = 0; nb < NB; ++nb) widen(ub[nb][h], b[nb]);
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+#pragma unroll
+          for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+              acc[tt][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[tt][s], b[nb][s], acc[tt][nb], 0, 0, 0);
       }
     }
-    if (c + 1 < nch) store_chunk((c + 1) & 1);  // the other buffers: last read before the previous barrier
+    if (c + 1 < nch) store_chunk((c + 1) & 1);  // the other buffer: last read before the previous barrier
     __syncthreads();
   }
-  const int t0 = tblk + wave * kSgTW;
+  // logits (token, expert) into LDS: lane l holds tokens 16 tt + 4 (l / 16) + i of expert 16 (w NB + nb) + l % 16
+  float* lgs = reinterpret_cast<float*>(s_m);
 #pragma unroll
-  for (int q = 0; q < kSgTW; ++q) {
-    const int t = t0 + q;
-    if (t < T) {
-      float lg[kRouteEPL];
+  for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
-      for (int i = 0; i < kRouteEPL; ++i) lg[i] = i < EPL ? acc[q][i] : -__builtin_inff();
-      route_select<true>(lg, t, lane, E, k, 1, scaling, bias, scores, ids, wout, n_group, topk_group);
-    }
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        lgs[(tt * 16 + 4 * (lane >> 4) + i) * LP + (wave * NB + nb) * 16 + r] = acc[tt][nb][i];
+  __syncthreads();
+  // selection: token tok of the workgroup on segment tok % 4 of wave tok / 4 (four tokens per wave)
+  constexpr int EPS = ER / 16;
+  for (int tok0 = wave * 4; tok0 < TB; tok0 += NW * 4) {
+    const int tok = tok0 + (lane >> 4);
+    const int64_t t = (int64_t)tblk + tok;
+    const bool on = tok < TB && t < T;
+    float lg[EPS];
+#pragma unroll
+    for (int i = 0; i < EPS; ++i) lg[i] = lgs[min(tok, TB - 1) * LP + i * 16 + r];
+    route_select_sig16<EPS>(lg, bsv, bias != nullptr, t, on, lane, E, k, scaling, scores, ids, wout, n_group,
+                            topk_group);
   }
 }
 
@@ -1638,6 +1826,28 @@ static void* dispatch_scratch(int* rc) {
   return p;
 }
 
+// the dynamic LDS of the larger router instantiations (up to 157 KB) is declared once per device before the launch
+template <int NW, int NB, int TT>
+static int sigmoid_launch(int grid, size_t lds, hipStream_t s, const uint16_t* x, int64_t ldx, const uint16_t* wr,
+                          const float* bias, int T, int d, int E, int k, float scaling, float* scores, int32_t* ids,
+                          float* w, int n_group, int topk_group) {
+  auto kern = route_sigmoid_kernel<NW, NB, TT>;
+  static std::atomic<bool> attr_set[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return HMOE_ERR_DEVICE;
+  if (!attr_set[dev].load(std::memory_order_acquire)) {
+    constexpr int kMax = 2 * (16 * TT + 16 * NB * NW) * kSmPitch;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, kMax) !=
+        hipSuccess)
+      return HMOE_ERR_LAUNCH;
+    attr_set[dev].store(true, std::memory_order_release);
+  }
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * NW), lds, s, x, ldx, wr, bias, T, d, E, k, scaling, scores, ids, w,
+                     n_group, topk_group);
+  HMOE_CHECK_LAUNCH();
+  return HMOE_OK;
+}
+
 }  // namespace hmoe
 
 using namespace hmoe;
@@ -1682,25 +1892,23 @@ int hmoe_route_sigmoid_group(const void* x, int64_t ldx, const void* wr, const f
     if (k > topk_group * eg) return HMOE_ERR_SHAPE;  // the kept groups must hold k experts
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int epl = (E + 63) / 64;
-  const size_t lds = (size_t)2 * epl * 64 * kSgPitch + 2 * kSgXBytes;
-  const int grid = (int)((T + kSgTok - 1) / kSgTok);
+  // waves x 16-expert blocks per wave cover E; two 16-token tiles per workgroup once that still gives a workgroup
+  // per CU (8192 tokens), else one
+  const int nw = E <= 64 ? 4 : 8, nb = E <= 128 ? 1 : 2, tt = T >= 8192 ? 2 : 1;
+  const size_t lds = (size_t)2 * (16 * tt + 16 * nb * nw) * kSmPitch;
+  const int grid = (int)((T + 16 * tt - 1) / (16 * tt));
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* wp = static_cast<const uint16_t*>(wr);
-#define HMOE_SG(EP)                                                                                             \
-  hipLaunchKernelGGL(route_sigmoid_kernel<EP>, dim3(grid), dim3(kSgThreads), lds, s, xp, ldx, wp, expert_bias, (int)T, \
-                     (int)d, E, k, scaling, scores, topk_ids, topk_w, n_group, topk_group)
-  if (epl == 1)
-    HMOE_SG(1);
-  else if (epl == 2)
-    HMOE_SG(2);
-  else if (epl == 3)
-    HMOE_SG(3);
-  else
-    HMOE_SG(4);
+#define HMOE_SG(NW, NB, TT)                                                                                      \
+  return sigmoid_launch<NW, NB, TT>(grid, lds, s, xp, ldx, wp, expert_bias, (int)T, (int)d, E, k, scaling, scores, \
+                                    topk_ids, topk_w, n_group, topk_group)
+  if (nw == 4 && tt == 2) HMOE_SG(4, 1, 2);
+  if (nw == 4) HMOE_SG(4, 1, 1);
+  if (nb == 1 && tt == 2) HMOE_SG(8, 1, 2);
+  if (nb == 1) HMOE_SG(8, 1, 1);
+  if (tt == 2) HMOE_SG(8, 2, 2);
+  HMOE_SG(8, 2, 1);
 #undef HMOE_SG
-  HMOE_CHECK_LAUNCH();
-  return HMOE_OK;
 }
 
 size_t hmoe_dispatch_workspace_size(int64_t T, int k, int E) { return dispatch_ws_bytes(T, k, E); }
