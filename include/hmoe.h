@@ -62,9 +62,8 @@ const char* hmoe_error_string(int code);
  * F.linear(x.float(), W.float()), top-k, w / (sum + 1e-20) * scaling).
  * x (T, d) bf16 with row stride ldx, wr (E, d) bf16, bias (E,) fp32 or NULL.  Outputs topk_ids (T, k) int32 and
  * topk_w (T, k) fp32 (slots in descending order, ties to the lower expert), logits (T, E) fp32 (NULL to skip).
- * The dot products use a fixed, documented reduction order (64 lane partials over 8-element groups, xor
- * butterfly), so ids, weights and logits are bit-reproducible by a host restatement.  d % 8 == 0, E <= 256,
- * k <= 16. */
+ * Each logit is the sequential fma sum over the row in element order (x[0] * w[0] first, from +0), plus the bias,
+ * so ids, weights and logits are bit-reproducible by a host restatement.  d % 8 == 0, E <= 256, k <= 16. */
 int hmoe_route_topk(const void* x, int64_t ldx, const void* wr, const float* bias, int64_t T, int64_t d, int E,
                     int k, int renorm, float scaling, float* logits, int32_t* topk_ids, float* topk_w,
                     hmoe_stream_t stream);

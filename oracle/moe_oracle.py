@@ -9,8 +9,9 @@ half of the oracle (oracle/router.c), loaded here through ctypes.
 
 Pinning (what each function is checked against, in tests/test_oracle.py):
   route / topk_from_logits   C restatement; ids vs torch.softmax + torch.topk on the same logits, logits vs
-                             float64 matmul, hexp vs math.exp (ulp bound), brute force on tiny inputs, ties, -inf bias
-  router_logits_seq          sequential fma sums; vs float64 matmul within the fp32 accumulation bound
+                             float64 matmul within the fp32 accumulation bound, hexp vs math.exp (ulp bound), brute
+                             force on tiny inputs, ties, -inf bias; the blocked fma order by a hand-derived case whose
+                             result the sequential element order would not give
   sigmoid_group_from_logits  C restatement; ids / weights vs the reference's torch steps (sigmoid, group top-2 sums,
                              group topk, masked topk, renormalise) run on CPU torch from the same scores; brute force
                              over all group subsets on tiny inputs; sigmoid vs float64 within 3 ulp; tie rules
@@ -109,7 +110,6 @@ def lib():
         L.orc_topk_from_logits.argtypes = [P, I64, I32, I32, I32, F32, P, P, P]
         L.orc_route.argtypes = [P, I64, P, P, I64, I64, I32, I32, I32, F32, P, P, P]
         L.orc_sigmoid_group_from_logits.argtypes = [P, I64, I32, I32, I32, I32, P, F32, P, P, P]
-        L.orc_router_logits_seq.argtypes = [P, I64, P, I64, I64, I32, P]
         L.orc_dispatch.argtypes = [P, I64, I32, I32, P, P, P, P]
         L.orc_dispatch.restype = I32
         L.orc_make_schedule.argtypes = [P, I32, I64, I32, P, P, P]
@@ -128,8 +128,9 @@ def hexp(x) -> np.ndarray:
 
 
 def router_logits(x_bits: np.ndarray, wr_bits: np.ndarray, bias=None) -> np.ndarray:
-    """fp32 router logits in the fixed reduction order of router.c.  x_bits (T, d), wr_bits (E, d): bf16 bit patterns
-    (uint16).  Convention source: aurora/hf_pipeline.py:352 (F.linear(x.float(), W.float()))."""
+    """fp32 router logits: per (token, expert) the fma chain over the row in router.c's blocked order, plus the bias
+    (router.c orc_router_logits).  x_bits (T, d), wr_bits (E, d): bf16 bit patterns (uint16).  Convention source:
+    aurora/hf_pipeline.py:352 (F.linear(x.float(), W.float()))."""
     x_bits = np.ascontiguousarray(x_bits, dtype=np.uint16)
     wr_bits = np.ascontiguousarray(wr_bits, dtype=np.uint16)
     T, d = x_bits.shape
@@ -166,20 +167,8 @@ def sigmoid_group_from_logits(logits, k, n_group, topk_group, bias=None, scaling
     return ids, w, sc
 
 
-def router_logits_seq(x_bits: np.ndarray, wr_bits: np.ndarray) -> np.ndarray:
-    """fp32 logits of the sigmoid router: per (token, expert) the sequential fma sum over the row in element order
-    (router.c orc_router_logits_seq).  Convention source: aurora/hf_pipeline.py:352."""
-    x_bits = np.ascontiguousarray(x_bits, dtype=np.uint16)
-    wr_bits = np.ascontiguousarray(wr_bits, dtype=np.uint16)
-    T, d = x_bits.shape
-    E = wr_bits.shape[0]
-    out = np.empty((T, E), dtype=np.float32)
-    lib().orc_router_logits_seq(_ptr(x_bits), d, _ptr(wr_bits), T, d, E, _ptr(out))
-    return out
-
-
 def route_sigmoid_group(x_bits, wr_bits, k, n_group, topk_group, bias=None, scaling=1.0):
-    logits = router_logits_seq(x_bits, wr_bits)
+    logits = router_logits(x_bits, wr_bits)
     ids, w, sc = sigmoid_group_from_logits(logits, k, n_group, topk_group, bias, scaling)
     return logits, ids, w, sc
 

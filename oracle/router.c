@@ -9,17 +9,19 @@
  *     F.linear(x.float(), W.float()) at :352, top-k at :359 via topk, renormalisation w / (sum + 1e-20) * scaling
  *     at :359).  This file fixes what the reference leaves open, and the HIP kernel replicates it operation by
  *     operation so that ids, weights and logits are bit-exact:
- *       * dot product order: 64 lane partials, lane l owns elements c*512 + 8l + i (c = 0.., i = 0..7) and adds
- *         them in (c, i) order starting from +0.0f; the 64 partials are then combined by the xor butterfly
- *         (offsets 32, 16, 8, 4, 2, 1); logit = dot (+ bias[e] when a bias is given);
+ *       * dot product order (both routers): a chain of fmas from +0.0f, acc = fmaf(x[i], w[e][i], acc), over the
+ *         row in 64-element blocks; inside block b, step s (0..15) takes the elements 64b + 16q + s for q = 0..3 in
+ *         that order (what chained v_mfma_f32_16x16x4_f32 steps compute when k-lane q holds the 16 consecutive
+ *         elements 64b + 16q .. 64b + 16q + 15); elements past d are skipped; logit = dot (+ bias[e] when a bias
+ *         is given, one rounded addition);
  *       * softmax: m = max logit; ex_e = hexp(logit_e - m); denominator S uses the same lane/butterfly structure
  *         (lane l sums experts l, l+64, ...); p_e = ex_e / S (IEEE division);
  *       * selection on the logits, descending, ties to the lower expert index (softmax is monotone, so this is
  *         torch.topk's order wherever two probabilities are not rounded to the same float);
  *       * weights: w_j = p_{e_j}; renorm: s = w_0 + w_1 + ... (in j order), w_j = w_j / (s + 1e-20f) * scaling;
  *         otherwise w_j = w_j * scaling.
- *   - the sigmoid, group-limited router of BailingMoeV2 (aurora/hf_pipeline.py:352-359): its logits are the
- *     sequential fma sums of orc_router_logits_seq (element order); orc_sigmoid_group_from_logits below states the
+ *   - the sigmoid, group-limited router of BailingMoeV2 (aurora/hf_pipeline.py:352-359): its logits are those of
+ *     orc_router_logits without a bias (the same order); orc_sigmoid_group_from_logits below states the
  *     orders of the selection;
  *   - hexp: exp by Cody-Waite range reduction (Cephes split ln2 = 0.693359375 - 2.12194440e-4), a degree-7 Taylor
  *     polynomial in Horner form with fmaf, and exponent scaling by ldexpf; arguments below -87 give 0, above 88
@@ -70,6 +72,7 @@ float orc_hexp(float x) {
     return ldexpf(p, (int)n);
 }
 
+/* xor butterfly over 64 lane values (offsets 32, 16, ..., 1): the softmax denominator's reduction */
 static float butterfly64(float* v) {
     for (int s = 32; s >= 1; s >>= 1) {
         float nv[64];
@@ -79,41 +82,22 @@ static float butterfly64(float* v) {
     return v[0];
 }
 
-/* logits (T, E) fp32 in the fixed order described above; x rows have stride ldx (elements). */
+/* logits (T, E) fp32 in the order described above; x rows have stride ldx (elements). */
 void orc_router_logits(const uint16_t* x, int64_t ldx, const uint16_t* wr, const float* bias, int64_t T, int64_t d,
                        int E, float* logits) {
-    int64_t nc = (d + 511) / 512;
-    for (int64_t t = 0; t < T; ++t) {
-        const uint16_t* xr = x + t * ldx;
-        for (int e = 0; e < E; ++e) {
-            const uint16_t* wrow = wr + (int64_t)e * d;
-            float v[64];
-            for (int l = 0; l < 64; ++l) {
-                float acc = 0.0f;
-                for (int64_t c = 0; c < nc; ++c)
-                    for (int i = 0; i < 8; ++i) {
-                        int64_t idx = c * 512 + l * 8 + i;
-                        if (idx < d) acc = acc + bf16_to_f32(xr[idx]) * bf16_to_f32(wrow[idx]);
-                    }
-                v[l] = acc;
-            }
-            float dot = butterfly64(v);
-            logits[t * E + e] = bias ? dot + bias[e] : dot;
-        }
-    }
-}
-
-/* logits (T, E) of the sigmoid router: for each (token, expert) the sequential fma sum over the row in element
- * order, acc = fmaf(x[i], w[e][i], acc) from +0.0f (the order of route_sigmoid_kernel). */
-void orc_router_logits_seq(const uint16_t* x, int64_t ldx, const uint16_t* wr, int64_t T, int64_t d, int E,
-                           float* logits) {
+    const int64_t nb = (d + 63) / 64;
     for (int64_t t = 0; t < T; ++t) {
         const uint16_t* xr = x + t * ldx;
         for (int e = 0; e < E; ++e) {
             const uint16_t* wrow = wr + (int64_t)e * d;
             float acc = 0.0f;
-            for (int64_t i = 0; i < d; ++i) acc = fmaf(bf16_to_f32(xr[i]), bf16_to_f32(wrow[i]), acc);
-            logits[t * E + e] = acc;
+            for (int64_t b = 0; b < nb; ++b)
+                for (int s = 0; s < 16; ++s)
+                    for (int q = 0; q < 4; ++q) {
+                        const int64_t i = 64 * b + 16 * q + s;
+                        if (i < d) acc = fmaf(bf16_to_f32(xr[i]), bf16_to_f32(wrow[i]), acc);
+                    }
+            logits[t * E + e] = bias ? acc + bias[e] : acc;
         }
     }
 }

@@ -583,20 +583,38 @@ def test_poziomka_cpu_path_vs_oracle(oracle):
     assert_close_bf16(out.float().numpy(), ref, "poziomka cpu path")
 
 
-def test_router_logits_seq_vs_float64(oracle):
-    """The sigmoid router's sequential fma logits against float64: within the fp32 accumulation bound d * 2^-24 *
-    sum|x w| (a transposed operand or a dropped term would be far outside it)."""
+def test_router_logits_ragged_vs_float64(oracle):
+    """Both routers' logits (no bias) against float64 on a row length off the 64-element block: within the fp32
+    accumulation bound d * 2^-24 * sum|x w| (a transposed operand or a dropped term would be far outside it)."""
     rng = np.random.default_rng(21)
     T, d, E = 40, 520, 24
     x = oracle.round_bf16(rng.standard_normal((T, d)))
     w = oracle.round_bf16(rng.standard_normal((E, d)) * 0.05)
-    lg = oracle.router_logits_seq(oracle.f32_to_bf16_bits(x), oracle.f32_to_bf16_bits(w))
+    lg = oracle.router_logits(oracle.f32_to_bf16_bits(x), oracle.f32_to_bf16_bits(w))
     ref = x.astype(np.float64) @ w.astype(np.float64).T
     bound = d * 2.0 ** -24 * (np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64).T)
     assert (np.abs(lg - ref) <= bound).all()
-    # a single term by hand: the first element's product leads the sum
+    # a single term by hand
     x1 = np.zeros((1, 8), np.float32)
     x1[0, 0] = 3.0
     w1 = np.zeros((1, 8), np.float32)
     w1[0, 0] = 0.5
-    assert oracle.router_logits_seq(oracle.f32_to_bf16_bits(x1), oracle.f32_to_bf16_bits(w1))[0, 0] == 1.5
+    assert oracle.router_logits(oracle.f32_to_bf16_bits(x1), oracle.f32_to_bf16_bits(w1))[0, 0] == 1.5
+
+
+def test_router_logits_blocked_order(oracle):
+    """The fma chain's order, by a case whose answer depends on it: products 2^24 (element 0), 1 (element 16) and
+    -2^24 (element 1).  In the blocked order (step 0 takes elements 0, 16, 32, 48, step 1 elements 1, 17, ...) the 1
+    is added to 2^24 and lost to rounding (2^24 + 1 is a tie, to even), then -2^24 cancels: 0.  The sequential
+    element order would cancel first and keep the 1; a reversed or pairwise order gives 1 as well."""
+    x = np.zeros((1, 64), np.float32)
+    w = np.zeros((1, 64), np.float32)
+    x[0, 0], w[0, 0] = 4096.0, 4096.0
+    x[0, 16], w[0, 16] = 1.0, 1.0
+    x[0, 1], w[0, 1] = -4096.0, 4096.0
+    lg = oracle.router_logits(oracle.f32_to_bf16_bits(x), oracle.f32_to_bf16_bits(w))
+    assert lg[0, 0] == 0.0
+    # with element 16 moved to 2 (processed after the cancellation in either order) the 1 survives
+    x[0, 16], w[0, 16] = 0.0, 0.0
+    x[0, 2], w[0, 2] = 1.0, 1.0
+    assert oracle.router_logits(oracle.f32_to_bf16_bits(x), oracle.f32_to_bf16_bits(w))[0, 0] == 1.0
