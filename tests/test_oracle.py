@@ -477,7 +477,7 @@ def test_golden_fixtures_reproduce(oracle):
 
 
 def test_bf16_products_exact_in_fp32():
-    # The router's lane partials use fused multiply-adds; that equals the multiply-then-add order because the product
+    # The routers' logits are fused multiply-add chains; each step equals a multiply then an add because the product
     # of two bf16 values (8 significant bits each) is exact in fp32.  Check it over the whole normal range.
     rng = np.random.default_rng(7)
     a = rng.integers(0, 1 << 16, 200000, dtype=np.uint32).astype(np.uint16)
