@@ -552,7 +552,7 @@ __global__ __launch_bounds__(256) void route_topk_direct_kernel(const uint16_t* 
                                                                 float* __restrict__ wout) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63, r = lane & 15, q = lane >> 4;
-  const int t0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 16;
+  const int t0 = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * 16;
   if (t0 >= T) return;  // a whole wave; the kernel has no barrier
   const int nbf = d / 64;  // whole blocks; a last partial block (d % 64 != 0) is handled after them
   const uint16_t* xr = x + (int64_t)min(t0 + r, T - 1) * ldx + 16 * q;
@@ -1556,9 +1556,12 @@ static int route_launch(const void* x, int64_t ldx, const void* wr, const float*
                         hipStream_t s) {
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* wp = static_cast<const uint16_t*>(wr);
-  if (E <= 16) {  // every wave its own 16 tokens and all experts, four waves per workgroup
-    hipLaunchKernelGGL(route_topk_direct_kernel, dim3((unsigned)((T + 63) / 64)), dim3(256), 0, s, xp, ldx, wp, bias,
-                       (int)T, (int)d, E, k, renorm, scaling, logits, topk_ids, topk_w);
+  if (E <= 16) {
+    // every wave its own 16 tokens and all experts; below 8192 tokens one wave per workgroup, so that the waves
+    // spread over more CUs (2048 tokens at d = 1536: 19.6 -> 16.7 us)
+    const int wpb = T >= 8192 ? 4 : 1;
+    hipLaunchKernelGGL(route_topk_direct_kernel, dim3((unsigned)((T + 16 * wpb - 1) / (16 * wpb))), dim3(64 * wpb), 0,
+                       s, xp, ldx, wp, bias, (int)T, (int)d, E, k, renorm, scaling, logits, topk_ids, topk_w);
     HMOE_CHECK_LAUNCH();
     return HMOE_OK;
   }
