@@ -50,3 +50,19 @@ def test_route_ties(oracle):
     wr = torch.zeros_like(wr)
     rids = _check(oracle, x, wr, 3)
     assert (rids == np.array([0, 1, 2])).all()
+
+
+@pytest.mark.parametrize("T,d,E,k", [(200, 1536, 16, 2), (100, 520, 40, 4)])
+def test_route_denormal_products(oracle, T, d, E, k):
+    """Products in the fp32 denormal range (x ~ 2^-70, w ~ 2^-62): the matrix-core fma chains keep denormals as the
+    oracle's fmaf does, so the tiny logits and the ids they select stay bit-exact.  E = 16 runs the register-fed
+    kernel, E = 40 the LDS-staged one that the sigmoid router shares (whose scores would not show the logits'
+    denormals: sigmoid of a denormal is 0.5)."""
+    print(f"route denormal T={T} d={d} E={E} k={k}", flush=True)
+    x, wr, _, _ = make_inputs(T, d, E, 8, seed=T + E)
+    x = (x.float() * 2.0 ** -70).bfloat16()
+    wr = (wr.float() * 2.0 ** -56).bfloat16()
+    _check(oracle, x, wr, k)
+    rl, _, _ = oracle.route(bits(x), bits(wr), k)
+    tiny = np.abs(rl) < np.finfo(np.float32).tiny
+    assert tiny.mean() > 0.5, tiny.mean()  # most logits are denormal
