@@ -189,3 +189,29 @@ def test_generic_activation_path_equals_fused_silu():
     print(f"identical outputs: {same:.6f}", flush=True)
     assert same > 0.99, same
     assert_close_bf16(f32(outs[1]), f32(outs[0]), "generic vs fused silu")
+
+
+@pytest.mark.parametrize("act", [nn.functional.silu, nn.GELU()])
+@pytest.mark.parametrize("T", [0, 1, 3])
+def test_fuse_moe_tiny_batches(oracle, act, T):
+    """Empty and few-token calls through both moe_infer paths (the fused SwiGLU and the module's own activation),
+    with widths off the granule: the right shape, and the values of the reference order for the tokens present."""
+    from trenowanie_generatora_obrazkow_amd.hf_compat import fuse_moe
+    print(f"fuse_moe tiny T={T} act={act}", flush=True)
+    d, h, E, k = 36, 20, 4, 2
+    torch.manual_seed(T)
+    model = nn.Sequential(_MoEBlock(d, h, E, act)).bfloat16()
+    wgu, wd = _stacks(model[0])
+    assert fuse_moe(model) == 1
+    blk = model.cuda()[0]
+    g = torch.Generator().manual_seed(31 + T)
+    x = torch.randn(T, d, generator=g).bfloat16()
+    ids = torch.zeros(0, k, dtype=torch.long)
+    if T:
+        ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)])
+    w = torch.rand(T, k, generator=g).softmax(-1)
+    y = blk.moe_infer(x.to(DEV), ids.to(DEV), w.to(DEV))
+    assert y.shape == (T, d) and y.dtype == torch.bfloat16
+    if T:
+        ref = _reference_act_layer(oracle, x, ids, w, wgu, wd, act)
+        assert_close_bf16(f32(y), ref, f"tiny moe_infer T={T}")
