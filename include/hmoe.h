@@ -62,15 +62,16 @@ const char* hmoe_error_string(int code);
  * F.linear(x.float(), W.float()), top-k, w / (sum + 1e-20) * scaling).
  * x (T, d) bf16 with row stride ldx, wr (E, d) bf16, bias (E,) fp32 or NULL.  Outputs topk_ids (T, k) int32 and
  * topk_w (T, k) fp32 (slots in descending order, ties to the lower expert), logits (T, E) fp32 (NULL to skip).
- * Each logit is the sequential fma sum over the row in element order (x[0] * w[0] first, from +0), plus the bias,
- * so ids, weights and logits are bit-reproducible by a host restatement.  d % 8 == 0, E <= 256, k <= 16. */
+ * Each logit is a fixed-order fp32 sum, so ids, weights and logits are bit-reproducible by a host restatement: the
+ * row in 64-element blocks, block b feeding fma chain b % 4 (each from +0, its blocks in order, step s of block b
+ * taking elements 64b + 16q + s for q = 0..3), logit = (c0 + c1) + (c2 + c3), plus the bias (one rounded addition).
+ * d % 8 == 0, E <= 256, k <= 16. */
 int hmoe_route_topk(const void* x, int64_t ldx, const void* wr, const float* bias, int64_t T, int64_t d, int E,
                     int k, int renorm, float scaling, float* logits, int32_t* topk_ids, float* topk_w,
                     hmoe_stream_t stream);
 
 /* Sigmoid, group-limited top-k router of BailingMoeV2: replaces the routing of aurora/hf_pipeline.py:352-359
- * (PoziomkaMoE.forward).  Logits in fp32, each the sequential fma sum over the row in element order
- * (x[0] * w[0] first; no bias in them); score = 1 / (1 + exp(-logit)) (the exp of the softmax router, IEEE
+ * (PoziomkaMoE.forward).  Logits in fp32, each the fixed-order sum of hmoe_route_topk (no bias in them); score = 1 / (1 + exp(-logit)) (the exp of the softmax router, IEEE
  * division); routing = score + expert_bias (fp32, NULL = 0) for
  * selection only; the experts form n_group groups of E / n_group, a group's value is the sum of its two largest
  * routing values, the topk_group best groups are kept (ties to the lower group) and the k best experts among them

@@ -10,8 +10,9 @@ half of the oracle (oracle/router.c), loaded here through ctypes.
 Pinning (what each function is checked against, in tests/test_oracle.py):
   route / topk_from_logits   C restatement; ids vs torch.softmax + torch.topk on the same logits, logits vs
                              float64 matmul within the fp32 accumulation bound, hexp vs math.exp (ulp bound), brute
-                             force on tiny inputs, ties, -inf bias; the blocked fma order by a hand-derived case whose
-                             result the sequential element order would not give
+                             force on tiny inputs, ties, -inf bias; the blocked fma order and the four partial chains
+                             by hand-derived cases whose results a sequential element order, or one chain over the
+                             blocks, would not give
   sigmoid_group_from_logits  C restatement; ids / weights vs the reference's torch steps (sigmoid, group top-2 sums,
                              group topk, masked topk, renormalise) run on CPU torch from the same scores; brute force
                              over all group subsets on tiny inputs; sigmoid vs float64 within 3 ulp; tie rules
@@ -128,7 +129,8 @@ def hexp(x) -> np.ndarray:
 
 
 def router_logits(x_bits: np.ndarray, wr_bits: np.ndarray, bias=None) -> np.ndarray:
-    """fp32 router logits: per (token, expert) the fma chain over the row in router.c's blocked order, plus the bias
+    """fp32 router logits: per (token, expert) four fma chains over the row in router.c's blocked order (64-element
+    block b feeding chain b % 4), summed as (c0 + c1) + (c2 + c3), plus the bias
     (router.c orc_router_logits).  x_bits (T, d), wr_bits (E, d): bf16 bit patterns (uint16).  Convention source:
     aurora/hf_pipeline.py:352 (F.linear(x.float(), W.float()))."""
     x_bits = np.ascontiguousarray(x_bits, dtype=np.uint16)

@@ -9,11 +9,12 @@
  *     F.linear(x.float(), W.float()) at :352, top-k at :359 via topk, renormalisation w / (sum + 1e-20) * scaling
  *     at :359).  This file fixes what the reference leaves open, and the HIP kernel replicates it operation by
  *     operation so that ids, weights and logits are bit-exact:
- *       * dot product order (both routers): a chain of fmas from +0.0f, acc = fmaf(x[i], w[e][i], acc), over the
- *         row in 64-element blocks; inside block b, step s (0..15) takes the elements 64b + 16q + s for q = 0..3 in
- *         that order (what chained v_mfma_f32_16x16x4_f32 steps compute when k-lane q holds the 16 consecutive
- *         elements 64b + 16q .. 64b + 16q + 15); elements past d are skipped; logit = dot (+ bias[e] when a bias
- *         is given, one rounded addition);
+ *       * dot product order (both routers): the row in 64-element blocks, block b feeding partial chain b % 4;
+ *         each chain is a sequence of fmas from +0.0f, acc_c = fmaf(x[i], w[e][i], acc_c), its blocks in increasing
+ *         order, inside block b step s (0..15) taking the elements 64b + 16q + s for q = 0..3 in that order (what
+ *         chained v_mfma_f32_16x16x4_f32 steps compute when k-lane q holds the 16 consecutive elements
+ *         64b + 16q .. 64b + 16q + 15); elements past d are skipped; dot = (acc_0 + acc_1) + (acc_2 + acc_3);
+ *         logit = dot (+ bias[e] when a bias is given, one rounded addition);
  *       * softmax: m = max logit; ex_e = hexp(logit_e - m); denominator S uses the same lane/butterfly structure
  *         (lane l sums experts l, l+64, ...); p_e = ex_e / S (IEEE division);
  *       * selection on the logits, descending, ties to the lower expert index (softmax is monotone, so this is
@@ -90,14 +91,15 @@ void orc_router_logits(const uint16_t* x, int64_t ldx, const uint16_t* wr, const
         const uint16_t* xr = x + t * ldx;
         for (int e = 0; e < E; ++e) {
             const uint16_t* wrow = wr + (int64_t)e * d;
-            float acc = 0.0f;
+            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
             for (int64_t b = 0; b < nb; ++b)
                 for (int s = 0; s < 16; ++s)
                     for (int q = 0; q < 4; ++q) {
                         const int64_t i = 64 * b + 16 * q + s;
-                        if (i < d) acc = fmaf(bf16_to_f32(xr[i]), bf16_to_f32(wrow[i]), acc);
+                        if (i < d) acc[b % 4] = fmaf(bf16_to_f32(xr[i]), bf16_to_f32(wrow[i]), acc[b % 4]);
                     }
-            logits[t * E + e] = bias ? acc + bias[e] : acc;
+            const float dot = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+            logits[t * E + e] = bias ? dot + bias[e] : dot;
         }
     }
 }

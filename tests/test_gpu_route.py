@@ -30,6 +30,19 @@ def test_route_bitexact(oracle, T, d, E, k):
     _check(oracle, x, wr, k)
 
 
+@pytest.mark.parametrize("T,d,E,k", [(40, 8, 16, 2), (40, 136, 9, 2), (33, 200, 16, 3), (50, 328, 4, 2),
+                                     (12300, 200, 7, 2), (12288, 8, 16, 4), (12352, 1032, 16, 2),
+                                     (70, 200, 24, 3), (40, 8, 48, 2)])
+def test_route_chain_edges(oracle, T, d, E, k):
+    """The four partial chains where rows end early: d = 8 (no whole block: only chain 0, from the partial block),
+    136 (chains 2 and 3 of the whole blocks empty, the partial block on chain 2), 200 (partial block on chain 3),
+    328 (chain 1 holds blocks 1 and 5); T below and above the token count where the E <= 16 router switches from
+    four waves per tile to one (12288), E above 16 for the LDS-staged kernel."""
+    print(f"route chains T={T} d={d} E={E} k={k}", flush=True)
+    x, wr, _, _ = make_inputs(T, d, E, 8, seed=T + d + E)
+    _check(oracle, x, wr, k, bias=np.linspace(-0.5, 0.5, E).astype(np.float32))
+
+
 def test_route_no_renorm_and_scaling(oracle):
     x, wr, _, _ = make_inputs(1000, 1024, 16, 8, seed=3)
     _check(oracle, x, wr, 4, renorm=False, scaling=2.5)

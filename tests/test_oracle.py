@@ -618,3 +618,21 @@ def test_router_logits_blocked_order(oracle):
     x[0, 16], w[0, 16] = 0.0, 0.0
     x[0, 2], w[0, 2] = 1.0, 1.0
     assert oracle.router_logits(oracle.f32_to_bf16_bits(x), oracle.f32_to_bf16_bits(w))[0, 0] == 1.0
+
+
+def test_router_logits_partial_chains(oracle):
+    """The four partial chains (64-element block b feeds chain b % 4) and their combine (c0 + c1) + (c2 + c3), by
+    hand: products 2^24 in block 0 (chain 0), 1 in block 2 (chain 2) and 1 in block 3 (chain 3) give 2^24 + 2 (the
+    two 1s meet first); one chain over the blocks in order would add each 1 to 2^24 and lose both to rounding
+    (2^24 + 1 is a tie, to even).  Block 4 folds back onto chain 0: 2^24, then 1 in block 4 is lost there too."""
+    d = 320
+    x = np.zeros((1, d), np.float32)
+    w = np.zeros((1, d), np.float32)
+    x[0, 0], w[0, 0] = 4096.0, 4096.0
+    x[0, 128], w[0, 128] = 1.0, 1.0
+    x[0, 192], w[0, 192] = 1.0, 1.0
+    lg = oracle.router_logits(oracle.f32_to_bf16_bits(x), oracle.f32_to_bf16_bits(w))
+    assert lg[0, 0] == 2.0 ** 24 + 2
+    x[0, 256], w[0, 256] = 1.0, 1.0  # block 4: chain 0, after its 2^24
+    lg = oracle.router_logits(oracle.f32_to_bf16_bits(x), oracle.f32_to_bf16_bits(w))
+    assert lg[0, 0] == 2.0 ** 24 + 2

@@ -379,10 +379,11 @@ __device__ __forceinline__ void route_select_sig16(const float (&lg)[EPS], const
 // chain bit for bit and no other summation order).  The operands: lane l holds A = x[token l % 16][.] and
 // B = w[expert l % 16][.] for k-lane q = l / 16; the 16 x 16 output block leaves tokens 4 (l / 16) + 0..3 of expert
 // l % 16 in lane l.  Giving k-lane q the 16 consecutive elements 64b + 16q .. 64b + 16q + 15 of 64-element block b,
-// step s of a chained accumulator takes elements 64b + 16q + s for q = 0..3: the fixed order of router.c (both
-// routers), bit for bit, and each operand of a block is 32 contiguous bytes of its row.  Past d the token values are
-// -0 and the weights +0: fma(-0, +0, acc) = acc for every acc (including either zero), so the padded steps change
-// nothing.
+// step s of a chained accumulator takes elements 64b + 16q + s for q = 0..3, and each operand of a block is 32
+// contiguous bytes of its row.  Block b feeds partial chain b % 4 (four independent accumulators: four products in
+// flight where one chain would wait on each result), and the logit is (c0 + c1) + (c2 + c3): the fixed order of
+// router.c (both routers), bit for bit.  Past d the token values are -0 and the weights +0: fma(-0, +0, acc) = acc
+// for every acc (including either zero), so the padded steps change nothing.
 //
 // route_mfma_kernel (the sigmoid router, and the softmax router for E > 16): a workgroup of NW waves routes 16 TT
 // tokens; wave w owns the expert blocks w NB .. w NB + NB - 1 (16 experts each).  Token rows and weight rows stream
@@ -448,11 +449,13 @@ __global__ __launch_bounds__(64 * NW) void route_mfma_kernel(const uint16_t* __r
     f[0] = bf_lo(u.x); f[1] = bf_hi(u.x); f[2] = bf_lo(u.y); f[3] = bf_hi(u.y);
     f[4] = bf_lo(u.z); f[5] = bf_hi(u.z); f[6] = bf_lo(u.w); f[7] = bf_hi(u.w);
   };
-  f32x4 acc[TT][NB];
+  f32x4 acc[TT][NB][4];  // one per partial chain: chunk c holds blocks 2c, 2c + 1, chains 2 (c % 2) + 0, 1
 #pragma unroll
   for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[tt][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int ch = 0; ch < 4; ++ch) acc[tt][nb][ch] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   float bsv[ER / 16];  // the bias of this lane's experts (i * 16 + lane % 16)
 #pragma unroll
   for (int i = 0; i < ER / 16; ++i) {
@@ -464,9 +467,11 @@ __global__ __launch_bounds__(64 * NW) void route_mfma_kernel(const uint16_t* __r
   load_chunk(0);
   store_chunk(0);
   __syncthreads();
-  for (int c = 0; c < nch; ++c) {
+  // chunk c: its parity (a compile-time constant, so that the chain indices are) selects chains 2 PAR, 2 PAR + 1
+  auto chunk = [&](int c, auto par) {
+    constexpr int PAR = decltype(par)::value;
     if (c + 1 < nch) load_chunk(c + 1);
-    const char* base = s_m + (c & 1) * STAGE;
+    const char* base = s_m + PAR * STAGE;
     if (live) {
       // every read of the chunk is issued before the first product (the LDS latency is paid once per chunk)
       uint4 ua[TT][4], ub[NB][4];
@@ -487,11 +492,16 @@ __global__ __launch_bounds__(64 * NW) void route_mfma_kernel(const uint16_t* __r
           for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
-              acc[tt][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[tt][s], b[nb][s], acc[tt][nb], 0, 0, 0);
+              acc[tt][nb][2 * PAR + (h >> 1)] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                  a[tt][s], b[nb][s], acc[tt][nb][2 * PAR + (h >> 1)], 0, 0, 0);
       }
     }
-    if (c + 1 < nch) store_chunk((c + 1) & 1);  // the other buffer: last read before the previous barrier
+    if (c + 1 < nch) store_chunk(1 - PAR);  // the other buffer: last read before the previous barrier
     __syncthreads();
+  };
+  for (int c = 0; c < nch; c += 2) {
+    chunk(c, std::integral_constant<int, 0>());
+    if (c + 1 < nch) chunk(c + 1, std::integral_constant<int, 1>());
   }
   // logits (token, expert) into LDS: lane l holds tokens 16 tt + 4 (l / 16) + i of expert 16 (w NB + nb) + l % 16
   float* lgs = reinterpret_cast<float*>(s_m);
@@ -501,7 +511,9 @@ __global__ __launch_bounds__(64 * NW) void route_mfma_kernel(const uint16_t* __r
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        lgs[(tt * 16 + 4 * (lane >> 4) + i) * LP + (wave * NB + nb) * 16 + r] = acc[tt][nb][i];
+        lgs[(tt * 16 + 4 * (lane >> 4) + i) * LP + (wave * NB + nb) * 16 + r] =
+            __fadd_rn(__fadd_rn(acc[tt][nb][0][i], acc[tt][nb][1][i]),
+                      __fadd_rn(acc[tt][nb][2][i], acc[tt][nb][3][i]));
   __syncthreads();
   if constexpr (SIG) {
     // selection: token tok of the workgroup on segment tok % 4 of wave tok / 4 (four tokens per wave)
@@ -536,13 +548,18 @@ __global__ __launch_bounds__(64 * NW) void route_mfma_kernel(const uint16_t* __r
   }
 }
 
-// The softmax router for E <= 16 without LDS: every wave routes its own 16 tokens against all experts, one 16 x 16
-// output block, with each lane's 32 contiguous bytes of x and of w per block loaded straight into registers kRdPF
-// blocks ahead (no staging, no barrier).  Rows past T read row T - 1 and experts past E read expert 0: their logits
-// are never stored nor selected.  The four tokens of a lane's output column (t0 + 4q + i) go through route_select16
-// together.
+// The softmax router for E <= 16 without LDS staging: a 16-token tile against all experts, one 16 x 16 output block
+// per partial chain, with each lane's 32 contiguous bytes of x and of w per block loaded straight into registers
+// kRdPF blocks ahead.  Rows past T read row T - 1 and experts past E read expert 0: their logits are never stored nor
+// selected.  SPLIT = 1: one wave runs all four chains of its tile (ring slot p holds block b0 + p, b0 a multiple of
+// 4, so slot p feeds chain p) and selects the tile's 16 tokens, four per lane (route_select16<4>); no barrier.
+// SPLIT = 4: the four waves of a workgroup share one tile, wave c running chain c (blocks c, c + 4, ...); the chain
+// sums meet in LDS, and wave c then selects tokens 4c .. 4c + 3 (route_select16<1>).  Four times the waves per tile
+// and a quarter of the blocks per wave: for token counts that leave most of the chip idle.
 constexpr int kRdPF = 4;  // blocks in flight per wave (8 and 12 measured slower: 22.8 and 24.0 against 21.7 us at C5)
+static_assert(kRdPF % 4 == 0, "ring slot p feeds chain p % 4");
 
+template <int SPLIT>
 __global__ __launch_bounds__(256) void route_topk_direct_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                                 const uint16_t* __restrict__ wr,
                                                                 const float* __restrict__ bias, int T, int d, int E,
@@ -551,13 +568,18 @@ __global__ __launch_bounds__(256) void route_topk_direct_kernel(const uint16_t* 
                                                                 int32_t* __restrict__ ids,
                                                                 float* __restrict__ wout) {
 #pragma clang fp contract(off)
+  static_assert(SPLIT == 1 || SPLIT == 4, "one wave per tile or one wave per chain");
+  constexpr int NA = SPLIT == 1 ? 4 : 1;  // chains this wave accumulates
   const int lane = threadIdx.x & 63, r = lane & 15, q = lane >> 4;
-  const int t0 = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * 16;
-  if (t0 >= T) return;  // a whole wave; the kernel has no barrier
+  const int wave = threadIdx.x >> 6;
+  const int t0 = (SPLIT == 1 ? blockIdx.x * (blockDim.x >> 6) + wave : blockIdx.x) * 16;
+  if (t0 >= T) return;  // SPLIT = 1: a whole wave (no barrier); SPLIT = 4: the whole workgroup (one tile)
   const int nbf = d / 64;  // whole blocks; a last partial block (d % 64 != 0) is handled after them
+  const int c = SPLIT == 1 ? 0 : wave;  // SPLIT = 4: the chain this wave runs
+  const int nj = SPLIT == 1 ? nbf : (nbf > c ? (nbf - c + 3) >> 2 : 0);  // whole blocks this wave runs
+  auto blk = [&](int j) { return SPLIT == 1 ? j : c + 4 * j; };
   const uint16_t* xr = x + (int64_t)min(t0 + r, T - 1) * ldx + 16 * q;
   const uint16_t* wrow = wr + (int64_t)(r < E ? r : 0) * d + 16 * q;
-  const float bv = bias && r < E ? bias[r] : 0.0f;
   // loads with no per-lane condition, so that the compiler can keep them in flight across the products
   auto load = [&](int b, uint4 (&xv)[2], uint4 (&wv)[2]) {
 #pragma unroll
@@ -566,7 +588,9 @@ __global__ __launch_bounds__(256) void route_topk_direct_kernel(const uint16_t* 
       wv[h] = *reinterpret_cast<const uint4*>(wrow + 64 * b + 8 * h);
     }
   };
-  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4 acc[NA];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   auto block = [&](const uint4 (&xv)[2], const uint4 (&wv)[2], float (&a)[16], float (&w)[16]) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -581,29 +605,30 @@ __global__ __launch_bounds__(256) void route_topk_direct_kernel(const uint16_t* 
       }
     }
   };
-  auto products = [&](const float (&a)[16], const float (&w)[16]) {
+  auto products = [&](f32x4& ac, const float (&a)[16], const float (&w)[16]) {
 #pragma unroll
-    for (int s2 = 0; s2 < 16; ++s2) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s2], w[s2], acc, 0, 0, 0);
+    for (int s2 = 0; s2 < 16; ++s2) ac = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s2], w[s2], ac, 0, 0, 0);
   };
-  if (nbf > 0) {
+  if (nj > 0) {
     // a ring of kRdPF blocks in registers; every load is unconditional (block indices past the end are clamped to
     // the last block and their values never used), so no slot value is merged across a branch and the loads stay
     // in flight across the products
     uint4 xs[kRdPF][2], ws[kRdPF][2];
 #pragma unroll
-    for (int p = 0; p < kRdPF; ++p) load(min(p, nbf - 1), xs[p], ws[p]);
-    for (int b0 = 0; b0 < nbf; b0 += kRdPF) {
+    for (int p = 0; p < kRdPF; ++p) load(blk(min(p, nj - 1)), xs[p], ws[p]);
+    for (int j0 = 0; j0 < nj; j0 += kRdPF) {
 #pragma unroll
       for (int p = 0; p < kRdPF; ++p) {
-        const int b = b0 + p;
+        const int j = j0 + p;
         float a[16], w[16];
         block(xs[p], ws[p], a, w);
-        load(min(b + kRdPF, nbf - 1), xs[p], ws[p]);  // the slot's values are widened: refill it
-        if (b < nbf) products(a, w);
+        load(blk(min(j + kRdPF, nj - 1)), xs[p], ws[p]);  // the slot's values are widened: refill it
+        if (j < nj) products(acc[p % NA], a, w);
       }
     }
   }
-  if (d & 63) {  // the partial block: pieces past d read the row's first piece and become -0 (x) / +0 (w)
+  if ((d & 63) && (SPLIT == 1 || c == (nbf & 3))) {
+    // the partial block (chain nbf % 4): pieces past d read the row's first piece and become -0 (x) / +0 (w)
     uint4 xv[2], wv[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -615,12 +640,31 @@ __global__ __launch_bounds__(256) void route_topk_direct_kernel(const uint16_t* 
     }
     float a[16], w[16];
     block(xv, wv, a, w);
-    products(a, w);
-  }
-  float lg[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) lg[i] = bias && r < E ? __fadd_rn(acc[i], bv) : acc[i];
-  route_select16<4>(lg, t0, lane, T, E, k, renorm, scaling, logits, ids, wout);
+    for (int ch = 0; ch < NA; ++ch)
+      if (NA == 1 || ch == (nbf & 3)) products(acc[ch], a, w);
+  }
+  const float bv = bias && r < E ? bias[r] : 0.0f;
+  if constexpr (SPLIT == 1) {
+    float lg[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float dot = __fadd_rn(__fadd_rn(acc[0][i], acc[1][i]), __fadd_rn(acc[2][i], acc[3][i]));
+      lg[i] = bias && r < E ? __fadd_rn(dot, bv) : dot;
+    }
+    route_select16<4>(lg, t0, lane, T, E, k, renorm, scaling, logits, ids, wout);
+  } else {
+    // chain sums by (chain, token, expert); lane l holds tokens 4 (l / 16) + i of expert l % 16
+    __shared__ float part[4][16 * 16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) part[c][(4 * q + i) * 16 + r] = acc[0][i];
+    __syncthreads();
+    const int tok = 4 * c + q;  // this lane's token in the tile (segment q of wave c)
+    const float dot = __fadd_rn(__fadd_rn(part[0][tok * 16 + r], part[1][tok * 16 + r]),
+                                __fadd_rn(part[2][tok * 16 + r], part[3][tok * 16 + r]));
+    const float lg[1] = {bias && r < E ? __fadd_rn(dot, bv) : dot};
+    route_select16<1>(lg, t0 + 4 * c, lane, T, E, k, renorm, scaling, logits, ids, wout);
+  }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -1551,17 +1595,24 @@ static int mfma_route_launch(int grid, hipStream_t s, const uint16_t* x, int64_t
   return HMOE_OK;
 }
 
+// below this many tokens the E <= 16 router runs four waves per tile (route_topk_direct_kernel<4>); measured at
+// d = 1536, E = 16: 2048 tokens 12.5 against 17.0 us, 8192 tokens 15.1 against 20.5, 16384 tokens 25.7 against 21.2
+constexpr int64_t kRouteSplitT = 12288;
+
 static int route_launch(const void* x, int64_t ldx, const void* wr, const float* bias, int64_t T, int64_t d, int E,
                         int k, int renorm, float scaling, float* logits, int32_t* topk_ids, float* topk_w,
                         hipStream_t s) {
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* wp = static_cast<const uint16_t*>(wr);
   if (E <= 16) {
-    // every wave its own 16 tokens and all experts; below 8192 tokens one wave per workgroup, so that the waves
-    // spread over more CUs (2048 tokens at d = 1536: 19.6 -> 16.7 us)
-    const int wpb = T >= 8192 ? 4 : 1;
-    hipLaunchKernelGGL(route_topk_direct_kernel, dim3((unsigned)((T + 16 * wpb - 1) / (16 * wpb))), dim3(64 * wpb), 0,
-                       s, xp, ldx, wp, bias, (int)T, (int)d, E, k, renorm, scaling, logits, topk_ids, topk_w);
+    // four waves per 16-token tile below kRouteSplitT tokens, else a wave per tile (four tiles per workgroup)
+    if (T < kRouteSplitT) {
+      hipLaunchKernelGGL(route_topk_direct_kernel<4>, dim3((unsigned)((T + 15) / 16)), dim3(256), 0, s, xp, ldx, wp,
+                         bias, (int)T, (int)d, E, k, renorm, scaling, logits, topk_ids, topk_w);
+    } else {
+      hipLaunchKernelGGL(route_topk_direct_kernel<1>, dim3((unsigned)((T + 63) / 64)), dim3(256), 0, s, xp, ldx, wp,
+                         bias, (int)T, (int)d, E, k, renorm, scaling, logits, topk_ids, topk_w);
+    }
     HMOE_CHECK_LAUNCH();
     return HMOE_OK;
   }
