@@ -31,13 +31,15 @@ def test_route_bitexact(oracle, T, d, E, k):
 
 
 @pytest.mark.parametrize("T,d,E,k", [(40, 8, 16, 2), (40, 136, 9, 2), (33, 200, 16, 3), (50, 328, 4, 2),
-                                     (12300, 200, 7, 2), (12288, 8, 16, 4), (12352, 1032, 16, 2),
+                                     (6150, 200, 7, 2), (6144, 8, 16, 4), (6160, 1032, 16, 2), (6143, 328, 11, 3),
+                                     (24600, 200, 7, 2), (24576, 8, 16, 4), (24592, 1032, 16, 2),
                                      (70, 200, 24, 3), (40, 8, 48, 2)])
 def test_route_chain_edges(oracle, T, d, E, k):
     """The four partial chains where rows end early: d = 8 (no whole block: only chain 0, from the partial block),
     136 (chains 2 and 3 of the whole blocks empty, the partial block on chain 2), 200 (partial block on chain 3),
-    328 (chain 1 holds blocks 1 and 5); T below and above the token count where the E <= 16 router switches from
-    four waves per tile to one (12288), E above 16 for the LDS-staged kernel."""
+    328 (chain 1 holds blocks 1 and 5); T around the token counts where the E <= 16 router goes from four waves per
+    tile to two (6144; an odd number of tiles at 6150 and 6143 leaves the last workgroup's second tile past T) and from
+    two to one (24576); E above 16 for the LDS-staged kernel."""
     print(f"route chains T={T} d={d} E={E} k={k}", flush=True)
     x, wr, _, _ = make_inputs(T, d, E, 8, seed=T + d + E)
     _check(oracle, x, wr, k, bias=np.linspace(-0.5, 0.5, E).astype(np.float32))

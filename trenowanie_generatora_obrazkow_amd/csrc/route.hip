@@ -553,9 +553,10 @@ __global__ __launch_bounds__(64 * NW) void route_mfma_kernel(const uint16_t* __r
 // kRdPF blocks ahead.  Rows past T read row T - 1 and experts past E read expert 0: their logits are never stored nor
 // selected.  SPLIT = 1: one wave runs all four chains of its tile (ring slot p holds block b0 + p, b0 a multiple of
 // 4, so slot p feeds chain p) and selects the tile's 16 tokens, four per lane (route_select16<4>); no barrier.
-// SPLIT = 4: the four waves of a workgroup share one tile, wave c running chain c (blocks c, c + 4, ...); the chain
-// sums meet in LDS, and wave c then selects tokens 4c .. 4c + 3 (route_select16<1>).  Four times the waves per tile
-// and a quarter of the blocks per wave: for token counts that leave most of the chip idle.
+// SPLIT = 2 or 4: SPLIT waves share a tile, wave c running chains c, c + SPLIT, ... (blocks c, c + SPLIT, ...; ring
+// slot p feeds the wave's chain p % (4 / SPLIT)); the chain sums meet in LDS, and wave c then selects tokens
+// 16 c / SPLIT .. of the tile, 4 / SPLIT per lane.  More waves per tile and fewer blocks per wave: for token counts
+// that leave most of the chip idle.
 constexpr int kRdPF = 4;  // blocks in flight per wave (8 and 12 measured slower: 22.8 and 24.0 against 21.7 us at C5)
 static_assert(kRdPF % 4 == 0, "ring slot p feeds chain p % 4");
 
@@ -568,16 +569,19 @@ __global__ __launch_bounds__(256) void route_topk_direct_kernel(const uint16_t* 
                                                                 int32_t* __restrict__ ids,
                                                                 float* __restrict__ wout) {
 #pragma clang fp contract(off)
-  static_assert(SPLIT == 1 || SPLIT == 4, "one wave per tile or one wave per chain");
-  constexpr int NA = SPLIT == 1 ? 4 : 1;  // chains this wave accumulates
+  static_assert(SPLIT == 1 || SPLIT == 2 || SPLIT == 4, "one, two or four waves per tile");
+  constexpr int NA = 4 / SPLIT;  // chains this wave accumulates: c, c + SPLIT, ...
   const int lane = threadIdx.x & 63, r = lane & 15, q = lane >> 4;
   const int wave = threadIdx.x >> 6;
-  const int t0 = (SPLIT == 1 ? blockIdx.x * (blockDim.x >> 6) + wave : blockIdx.x) * 16;
-  if (t0 >= T) return;  // SPLIT = 1: a whole wave (no barrier); SPLIT = 4: the whole workgroup (one tile)
+  const int tg = wave / SPLIT;  // the wave's tile within the workgroup
+  const int t0 = (blockIdx.x * ((int)(blockDim.x >> 6) / SPLIT) + tg) * 16;
+  // SPLIT = 1: a whole wave (no barrier); SPLIT = 4: the whole workgroup (one tile).  SPLIT = 2: the second tile of
+  // the last workgroup may start past T; its waves run on clamped rows and store nothing (route_select16 checks t)
+  if (SPLIT != 2 && t0 >= T) return;
   const int nbf = d / 64;  // whole blocks; a last partial block (d % 64 != 0) is handled after them
-  const int c = SPLIT == 1 ? 0 : wave;  // SPLIT = 4: the chain this wave runs
-  const int nj = SPLIT == 1 ? nbf : (nbf > c ? (nbf - c + 3) >> 2 : 0);  // whole blocks this wave runs
-  auto blk = [&](int j) { return SPLIT == 1 ? j : c + 4 * j; };
+  const int c = wave % SPLIT;  // this wave's first chain
+  const int nj = nbf > c ? (nbf - c + SPLIT - 1) / SPLIT : 0;  // whole blocks this wave runs: c, c + SPLIT, ...
+  auto blk = [&](int j) { return c + SPLIT * j; };
   const uint16_t* xr = x + (int64_t)min(t0 + r, T - 1) * ldx + 16 * q;
   const uint16_t* wrow = wr + (int64_t)(r < E ? r : 0) * d + 16 * q;
   // loads with no per-lane condition, so that the compiler can keep them in flight across the products
@@ -627,7 +631,7 @@ __global__ __launch_bounds__(256) void route_topk_direct_kernel(const uint16_t* 
       }
     }
   }
-  if ((d & 63) && (SPLIT == 1 || c == (nbf & 3))) {
+  if ((d & 63) && c == (nbf & 3) % SPLIT) {
     // the partial block (chain nbf % 4): pieces past d read the row's first piece and become -0 (x) / +0 (w)
     uint4 xv[2], wv[2];
 #pragma unroll
@@ -641,8 +645,8 @@ __global__ __launch_bounds__(256) void route_topk_direct_kernel(const uint16_t* 
     float a[16], w[16];
     block(xv, wv, a, w);
 #pragma unroll
-    for (int ch = 0; ch < NA; ++ch)
-      if (NA == 1 || ch == (nbf & 3)) products(acc[ch], a, w);
+    for (int i = 0; i < NA; ++i)
+      if (NA == 1 || i == (nbf & 3) / SPLIT) products(acc[i], a, w);
   }
   const float bv = bias && r < E ? bias[r] : 0.0f;
   if constexpr (SPLIT == 1) {
@@ -655,15 +659,22 @@ __global__ __launch_bounds__(256) void route_topk_direct_kernel(const uint16_t* 
     route_select16<4>(lg, t0, lane, T, E, k, renorm, scaling, logits, ids, wout);
   } else {
     // chain sums by (chain, token, expert); lane l holds tokens 4 (l / 16) + i of expert l % 16
-    __shared__ float part[4][16 * 16];
+    constexpr int NI = 4 / SPLIT;  // tokens per lane in the selection: wave c takes tokens 16 c / SPLIT ..
+    __shared__ float part[SPLIT == 2 ? 2 : 1][4][16 * 16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) part[c][(4 * q + i) * 16 + r] = acc[0][i];
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) part[tg][c + SPLIT * a][(4 * q + i) * 16 + r] = acc[a][i];
     __syncthreads();
-    const int tok = 4 * c + q;  // this lane's token in the tile (segment q of wave c)
-    const float dot = __fadd_rn(__fadd_rn(part[0][tok * 16 + r], part[1][tok * 16 + r]),
-                                __fadd_rn(part[2][tok * 16 + r], part[3][tok * 16 + r]));
-    const float lg[1] = {bias && r < E ? __fadd_rn(dot, bv) : dot};
-    route_select16<1>(lg, t0 + 4 * c, lane, T, E, k, renorm, scaling, logits, ids, wout);
+    float lg[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int tok = 16 / SPLIT * c + i + NI * q;  // route_select16's token for (lane, i)
+      const float* pt = part[tg][0] + tok * 16 + r;
+      const float dot = __fadd_rn(__fadd_rn(pt[0], pt[256]), __fadd_rn(pt[512], pt[768]));
+      lg[i] = bias && r < E ? __fadd_rn(dot, bv) : dot;
+    }
+    route_select16<NI>(lg, t0 + 16 / SPLIT * c, lane, T, E, k, renorm, scaling, logits, ids, wout);
   }
 }
 
@@ -1595,9 +1606,10 @@ static int mfma_route_launch(int grid, hipStream_t s, const uint16_t* x, int64_t
   return HMOE_OK;
 }
 
-// below this many tokens the E <= 16 router runs four waves per tile (route_topk_direct_kernel<4>); measured at
-// d = 1536, E = 16: 2048 tokens 12.5 against 17.0 us, 8192 tokens 15.1 against 20.5, 16384 tokens 25.7 against 21.2
-constexpr int64_t kRouteSplitT = 12288;
+// waves per 16-token tile of the E <= 16 router by token count, from same-process A/Bs at d = 1536, E = 16 (one /
+// two / four waves): 2048 tokens 17.0 / 12.3 / 11.6 us, 4096 17.0 / 12.4 / 11.6, 8192 20.5 / 12.6 / 14.9, 16384
+// 20.9 / 20.0 / 25.7, 32768 32.9 / 33.8 / 46.3
+constexpr int64_t kRouteSplit4T = 6144, kRouteSplit2T = 24576;
 
 static int route_launch(const void* x, int64_t ldx, const void* wr, const float* bias, int64_t T, int64_t d, int E,
                         int k, int renorm, float scaling, float* logits, int32_t* topk_ids, float* topk_w,
@@ -1605,9 +1617,13 @@ static int route_launch(const void* x, int64_t ldx, const void* wr, const float*
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* wp = static_cast<const uint16_t*>(wr);
   if (E <= 16) {
-    // four waves per 16-token tile below kRouteSplitT tokens, else a wave per tile (four tiles per workgroup)
-    if (T < kRouteSplitT) {
+    // four waves per 16-token tile below kRouteSplit4T tokens, two below kRouteSplit2T, else one (four tiles per
+    // workgroup)
+    if (T < kRouteSplit4T) {
       hipLaunchKernelGGL(route_topk_direct_kernel<4>, dim3((unsigned)((T + 15) / 16)), dim3(256), 0, s, xp, ldx, wp,
+                         bias, (int)T, (int)d, E, k, renorm, scaling, logits, topk_ids, topk_w);
+    } else if (T < kRouteSplit2T) {
+      hipLaunchKernelGGL(route_topk_direct_kernel<2>, dim3((unsigned)((T + 31) / 32)), dim3(256), 0, s, xp, ldx, wp,
                          bias, (int)T, (int)d, E, k, renorm, scaling, logits, topk_ids, topk_w);
     } else {
       hipLaunchKernelGGL(route_topk_direct_kernel<1>, dim3((unsigned)((T + 63) / 64)), dim3(256), 0, s, xp, ldx, wp,
