@@ -106,7 +106,8 @@ def time_steps(step, steps, warmup, graph, probe_kernel, probe_every=1, probe_fi
         ms = (time.perf_counter() - t0) * 1e3 / steps
         del g
     # the probe's two event records cost the stream a few microseconds each, so every PROBE_STRIDE-th step carries
-    # them (the first step always)
+    # them (the first step always).  A forward without gradient runs as one C call (ops.moe_forward) except in the
+    # steps that carry the probe, which launch the same kernels op by op so that the events can sit between them
     probes = {probe_kernel: []}
     torch.cuda.synchronize()
     t0 = time.perf_counter()

@@ -211,6 +211,21 @@ int hmoe_combine(const void* y, const int32_t* inv_pos, int64_t T, int k, int64_
 int hmoe_combine_add(const void* y, const int32_t* inv_pos, int64_t T, int k, int64_t d, const void* add, void* out,
                      int dtype, hmoe_stream_t stream);
 
+/* Whole routed forward in one call (inference): replaces the body of aurora/hf_compat.py:69-82 (route, sort,
+ * gather, grouped gate/up, act * up, grouped down with weight and scatter, sum over slots) for a softmax top-k router
+ * (conventions of aurora/hf_pipeline.py:352-359).  It runs hmoe_route_topk, hmoe_dispatch_tiles,
+ * hmoe_gate_up_swiglu_tiles (h >= 4096, tiles below 2^31 bytes) or hmoe_gate_up_swiglu (rows gathered through
+ * a_idx), hmoe_down_scatter and hmoe_combine in that order, with the intermediates (sort arrays, tiles, act, y) in
+ * the workspace, so out, topk_ids, topk_w and logits (NULL to skip) are those the five calls give one by one.  x (T,
+ * d) bf16 with row stride ldx; wr (E, d), wgu (E, d, 2h), wd (E, h, d) bf16; bias (E,) fp32 or NULL; out (T, d) bf16.
+ * workspace: hmoe_moe_forward_workspace_size(T, d, E, k, h) bytes, 256-byte aligned.  Limits as the five entry
+ * points (d % 8 == 0, h % 8 == 0, E <= 256, k <= 16). */
+size_t hmoe_moe_forward_workspace_size(int64_t T, int64_t d, int E, int k, int64_t h);
+int hmoe_moe_forward(const void* x, int64_t ldx, const void* wr, const float* bias, const void* wgu, const void* wd,
+                     int64_t T, int64_t d, int E, int k, int64_t h, int renorm, float scaling, void* out,
+                     int32_t* topk_ids, float* topk_w, float* logits, void* workspace, size_t workspace_bytes,
+                     hmoe_stream_t stream);
+
 /* ---------------------------------------------------------------------------------------------------------------
  * Backward.  The reference has no backward for this path (aurora/hf_compat.py:62 is @torch.no_grad); each entry
  * point below differentiates the forward line it names.

@@ -129,6 +129,17 @@ def test_argument_validation_codes(lib):
     assert L.hmoe_unpermute_bwd(P, 5, P, None, None, 4, 2, 64, 0, P, None) == -3
     assert L.hmoe_router_bwd(P, P, P, 16, 300, 2, 1, 1.0, P, 64, 64, P, None, 2, None, 0, None) == -2
     assert L.hmoe_router_bwd(P, P, P, 16, 8, 2, 1, 1.0, P, 64, 64, P, P, 2, None, 0, None) == -5
+    # one-call forward: workspace missing / short, misaligned operands, widths off the granule, k > E, empty input
+    ws = L.hmoe_moe_forward_workspace_size(4, 64, 8, 2, 64)
+    fwd = lambda x, T, d, E, k, h, ws_ptr, ws_b: L.hmoe_moe_forward(x, d, P, None, P, P, T, d, E, k, h, 1, 1.0, P, P, P,
+                                                                    None, ws_ptr, ws_b, None)
+    assert fwd(P, 4, 64, 8, 2, 64, None, 0) == -5
+    assert fwd(P, 4, 64, 8, 2, 64, P, ws - 1) == -5
+    assert fwd(P + 8, 4, 64, 8, 2, 64, P, ws) == -1
+    assert fwd(P, 4, 64, 8, 2, 64, P + 16, ws) == -1  # workspace not 256-byte aligned
+    assert fwd(P, 4, 64, 8, 2, 60, P, L.hmoe_moe_forward_workspace_size(4, 64, 8, 2, 60)) == -2
+    assert fwd(P, 4, 64, 8, 9, 64, P, ws) == -1
+    assert fwd(P, 0, 64, 8, 2, 64, None, 0) == 0
 
 
 def test_workspace_queries(lib):
@@ -139,6 +150,16 @@ def test_workspace_queries(lib):
     # one fp32 (E, d) partial per 128-token chunk
     assert L.hmoe_router_bwd_workspace_size(16384, 16, 1536) == 128 * 16 * 1536 * 4
     assert L.hmoe_router_bwd_workspace_size(129, 16, 1536) == 2 * 16 * 1536 * 4
+    # one-call forward: at least act (M h), y (M d), the sort arrays and the dispatch workspace; the row-group tiles
+    # only from h = 4096 on; 0 for sizes no entry point takes
+    T, d, E, k = 2048, 1024, 8, 2
+    M = T * k
+    base = M * 2048 * 2 + M * d * 2 + 3 * M * 4 + M * 2 + L.hmoe_dispatch_workspace_size(T, k, E)
+    small = L.hmoe_moe_forward_workspace_size(T, d, E, k, 2048)
+    assert base <= small < base + 16 * 256 and small % 256 == 0
+    wide = L.hmoe_moe_forward_workspace_size(T, d, E, k, 4096)
+    assert wide - small >= M * 2048 * 2 + L.hmoe_xs_tiles_bytes(M, E, d)
+    assert L.hmoe_moe_forward_workspace_size(T, d, E, 9, 2048) == 0 and L.hmoe_moe_forward_workspace_size(-1, d, E, k, 64) == 0
 
 
 def test_bench_refuses_multi_gpu():

@@ -1,0 +1,91 @@
+"""The one-call forward (hmoe_moe_forward, ops.moe_forward) against the same layer driven entry point by entry
+point: out, topk_ids, topk_w and logits bit-identical, on both gate/up forms (row-group tiles from h = 4096 on, rows
+gathered through a_idx below), ragged widths and counts, a logit bias, no renormalisation, one token and none; and
+moe_swiglu without a gradient to record (the one-call path) against the same call recording one (the autograd
+path)."""
+import numpy as np
+import pytest
+import torch
+
+from tests.util import make_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _op_by_op(x, wr, wgu, wd, k, bias, renorm):
+    from trenowanie_generatora_obrazkow_amd import ops
+    T = x.shape[0]
+    E = wgu.shape[0]
+    logits, ids, tw = ops.route_topk(x, wr, k, bias=bias, renorm=renorm)
+    disp, act, _ = ops.routed_gate_up(x, ids, E, wgu, topk_w=tw)
+    y, _ = ops.down_scatter(act, wd, disp.counts, T * k, disp.w_sorted, disp.order)
+    return ops.combine(y, T, k), ids, tw, logits
+
+
+def _same(a, b, name):
+    assert a.shape == b.shape and a.dtype == b.dtype, name
+    assert torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a,
+                       b.view(torch.int16) if b.dtype == torch.bfloat16 else b), name
+
+
+@pytest.mark.parametrize("T,d,E,k,h,bias,renorm", [(512, 256, 8, 2, 512, False, True),
+                                                   (2048, 1024, 8, 2, 2048, True, True),
+                                                   (600, 1536, 16, 2, 4096, False, True),
+                                                   (77, 520, 5, 3, 24, True, False),
+                                                   (300, 256, 64, 6, 96, False, True),
+                                                   (1, 264, 12, 4, 40, True, True)])
+def test_one_call_forward_matches_op_by_op(T, d, E, k, h, bias, renorm):
+    from trenowanie_generatora_obrazkow_amd import ops
+    print(f"moe_forward T={T} d={d} E={E} k={k} h={h} bias={bias} renorm={renorm}", flush=True)
+    dev = torch.device("cuda")
+    x, wr, wgu, wd = (t.to(dev) for t in make_inputs(T, d, E, h, seed=T + h))
+    b = torch.linspace(-0.3, 0.3, E, device=dev) if bias else None
+    ref = _op_by_op(x, wr, wgu, wd, k, b, renorm)
+    out, ids, tw, logits = ops.moe_forward(x, wr, wgu, wd, k, bias=b, renorm=renorm, want_logits=True)
+    torch.cuda.synchronize()
+    for got, want, name in zip((out, ids, tw, logits), ref, ("out", "topk_ids", "topk_w", "logits")):
+        _same(got, want, name)
+    # a second call with the intermediates of the first still in the caching allocator: same bits
+    out2, ids2, tw2, _ = ops.moe_forward(x, wr, wgu, wd, k, bias=b, renorm=renorm)
+    _same(out2, out, "out (second call)")
+    _same(ids2, ids, "topk_ids (second call)")
+
+
+def test_one_call_forward_strided_rows_and_empty():
+    from trenowanie_generatora_obrazkow_amd import ops
+    dev = torch.device("cuda")
+    x, wr, wgu, wd = (t.to(dev) for t in make_inputs(130, 512, 8, 128, seed=5))
+    wide = torch.zeros(130, 640, device=dev, dtype=torch.bfloat16)
+    wide[:, :512] = x
+    xs = wide[:, :512]  # rows 640 elements apart
+    ref = _op_by_op(x, wr, wgu, wd, 2, None, True)
+    out, ids, tw, _ = ops.moe_forward(xs, wr, wgu, wd, 2)
+    _same(out, ref[0], "out")
+    _same(ids, ref[1], "topk_ids")
+    out0, ids0, tw0, _ = ops.moe_forward(x[:0], wr, wgu, wd, 2)
+    assert out0.shape == (0, 512) and ids0.shape == (0, 2) and tw0.shape == (0, 2)
+
+
+@pytest.mark.parametrize("wdt", [torch.bfloat16, torch.float32])
+def test_moe_swiglu_no_grad_uses_one_call_with_same_result(wdt):
+    from trenowanie_generatora_obrazkow_amd import moe_swiglu
+    dev = torch.device("cuda")
+    x, wr, wgu, wd = (t.to(dev) for t in make_inputs(1000, 768, 16, 256, seed=7))
+    wr, wgu, wd = (t.to(wdt) for t in (wr, wgu, wd))
+    bias = torch.linspace(-0.2, 0.2, 16, device=dev)
+    with torch.no_grad():
+        out_ng, ids_ng, tw_ng = moe_swiglu(x, wr, wgu, wd, 2, logit_bias=bias)
+    params = [t.clone().requires_grad_(True) for t in (wr, wgu, wd)]
+    out_g, ids_g, tw_g = moe_swiglu(x, *params, 2, logit_bias=bias)
+    assert out_g.requires_grad and not out_ng.requires_grad
+    _same(out_ng, out_g.detach(), "out")
+    _same(ids_ng, ids_g, "topk_ids")
+    _same(tw_ng, tw_g.detach(), "topk_w")
+    # the module under inference mode takes the same path
+    from trenowanie_generatora_obrazkow_amd import MoESwiGLU
+    m = MoESwiGLU(768, 256, 16, 2).to(dev)
+    h_in = torch.randn(2, 50, 768, device=dev).bfloat16()
+    with torch.inference_mode():
+        a = m(h_in)
+    b_ = m(h_in).detach()
+    assert np.array_equal(a.float().cpu().numpy(), b_.float().cpu().numpy())

@@ -10,7 +10,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB_DIR = os.path.join(HERE, "_lib")
 LIB = os.path.join(LIB_DIR, "libhmoe.so")
-SOURCES = ["route.hip", "gemm.hip"]
+SOURCES = ["route.hip", "gemm.hip", "layer.hip"]
 ARCH = os.environ.get("HMOE_ARCH", "gfx950")
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in generated code.

@@ -125,7 +125,15 @@ def moe_swiglu(x, router_weight, w_gu, w_d, top_k, logit_bias=None, renorm=True)
 
     router_weight (E, d), w_gu (E, d, 2h) = [gate | up], w_d (E, h, d): bf16, or fp32 / fp16 (rounded to bf16 for
     the products, gradients in the weights' dtype).  logit_bias (E,) fp32 is added to the router logits (no gradient).  Gradients reach
-    x and the three weights from `out` and from `topk_weight` (softmax + renormalisation Jacobian)."""
+    x and the three weights from `out` and from `topk_weight` (softmax + renormalisation Jacobian).  Without a
+    gradient to record (grad mode off, or no input requiring one) the forward runs as one C call
+    (ops.moe_forward): the same kernels and outputs, a fraction of the host time."""
+    if not (torch.is_grad_enabled() and (x.requires_grad or router_weight.requires_grad or w_gu.requires_grad
+                                         or w_d.requires_grad)):
+        _check_layer_args(x, router_weight, w_gu, w_d, logit_bias, top_k)
+        out, ids, tw, _ = ops.moe_forward(x, _bf16(router_weight), _bf16(w_gu), _bf16(w_d), top_k, bias=logit_bias,
+                                          renorm=renorm)
+        return out, ids, tw
     return _MoEFunction.apply(x, router_weight, w_gu, w_d, logit_bias, top_k, renorm)
 
 

@@ -123,6 +123,51 @@ def route_topk(x: torch.Tensor, wr: torch.Tensor, k: int, bias=None, renorm=True
     return logits, ids, w
 
 
+def moe_forward(x, wr, wgu, wd, k, bias=None, renorm=True, scaling=1.0, want_logits=False):
+    """The routed forward of a layer in one C call (hmoe_moe_forward): route_topk, routed_gate_up, down_scatter and
+    combine, with the same outputs and their intermediates in one workspace, for callers whose host time per layer
+    matters (small batches).  x (T, d) bf16 with contiguous rows; wr (E, d), wgu (E, d, 2h), wd (E, h, d) bf16,
+    contiguous; bias (E,) or None -> (out (T, d) bf16, topk_ids (T, k) int32, topk_w (T, k) fp32, logits (T, E)
+    fp32 or None)."""
+    T, d = x.shape
+    E = wr.shape[0]
+    _router_args(x, wr)
+    _need(wr, "router weight", (E, d), _BF16)
+    if wgu.dim() != 3 or wd.dim() != 3:
+        raise ValueError("wgu (E, d, 2h) and wd (E, h, d) expected")
+    h = wd.shape[1]
+    _need(wgu, "wgu", (E, d, 2 * h), _BF16)
+    _need(wd, "wd", (E, h, d), _BF16)
+    if bias is not None:
+        if tuple(bias.shape) != (E,):
+            raise ValueError(f"logit bias: shape {tuple(bias.shape)}, expected ({E},)")
+        bias = _contig(bias.to(torch.float32), "bias")
+    if probe is not None and any(n in probe for n in _FWD_OPS):
+        # event timing of single ops (bench.py's probe) needs the launches apart: the same entry points one by one
+        logits, ids, w = route_topk(x, wr, k, bias=bias, renorm=renorm, scaling=scaling, want_logits=want_logits)
+        disp, act, _ = routed_gate_up(x, ids, E, wgu, topk_w=w, want_inv=True)
+        y, _ = down_scatter(act, wd, disp.counts, T * k, disp.w_sorted, disp.order)
+        return combine(y, T, k, inv_pos=disp.inv_pos), ids, w, logits
+    lib = L.lib()
+    ws_bytes = lib.hmoe_moe_forward_workspace_size(T, d, E, k, h)
+    if ws_bytes == 0:
+        raise ValueError(f"moe_forward: unsupported sizes T={T} d={d} E={E} k={k} h={h}")
+    dev = x.device
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+    out = torch.empty(T, d, device=dev, dtype=torch.bfloat16)
+    ids = torch.empty(T, k, device=dev, dtype=torch.int32)
+    w = torch.empty(T, k, device=dev, dtype=torch.float32)
+    logits = torch.empty(T, E, device=dev, dtype=torch.float32) if want_logits else None
+    with _Probe("moe_forward"):
+        L.call("hmoe_moe_forward", L.ptr(x), x.stride(0), L.ptr(wr), L.ptr(bias), L.ptr(wgu), L.ptr(wd), T, d, E, k,
+               h, int(bool(renorm)), float(scaling), L.ptr(out), L.ptr(ids), L.ptr(w), L.ptr(logits), L.ptr(ws),
+               ws_bytes, _dev_stream(x))
+    return out, ids, w, logits
+
+
+_FWD_OPS = ("route_topk", "dispatch", "gate_up_swiglu", "down_scatter", "combine")
+
+
 def route_sigmoid_group(x: torch.Tensor, wr: torch.Tensor, k: int, n_group: int, topk_group: int, expert_bias=None,
                         scaling=1.0, want_scores=False):
     """BailingMoeV2 sigmoid, group-limited router -> (scores (T, E) fp32 or None, topk_ids (T, k) int32,
