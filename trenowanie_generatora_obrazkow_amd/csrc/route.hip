@@ -889,6 +889,106 @@ __global__ __launch_bounds__(256) void dispatch_index_kernel(const void* __restr
   }
 }
 
+// Small inputs without row copies (M <= kSmallM flat rows, E <= kSmallE): the three passes in one workgroup of 16
+// waves.  Wave w takes the flat rows [w C, (w + 1) C) (C = kSmallRows * 64), 64 at a time in flat order: a row's rank
+// among the wave's earlier rows of its expert comes from the wave ballots of the histogram pass (peers agree on every
+// id bit) plus the wave's running count, kept in LDS per (wave, expert).  The waves' counts are then scanned per
+// expert (wave order = flat order) and the totals over the experts, and each row's position is its expert's start
+// plus the earlier waves' count plus its rank: the same stable counting sort, so the same outputs as the three
+// passes, with one launch instead of three.
+constexpr int kSmallRows = 8;                   // flat rows per lane
+constexpr int kSmallE = 64;                     // experts: one lane each in the scan
+constexpr int64_t kSmallM = 16 * 64 * kSmallRows;  // 8192 flat rows
+
+__global__ __launch_bounds__(1024) void dispatch_small_kernel(const void* __restrict__ ids, int ids64,
+                                                              const void* __restrict__ tw, int tw_dtype, int ws_f16,
+                                                              int64_t M, int k, int E, int nbits,
+                                                              int32_t* __restrict__ counts,
+                                                              int64_t* __restrict__ counts64,
+                                                              int32_t* __restrict__ starts,
+                                                              int32_t* __restrict__ order, int32_t* __restrict__ a_idx,
+                                                              int32_t* __restrict__ inv_pos,
+                                                              uint16_t* __restrict__ w_sorted,
+                                                              int32_t* __restrict__ n_invalid) {
+  __shared__ int run[16][kSmallE];  // per wave and expert: its rows so far, then the earlier waves' rows
+  __shared__ int st[kSmallE + 1];   // expert starts
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  for (int e = lane; e < kSmallE; e += 64) run[w][e] = 0;
+  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const int64_t f0 = (int64_t)w * 64 * kSmallRows;
+  int ev[kSmallRows], rk[kSmallRows];
+#pragma unroll
+  for (int i = 0; i < kSmallRows; ++i) {
+    const int64_t f = f0 + i * 64 + lane;
+    ev[i] = f < M ? load_id(ids, ids64, f) : -1;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kSmallRows; ++i) {
+    const int e = ev[i];
+    const bool valid = e >= 0 && e < E;
+    uint64_t peers = __ballot(valid);
+    for (int b = 0; b < nbits; ++b) {
+      const bool bit = valid && ((e >> b) & 1);
+      const uint64_t m1 = __ballot(bit);
+      peers &= ((e >> b) & 1) ? m1 : ~m1;
+    }
+    const int r = __popcll(peers & lt);
+    int basecnt = 0;
+    if (valid) basecnt = run[w][e];
+    rk[i] = basecnt + r;
+    __builtin_amdgcn_wave_barrier();  // every lane has read run[w][.] before the step's first lane updates it
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    if (valid && r == 0) run[w][e] = basecnt + __popcll(peers);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+  }
+  __syncthreads();
+  // per expert (lane e of wave 0): exclusive prefix over the waves, the total, then the starts over the experts
+  if (w == 0) {
+    int tot = 0;
+    if (lane < E) {
+#pragma unroll
+      for (int ww = 0; ww < 16; ++ww) {
+        const int c = run[ww][lane];
+        run[ww][lane] = tot;
+        tot += c;
+      }
+    }
+    int incl = lane < E ? tot : 0;
+#pragma unroll
+    for (int sft = 1; sft < 64; sft <<= 1) {
+      const int o = __shfl_up(incl, sft, 64);
+      if (lane >= sft) incl += o;
+    }
+    if (lane < E) {
+      st[lane] = incl - tot;
+      counts[lane] = tot;
+      if (counts64) counts64[lane] = tot;
+      starts[lane] = incl - tot;
+    }
+    if (lane == 63) {
+      st[E] = incl;
+      starts[E] = incl;
+      if (n_invalid) n_invalid[0] = (int32_t)(M - incl);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kSmallRows; ++i) {
+    const int64_t f = f0 + i * 64 + lane;
+    if (f >= M) break;
+    const int e = ev[i];
+    const int64_t pos = (e >= 0 && e < E) ? (int64_t)st[e] + run[w][e] + rk[i] : -1;
+    if (pos >= 0) {
+      order[pos] = (int32_t)f;
+      if (a_idx) a_idx[pos] = (int32_t)(f / k);
+      if (w_sorted) w_sorted[pos] = route_w16(tw, tw_dtype, f, ws_f16);
+    }
+    if (inv_pos) inv_pos[f] = (int32_t)pos;
+  }
+}
+
 // one wave per token: sorted positions of its k rows, index arrays, then the row copies x[t] -> xs[pos_j] and into
 // the row-group tiles (64-byte pieces: slice s of row pos_j, its chunks swizzled as in the K-major LDS image)
 // KT: the slot count k when it is 1, 2, 4 or 8 (0: any k up to kMaxK), so the per-slot arrays hold only k entries
@@ -1702,6 +1802,12 @@ static int dispatch_impl(const void* topk_ids, int ids_dtype, const void* topk_w
   int nbits = 0;
   while ((1 << nbits) < E) ++nbits;
   const int ids64 = ids_dtype == HMOE_DT_I64;
+  if (!xs && !xs_tiles && M <= kSmallM && E <= kSmallE) {
+    hipLaunchKernelGGL(dispatch_small_kernel, dim3(1), dim3(1024), 0, s, topk_ids, ids64, topk_w, w_dtype, (int)f16,
+                       M, k, E, nbits, counts, counts64, starts, order, a_idx, inv_pos, w_sorted, n_invalid);
+    HMOE_CHECK_LAUNCH();
+    return HMOE_OK;
+  }
   if (M > 0) {
     hipLaunchKernelGGL(dispatch_hist_kernel, dim3((unsigned)nblk), dim3(64), 0, s, topk_ids, ids64, M, E, nbits,
                        hist, rank);
