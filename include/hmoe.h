@@ -65,7 +65,9 @@ const char* hmoe_error_string(int code);
  * Each logit is a fixed-order fp32 sum, so ids, weights and logits are bit-reproducible by a host restatement: the
  * row in 64-element blocks, block b feeding fma chain b % 4 (each from +0, its blocks in order, step s of block b
  * taking elements 64b + 16q + s for q = 0..3), logit = (c0 + c1) + (c2 + c3), plus the bias (one rounded addition).
- * d % 8 == 0, E <= 256, k <= 16. */
+ * With E > 16, T * E <= 2^18 and a logits buffer, the logits are first written there per (16 tokens, 16 experts)
+ * block and the selection then reads them (two launches spread over the chip; the same results): passing logits is
+ * faster for small inputs even when they are not needed.  d % 8 == 0, E <= 256, k <= 16. */
 int hmoe_route_topk(const void* x, int64_t ldx, const void* wr, const float* bias, int64_t T, int64_t d, int E,
                     int k, int renorm, float scaling, float* logits, int32_t* topk_ids, float* topk_w,
                     hmoe_stream_t stream);
@@ -76,7 +78,8 @@ int hmoe_route_topk(const void* x, int64_t ldx, const void* wr, const float* bia
  * selection only; the experts form n_group groups of E / n_group, a group's value is the sum of its two largest
  * routing values, the topk_group best groups are kept (ties to the lower group) and the k best experts among them
  * selected (descending, ties to the lower expert); topk_w = selected scores / (their sum in slot order + 1e-20) *
- * scaling.  scores (T, E) fp32 receives the sigmoid scores (NULL to skip).  E % n_group == 0; unless
+ * scaling.  scores (T, E) fp32 receives the sigmoid scores (NULL to skip; for T * E <= 2^18 the logits pass through
+ * it as in hmoe_route_topk, so passing it is faster for small inputs).  E % n_group == 0; unless
  * topk_group >= n_group (every group kept), E / n_group is a power of two in [2, 64] and k <= topk_group *
  * E / n_group.  Other limits as hmoe_route_topk. */
 int hmoe_route_sigmoid_group(const void* x, int64_t ldx, const void* wr, const float* expert_bias, int64_t T,

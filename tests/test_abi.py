@@ -150,11 +150,11 @@ def test_workspace_queries(lib):
     # one fp32 (E, d) partial per 128-token chunk
     assert L.hmoe_router_bwd_workspace_size(16384, 16, 1536) == 128 * 16 * 1536 * 4
     assert L.hmoe_router_bwd_workspace_size(129, 16, 1536) == 2 * 16 * 1536 * 4
-    # one-call forward: at least act (M h), y (M d), the sort arrays and the dispatch workspace; the row-group tiles
-    # only from h = 4096 on; 0 for sizes no entry point takes
+    # one-call forward: at least the router logits (T E), act (M h), y (M d), the sort arrays and the dispatch
+    # workspace; the row-group tiles only from h = 4096 on; 0 for sizes no entry point takes
     T, d, E, k = 2048, 1024, 8, 2
     M = T * k
-    base = M * 2048 * 2 + M * d * 2 + 3 * M * 4 + M * 2 + L.hmoe_dispatch_workspace_size(T, k, E)
+    base = T * E * 4 + M * 2048 * 2 + M * d * 2 + 3 * M * 4 + M * 2 + L.hmoe_dispatch_workspace_size(T, k, E)
     small = L.hmoe_moe_forward_workspace_size(T, d, E, k, 2048)
     assert base <= small < base + 16 * 256 and small % 256 == 0
     wide = L.hmoe_moe_forward_workspace_size(T, d, E, k, 4096)

@@ -81,3 +81,35 @@ def test_route_denormal_products(oracle, T, d, E, k):
     rl, _, _ = oracle.route(bits(x), bits(wr), k)
     tiny = np.abs(rl) < np.finfo(np.float32).tiny
     assert tiny.mean() > 0.5, tiny.mean()  # most logits are denormal
+
+
+@pytest.mark.parametrize("T,d,E,k,sig", [(64, 2048, 128, 8, True), (333, 1536, 256, 4, True), (40, 520, 16, 2, True),
+                                         (256, 2048, 64, 4, False), (1000, 1032, 60, 4, False),
+                                         (2048, 1024, 128, 8, True), (4096, 1024, 64, 4, False)])
+def test_route_small_inputs_with_and_without_buffer(T, d, E, k, sig):
+    """Small inputs route through the caller's logits / scores buffer (a logits pass over (16-token, 16-expert)
+    blocks, then the selection); without one they take the one-launch kernel.  Both give the same ids and weights,
+    and the buffered logits are those of the one-launch kernel at a size where it writes them."""
+    from trenowanie_generatora_obrazkow_amd import _lib as L
+    print(f"route small T={T} d={d} E={E} k={k} sigmoid={sig}", flush=True)
+    dev = torch.device("cuda")
+    x, wr, _, _ = make_inputs(T, d, E, 8, seed=T + E + k)
+    x, wr = x.to(dev), wr.to(dev)
+    bias = torch.linspace(-0.1, 0.1, E, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for with_buf in (True, False):
+        buf = torch.empty(T, E, device=dev) if with_buf else None
+        ids = torch.empty(T, k, device=dev, dtype=torch.int32)
+        w = torch.empty(T, k, device=dev)
+        ptr = lambda t: None if t is None else t.data_ptr()
+        if sig:
+            L.call("hmoe_route_sigmoid_group", x.data_ptr(), x.stride(0), wr.data_ptr(), bias.data_ptr(), T, d, E, k,
+                   8 if E % 8 == 0 and E >= 16 else 1, 4 if E % 8 == 0 and E >= 16 else 1, 2.5, ptr(buf),
+                   ids.data_ptr(), w.data_ptr(), s)
+        else:
+            L.call("hmoe_route_topk", x.data_ptr(), x.stride(0), wr.data_ptr(), bias.data_ptr(), T, d, E, k, 1, 1.0,
+                   ptr(buf), ids.data_ptr(), w.data_ptr(), s)
+        outs.append((ids.cpu(), w.cpu()))
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[0][1].view(torch.int32), outs[1][1].view(torch.int32))

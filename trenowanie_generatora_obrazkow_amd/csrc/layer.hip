@@ -18,7 +18,7 @@ constexpr int64_t kTilesMinH = 4096;
 size_t al256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
 struct FwdLayout {
-  size_t counts, starts, order, a_idx, inv, w_sorted, n_invalid, dws, tiles, act, y, total;
+  size_t logits, counts, starts, order, a_idx, inv, w_sorted, n_invalid, dws, tiles, act, y, total;
   size_t dws_bytes;
   bool tiles_on;
 };
@@ -36,6 +36,7 @@ bool fwd_layout(int64_t T, int64_t d, int E, int k, int64_t h, FwdLayout& L) {
     o += al256(bytes > 0 ? bytes : 1);
     return at;
   };
+  L.logits = take(static_cast<size_t>(T) * static_cast<size_t>(E) * 4);  // the router's, when the caller has none
   L.counts = take(static_cast<size_t>(E) * 4);
   L.starts = take(static_cast<size_t>(E + 1) * 4);
   L.order = take(static_cast<size_t>(M) * 4);
@@ -87,7 +88,10 @@ int hmoe_moe_forward(const void* x, int64_t ldx, const void* wr, const float* bi
   void* tiles = L.tiles_on ? ws + L.tiles : nullptr;
   void* act = ws + L.act;
   void* y = ws + L.y;
-  int rc = hmoe_route_topk(x, ldx, wr, bias, T, d, E, k, renorm, scaling, logits, topk_ids, topk_w, stream);
+  // the logits go to the workspace when the caller keeps none: with more than 16 experts small token counts route
+  // through them
+  float* lg = logits ? logits : reinterpret_cast<float*>(ws + L.logits);
+  int rc = hmoe_route_topk(x, ldx, wr, bias, T, d, E, k, renorm, scaling, lg, topk_ids, topk_w, stream);
   if (rc != HMOE_OK) return rc;
   rc = hmoe_dispatch_tiles(topk_ids, HMOE_DT_I32, topk_w, HMOE_DT_F32, T, k, E, L.tiles_on ? x : nullptr,
                            L.tiles_on ? ldx : 0, L.tiles_on ? d : 0, nullptr, tiles, counts, nullptr, starts, order,

@@ -678,6 +678,133 @@ __global__ __launch_bounds__(256) void route_topk_direct_kernel(const uint16_t* 
   }
 }
 
+// Both routers for E > 16 (the sigmoid router for any E) at small token counts, in two launches over the caller's
+// (T, E) logits / scores buffer.  route_block_logits_kernel: a workgroup per (16-token tile, 16-expert block), its
+// four waves running the four partial chains (wave c: blocks c, c + 4, ...; operands straight into registers as in
+// route_topk_direct_kernel), the chain sums added in LDS as (c0 + c1) + (c2 + c3), the logits (no bias) stored.
+// route_select_kernel then selects as route_mfma_kernel does (four tokens per wave for the sigmoid router, one per
+// wave for the softmax router), writing the scores / biased logits over what it read.  route_mfma_kernel stages a
+// tile's rows once in LDS for all experts, so with few tokens it runs on a few CUs, each walking the whole row with a
+// barrier per 128-element chunk; here the tiles x blocks workgroups spread over the chip.
+__global__ __launch_bounds__(256) void route_block_logits_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                 const uint16_t* __restrict__ wr, int T, int d,
+                                                                 int E, float* __restrict__ out) {
+#pragma clang fp contract(off)
+  __shared__ float part[4][16 * 16];
+  const int lane = threadIdx.x & 63, r = lane & 15, q = lane >> 4;
+  const int c = threadIdx.x >> 6;  // the chain this wave runs
+  const int t0 = blockIdx.x * 16, e0 = blockIdx.y * 16;
+  const int nbf = d / 64;
+  const int nj = nbf > c ? (nbf - c + 3) >> 2 : 0;  // whole blocks c, c + 4, ...
+  const uint16_t* xr = x + (int64_t)min(t0 + r, T - 1) * ldx + 16 * q;
+  const uint16_t* wrow = wr + (int64_t)(e0 + r < E ? e0 + r : 0) * d + 16 * q;
+  auto load = [&](int b, uint4 (&xv)[2], uint4 (&wv)[2]) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      xv[h] = *reinterpret_cast<const uint4*>(xr + 64 * b + 8 * h);
+      wv[h] = *reinterpret_cast<const uint4*>(wrow + 64 * b + 8 * h);
+    }
+  };
+  auto widen = [&](const uint4 (&xv)[2], const uint4 (&wv)[2], float (&a)[16], float (&w)[16]) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t xw[4] = {xv[h].x, xv[h].y, xv[h].z, xv[h].w};
+      const uint32_t ww[4] = {wv[h].x, wv[h].y, wv[h].z, wv[h].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[8 * h + 2 * i] = bf_lo(xw[i]);
+        a[8 * h + 2 * i + 1] = bf_hi(xw[i]);
+        w[8 * h + 2 * i] = bf_lo(ww[i]);
+        w[8 * h + 2 * i + 1] = bf_hi(ww[i]);
+      }
+    }
+  };
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto products = [&](const float (&a)[16], const float (&w)[16]) {
+#pragma unroll
+    for (int s2 = 0; s2 < 16; ++s2) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s2], w[s2], acc, 0, 0, 0);
+  };
+  if (nj > 0) {
+    uint4 xs[kRdPF][2], ws[kRdPF][2];
+#pragma unroll
+    for (int p = 0; p < kRdPF; ++p) load(c + 4 * min(p, nj - 1), xs[p], ws[p]);
+    for (int j0 = 0; j0 < nj; j0 += kRdPF) {
+#pragma unroll
+      for (int p = 0; p < kRdPF; ++p) {
+        const int j = j0 + p;
+        float a[16], w[16];
+        widen(xs[p], ws[p], a, w);
+        load(c + 4 * min(j + kRdPF, nj - 1), xs[p], ws[p]);
+        if (j < nj) products(a, w);
+      }
+    }
+  }
+  if ((d & 63) && c == (nbf & 3)) {  // the partial block, as in route_topk_direct_kernel
+    uint4 xv[2], wv[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const bool in = 64 * nbf + 16 * q + 8 * h < d;
+      const int off = in ? 64 * nbf + 8 * h : -16 * q;
+      const uint4 xl = *reinterpret_cast<const uint4*>(xr + off), wl = *reinterpret_cast<const uint4*>(wrow + off);
+      xv[h] = in ? xl : make_uint4(0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u);
+      wv[h] = in ? wl : make_uint4(0, 0, 0, 0);
+    }
+    float a[16], w[16];
+    widen(xv, wv, a, w);
+    products(a, w);
+  }
+  // lane l holds tokens 4 (l / 16) + i of expert e0 + l % 16
+#pragma unroll
+  for (int i = 0; i < 4; ++i) part[c][(4 * q + i) * 16 + r] = acc[i];
+  __syncthreads();
+  const int tok = threadIdx.x >> 4, e = threadIdx.x & 15;  // one (token, expert) of the tile per thread
+  if (t0 + tok < T && e0 + e < E) {
+    const int o = tok * 16 + e;
+    out[(int64_t)(t0 + tok) * E + e0 + e] =
+        __fadd_rn(__fadd_rn(part[0][o], part[1][o]), __fadd_rn(part[2][o], part[3][o]));
+  }
+}
+
+template <bool SIG, int EPS>
+__global__ __launch_bounds__(256) void route_select_kernel(const float* __restrict__ bias, int T, int E, int k,
+                                                           int renorm, float scaling, float* __restrict__ lgbuf,
+                                                           int32_t* __restrict__ ids, float* __restrict__ wout,
+                                                           int n_group, int topk_group) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if constexpr (SIG) {
+    // four tokens per wave: segment q takes one token, lane j of it experts i * 16 + j
+    const int r = lane & 15;
+    const int64_t t = ((int64_t)blockIdx.x * 4 + wave) * 4 + (lane >> 4);
+    if (((int64_t)blockIdx.x * 4 + wave) * 4 >= T) return;  // a whole wave past T
+    const bool live = t < T;
+    float lg[EPS], bsv[EPS];
+#pragma unroll
+    for (int i = 0; i < EPS; ++i) {
+      const int e = i * 16 + r;
+      lg[i] = live && e < E ? lgbuf[t * E + e] : 0.0f;
+      bsv[i] = bias && e < E ? bias[e] : 0.0f;
+    }
+    route_select_sig16<EPS>(lg, bsv, bias != nullptr, t, live, lane, E, k, scaling, lgbuf, ids, wout, n_group,
+                            topk_group);
+  } else {
+    // softmax: one token per wave, lane l holding experts l, l + 64, ... (bias added to the logit)
+    const int t = blockIdx.x * 4 + wave;
+    if (t >= T) return;
+    float lg[kRouteEPL];
+#pragma unroll
+    for (int i = 0; i < kRouteEPL; ++i) {
+      const int e = i * 64 + lane;
+      lg[i] = -__builtin_inff();
+      if (e < E) {
+        lg[i] = lgbuf[(int64_t)t * E + e];
+        if (bias) lg[i] = __fadd_rn(lg[i], bias[e]);
+      }
+    }
+    route_select(lg, t, lane, E, k, renorm, scaling, lgbuf, ids, wout);
+  }
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // Dispatch: stable counting sort of flat ids.  Pass 1 (one wave per block of kFPB flat rows): per-block expert
 // histogram and the stable rank of each flat row among earlier rows of the same expert inside its block (wave
@@ -1706,6 +1833,38 @@ static int mfma_route_launch(int grid, hipStream_t s, const uint16_t* x, int64_t
   return HMOE_OK;
 }
 
+// Up to this many (token, expert) logits, given a logits / scores buffer, the routers with E > 16 (the sigmoid
+// router for any E) take the two-launch form (route_block_logits_kernel + route_select_kernel).  Same-process A/Bs
+// against route_mfma_kernel: sigmoid E = 128 at 64 / 512 / 2048 / 4096 tokens 20.1 / 20.5 / 36.2 / 59.0 against
+// 40.1 / 40.7 / 40.8 / 42.8 us, E = 256 at 333 tokens 33.8 against 60.2; softmax E = 64 at 256 / 2048 / 4096 / 16384
+// tokens 14.1 / 16.2 / 25.7 / 104.8 against 36.2 / 26.7 / 27.2 / 68.2.
+constexpr int64_t kRouteBlockTE = 1 << 18;
+
+// the two-launch form: block logits into lgbuf, then the selection over it
+template <bool SIG>
+static int block_route_launch(hipStream_t s, const uint16_t* x, int64_t ldx, const uint16_t* wr, const float* bias,
+                              int T, int d, int E, int k, int renorm, float scaling, float* lgbuf, int32_t* ids,
+                              float* w, int n_group, int topk_group) {
+  hipLaunchKernelGGL(route_block_logits_kernel, dim3((unsigned)((T + 15) / 16), (unsigned)((E + 15) / 16)),
+                     dim3(256), 0, s, x, ldx, wr, T, d, E, lgbuf);
+  HMOE_CHECK_LAUNCH();
+  const int nwv = SIG ? (T + 3) / 4 : T;  // waves: four tokens each (sigmoid) or one
+  const dim3 grid((unsigned)((nwv + 3) / 4));
+  // the sigmoid selection holds E / 16 expert slots per lane (4, 8 or 16, as in route_mfma_kernel)
+  constexpr int EPS_MID = SIG ? 8 : 4, EPS_MAX = SIG ? 16 : 4;
+  if (!SIG || E <= 64)
+    hipLaunchKernelGGL((route_select_kernel<SIG, 4>), grid, dim3(256), 0, s, bias, T, E, k, renorm, scaling, lgbuf,
+                       ids, w, n_group, topk_group);
+  else if (E <= 128)
+    hipLaunchKernelGGL((route_select_kernel<SIG, EPS_MID>), grid, dim3(256), 0, s, bias, T, E, k, renorm, scaling,
+                       lgbuf, ids, w, n_group, topk_group);
+  else
+    hipLaunchKernelGGL((route_select_kernel<SIG, EPS_MAX>), grid, dim3(256), 0, s, bias, T, E, k, renorm, scaling,
+                       lgbuf, ids, w, n_group, topk_group);
+  HMOE_CHECK_LAUNCH();
+  return HMOE_OK;
+}
+
 // waves per 16-token tile of the E <= 16 router by token count, from same-process A/Bs at d = 1536, E = 16 (one /
 // two / four waves): 2048 tokens 17.0 / 12.3 / 11.6 us, 4096 17.0 / 12.4 / 11.6, 8192 20.5 / 12.6 / 14.9, 16384
 // 20.9 / 20.0 / 25.7, 32768 32.9 / 33.8 / 46.3
@@ -1732,6 +1891,9 @@ static int route_launch(const void* x, int64_t ldx, const void* wr, const float*
     HMOE_CHECK_LAUNCH();
     return HMOE_OK;
   }
+  if (T * E <= kRouteBlockTE && logits)
+    return block_route_launch<false>(s, xp, ldx, wp, bias, (int)T, (int)d, E, k, renorm, scaling, logits, topk_ids,
+                                     topk_w, 1, 1);
 #define HMOE_RT(NW, NB, TT)                                                                                      \
   return mfma_route_launch<NW, NB, TT, false>((int)((T + 16 * (TT) - 1) / (16 * (TT))), s, xp, ldx, wp, bias,    \
                                               (int)T, (int)d, E, k, renorm, scaling, logits, topk_ids, topk_w, 1, 1)
@@ -1919,6 +2081,9 @@ int hmoe_route_sigmoid_group(const void* x, int64_t ldx, const void* wr, const f
   const int grid = (int)((T + 16 * tt - 1) / (16 * tt));
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* wp = static_cast<const uint16_t*>(wr);
+  if (T * E <= kRouteBlockTE && scores)
+    return block_route_launch<true>(s, xp, ldx, wp, expert_bias, (int)T, (int)d, E, k, 1, scaling, scores, topk_ids,
+                                    topk_w, n_group, topk_group);
 #define HMOE_SG(NW, NB, TT)                                                                                      \
   return mfma_route_launch<NW, NB, TT, true>(grid, s, xp, ldx, wp, expert_bias, (int)T, (int)d, E, k, 1,        \
                                                     scaling, scores, topk_ids, topk_w, n_group, topk_group)

@@ -114,13 +114,14 @@ def route_topk(x: torch.Tensor, wr: torch.Tensor, k: int, bias=None, renorm=True
             raise ValueError(f"logit bias: shape {tuple(bias.shape)}, expected ({E},)")
         bias = _contig(bias.to(torch.float32), "bias")
     s = _dev_stream(x)
-    logits = torch.empty(T, E, device=x.device, dtype=torch.float32) if want_logits else None
+    # above 16 experts the logits buffer is passed even when not wanted: small token counts route through it
+    logits = torch.empty(T, E, device=x.device, dtype=torch.float32) if want_logits or E > 16 else None
     ids = torch.empty(T, k, device=x.device, dtype=torch.int32)
     w = torch.empty(T, k, device=x.device, dtype=torch.float32)
     with _Probe("route_topk"):
         L.call("hmoe_route_topk", L.ptr(x), x.stride(0), L.ptr(wr), L.ptr(bias), T, d, E, k, int(bool(renorm)),
                float(scaling), L.ptr(logits), L.ptr(ids), L.ptr(w), s)
-    return logits, ids, w
+    return (logits if want_logits else None), ids, w
 
 
 def moe_forward(x, wr, wgu, wd, k, bias=None, renorm=True, scaling=1.0, want_logits=False):
@@ -181,13 +182,15 @@ def route_sigmoid_group(x: torch.Tensor, wr: torch.Tensor, k: int, n_group: int,
             raise ValueError(f"expert bias: shape {tuple(expert_bias.shape)}, expected ({E},)")
         expert_bias = _contig(expert_bias.to(torch.float32), "expert bias")
     s = _dev_stream(x)
-    scores = torch.empty(T, E, device=x.device, dtype=torch.float32) if want_scores else None
+    # the scores buffer is passed even when not wanted: small token counts route through it (two launches that
+    # spread the work over the chip)
+    scores = torch.empty(T, E, device=x.device, dtype=torch.float32)
     ids = torch.empty(T, k, device=x.device, dtype=torch.int32)
     w = torch.empty(T, k, device=x.device, dtype=torch.float32)
     with _Probe("route_topk"):
         L.call("hmoe_route_sigmoid_group", L.ptr(x), x.stride(0), L.ptr(wr), L.ptr(expert_bias), T, d, E, k, n_group,
                topk_group, float(scaling), L.ptr(scores), L.ptr(ids), L.ptr(w), s)
-    return scores, ids, w
+    return (scores if want_scores else None), ids, w
 
 
 @dataclass
