@@ -1024,7 +1024,7 @@ __global__ __launch_bounds__(256) void dispatch_index_kernel(const void* __restr
 // plus the earlier waves' count plus its rank: the same stable counting sort, so the same outputs as the three
 // passes, with one launch instead of three.
 constexpr int kSmallRows = 8;                   // flat rows per lane
-constexpr int kSmallE = 64;                     // experts: one lane each in the scan
+constexpr int kSmallE = 256;                    // experts: four consecutive ones per lane in the scan
 constexpr int64_t kSmallM = 16 * 64 * kSmallRows;  // 8192 flat rows
 
 __global__ __launch_bounds__(1024) void dispatch_small_kernel(const void* __restrict__ ids, int ids64,
@@ -1040,7 +1040,7 @@ __global__ __launch_bounds__(1024) void dispatch_small_kernel(const void* __rest
   __shared__ int run[16][kSmallE];  // per wave and expert: its rows so far, then the earlier waves' rows
   __shared__ int st[kSmallE + 1];   // expert starts
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  for (int e = lane; e < kSmallE; e += 64) run[w][e] = 0;
+  for (int e = lane; e < E; e += 64) run[w][e] = 0;
   const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   const int64_t f0 = (int64_t)w * 64 * kSmallRows;
   int ev[kSmallRows], rk[kSmallRows];
@@ -1071,28 +1071,45 @@ __global__ __launch_bounds__(1024) void dispatch_small_kernel(const void* __rest
     __builtin_amdgcn_wave_barrier();
   }
   __syncthreads();
-  // per expert (lane e of wave 0): exclusive prefix over the waves, the total, then the starts over the experts
-  if (w == 0) {
+  // thread e: expert e's exclusive prefix over the waves and its total
+  if ((int)threadIdx.x < E) {
+    const int e = threadIdx.x;
     int tot = 0;
-    if (lane < E) {
 #pragma unroll
-      for (int ww = 0; ww < 16; ++ww) {
-        const int c = run[ww][lane];
-        run[ww][lane] = tot;
-        tot += c;
-      }
+    for (int ww = 0; ww < 16; ++ww) {
+      const int c = run[ww][e];
+      run[ww][e] = tot;
+      tot += c;
     }
-    int incl = lane < E ? tot : 0;
+    st[e] = tot;
+  }
+  __syncthreads();
+  // wave 0, lane l: the starts of experts 4 l .. 4 l + 3 (in order, after a wave prefix of the lanes' sums)
+  if (w == 0) {
+    int tot[4], lsum = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = 4 * lane + j;
+      tot[j] = e < E ? st[e] : 0;
+      lsum += tot[j];
+    }
+    int incl = lsum;
 #pragma unroll
     for (int sft = 1; sft < 64; sft <<= 1) {
       const int o = __shfl_up(incl, sft, 64);
       if (lane >= sft) incl += o;
     }
-    if (lane < E) {
-      st[lane] = incl - tot;
-      counts[lane] = tot;
-      if (counts64) counts64[lane] = tot;
-      starts[lane] = incl - tot;
+    int at = incl - lsum;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = 4 * lane + j;
+      if (e < E) {
+        st[e] = at;
+        counts[e] = tot[j];
+        if (counts64) counts64[e] = tot[j];
+        starts[e] = at;
+      }
+      at += tot[j];
     }
     if (lane == 63) {
       st[E] = incl;
