@@ -89,3 +89,21 @@ def test_moe_swiglu_no_grad_uses_one_call_with_same_result(wdt):
         a = m(h_in)
     b_ = m(h_in).detach()
     assert np.array_equal(a.float().cpu().numpy(), b_.float().cpu().numpy())
+
+
+def test_one_call_forward_under_the_bench_probe():
+    """With bench.py's event probe set, moe_forward launches the same entry points one by one (so that events can
+    sit between them) and records the probed ops; the outputs are the one-call ones."""
+    from trenowanie_generatora_obrazkow_amd import ops
+    dev = torch.device("cuda")
+    x, wr, wgu, wd = (t.to(dev) for t in make_inputs(700, 512, 40, 256, seed=11))
+    ref = ops.moe_forward(x, wr, wgu, wd, 4, want_logits=True)
+    ops.probe = {"gate_up_swiglu": [], "combine": []}
+    try:
+        got = ops.moe_forward(x, wr, wgu, wd, 4, want_logits=True)
+        torch.cuda.synchronize()
+        assert len(ops.probe["gate_up_swiglu"]) == 1 and len(ops.probe["combine"]) == 1
+    finally:
+        ops.probe = None
+    for a, b, name in zip(got, ref, ("out", "topk_ids", "topk_w", "logits")):
+        _same(a, b, name)
