@@ -20,10 +20,12 @@ def _ref_dispatch(ids_cpu, E, k):
 @pytest.mark.parametrize("T,E,k,skew", [(512, 8, 2, 0), (16384, 16, 2, 0), (16384, 16, 2, 1), (8192, 128, 8, 0),
                                         (1, 4, 2, 0), (1000, 3, 3, 1), (5000, 1024, 1, 0),
                                         (100000, 48, 2, 1),
-                                        # around the one-workgroup pass (no row copies, <= 8192 rows, E <= 256)
+                                        # around the one-workgroup pass (no row copies, E <= 256, at most 8192
+                                        # rows with E <= 16, 4096 above)
                                         (4096, 64, 2, 1), (1024, 64, 8, 0), (8193, 64, 1, 0), (1024, 65, 8, 0),
                                         (1365, 33, 6, 1), (3, 1, 1, 0), (512, 128, 8, 0), (300, 256, 8, 1),
-                                        (1024, 200, 8, 0), (1000, 257, 2, 0)])
+                                        (1024, 200, 8, 0), (1000, 257, 2, 0), (4096, 16, 2, 1), (8193, 16, 1, 0),
+                                        (512, 64, 8, 0), (4097, 64, 1, 0), (700, 17, 5, 1)])
 def test_dispatch_bitexact(oracle, T, E, k, skew):
     from trenowanie_generatora_obrazkow_amd import ops
     print(f"dispatch T={T} E={E} k={k} skew={skew}", flush=True)

@@ -1017,7 +1017,7 @@ __global__ __launch_bounds__(256) void dispatch_index_kernel(const void* __restr
 }
 
 // Small inputs without row copies (M <= kSmallM flat rows, E <= kSmallE): the three passes in one workgroup of 16
-// waves.  Wave w takes the flat rows [w C, (w + 1) C) (C = kSmallRows * 64), 64 at a time in flat order: a row's rank
+// waves.  Wave w takes the flat rows [w C, (w + 1) C) (C = 64 * ceil(M / 1024)), 64 at a time in flat order: a row's rank
 // among the wave's earlier rows of its expert comes from the wave ballots of the histogram pass (peers agree on every
 // id bit) plus the wave's running count, kept in LDS per (wave, expert).  The waves' counts are then scanned per
 // expert (wave order = flat order) and the totals over the experts, and each row's position is its expert's start
@@ -1042,16 +1042,18 @@ __global__ __launch_bounds__(1024) void dispatch_small_kernel(const void* __rest
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   for (int e = lane; e < E; e += 64) run[w][e] = 0;
   const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  const int64_t f0 = (int64_t)w * 64 * kSmallRows;
+  const int steps = (int)((M + 1023) / 1024);  // 64-row steps per wave (at most kSmallRows)
+  const int64_t f0 = (int64_t)w * 64 * steps;
   int ev[kSmallRows], rk[kSmallRows];
 #pragma unroll
   for (int i = 0; i < kSmallRows; ++i) {
     const int64_t f = f0 + i * 64 + lane;
-    ev[i] = f < M ? load_id(ids, ids64, f) : -1;
+    ev[i] = i < steps && f < M ? load_id(ids, ids64, f) : -1;
   }
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < kSmallRows; ++i) {
+    if (i >= steps) break;  // wave-uniform
     const int e = ev[i];
     const bool valid = e >= 0 && e < E;
     uint64_t peers = __ballot(valid);
@@ -1121,7 +1123,7 @@ __global__ __launch_bounds__(1024) void dispatch_small_kernel(const void* __rest
 #pragma unroll
   for (int i = 0; i < kSmallRows; ++i) {
     const int64_t f = f0 + i * 64 + lane;
-    if (f >= M) break;
+    if (i >= steps || f >= M) break;
     const int e = ev[i];
     const int64_t pos = (e >= 0 && e < E) ? (int64_t)st[e] + run[w][e] + rk[i] : -1;
     if (pos >= 0) {
@@ -1981,7 +1983,9 @@ static int dispatch_impl(const void* topk_ids, int ids_dtype, const void* topk_w
   int nbits = 0;
   while ((1 << nbits) < E) ++nbits;
   const int ids64 = ids_dtype == HMOE_DT_I64;
-  if (!xs && !xs_tiles && M <= kSmallM && E <= kSmallE) {
+  // the one-workgroup pass up to 8192 rows with E <= 16, 4096 above (kernel time at 8192 rows and 64 or 128
+  // experts: 16.3 and 18.9 us, the three passes about 14)
+  if (!xs && !xs_tiles && M <= (E <= 16 ? kSmallM : kSmallM / 2) && E <= kSmallE) {
     hipLaunchKernelGGL(dispatch_small_kernel, dim3(1), dim3(1024), 0, s, topk_ids, ids64, topk_w, w_dtype, (int)f16,
                        M, k, E, nbits, counts, counts64, starts, order, a_idx, inv_pos, w_sorted, n_invalid);
     HMOE_CHECK_LAUNCH();
