@@ -2,7 +2,6 @@
 against something independent of its own formula -- the mathematics (closed forms, brute force, invariants), torch's
 own routines (softmax/topk, argsort/bincount, _grouped_mm, autograd), hand-derived known answers, and the golden
 fixtures in tests/golden/.  CPU only."""
-import math
 from itertools import combinations
 
 import numpy as np
