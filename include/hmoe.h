@@ -229,6 +229,24 @@ int hmoe_moe_forward(const void* x, int64_t ldx, const void* wr, const float* bi
                      int32_t* topk_ids, float* topk_w, float* logits, void* workspace, size_t workspace_bytes,
                      hmoe_stream_t stream);
 
+/* The expert part of the routed forward in one call, for routing decided by the model's own gate: replaces
+ * aurora/hf_compat.py:69-81 (sort, gather, grouped gate/up, act * up, grouped down with weight and scatter) for a
+ * silu block.  It runs hmoe_dispatch_tiles, then hmoe_gate_up_swiglu_tiles (16-bit weights, h >= 4096, tiles below
+ * 2^31 bytes), hmoe_gate_up_swiglu_i8 (w_dtype HMOE_DT_I8, scales wgu_s / wd_s as in the _i8 entry points) or
+ * hmoe_gate_up_swiglu (rows gathered through a_idx), then hmoe_down_scatter(_i8), with the sort arrays, tiles and act
+ * in the workspace, so y, inv_pos and n_invalid are what those calls give one by one.  topk_ids / topk_w as
+ * hmoe_dispatch; 16-bit weights have the activations' type dtype (bf16 or fp16).  Outputs: y (T * k, d) of dtype in
+ * (token, slot) order (rows of slots routed nowhere are not written), inv_pos (T * k,) int32 (negative for those
+ * slots; hmoe_combine with it reads them as zeros), n_invalid (1,) int32.  workspace:
+ * hmoe_moe_experts_workspace_size(T, d, E, k, h, w_dtype, dtype) bytes, 256-byte aligned.  Limits as the entry points
+ * it runs. */
+size_t hmoe_moe_experts_workspace_size(int64_t T, int64_t d, int E, int k, int64_t h, int w_dtype, int dtype);
+int hmoe_moe_experts(const void* x, int64_t ldx, const void* topk_ids, int ids_dtype, const void* topk_w,
+                     int topk_w_dtype, const void* wgu, const void* wgu_s, int wgu_s_dtype, const void* wd,
+                     const void* wd_s, int wd_s_dtype, int w_dtype, int64_t T, int64_t d, int E, int k, int64_t h,
+                     void* y, int32_t* inv_pos, int32_t* n_invalid, void* workspace, size_t workspace_bytes,
+                     int dtype, hmoe_stream_t stream);
+
 /* ---------------------------------------------------------------------------------------------------------------
  * Backward.  The reference has no backward for this path (aurora/hf_compat.py:62 is @torch.no_grad); each entry
  * point below differentiates the forward line it names.

@@ -107,3 +107,43 @@ def test_one_call_forward_under_the_bench_probe():
         ops.probe = None
     for a, b, name in zip(got, ref, ("out", "topk_ids", "topk_w", "logits")):
         _same(a, b, name)
+
+
+@pytest.mark.parametrize("T,d,E,k,h,wdt,bad", [(64, 2048, 128, 8, 320, "int8", False), (700, 520, 12, 3, 264, "bf16", True),
+                                               (300, 1536, 16, 2, 4096, "bf16", False), (500, 256, 8, 2, 512, "fp16", False),
+                                               (1, 256, 4, 2, 64, "int8", True), (0, 256, 4, 2, 64, "bf16", False)])
+def test_one_call_experts_matches_op_by_op(T, d, E, k, h, wdt, bad):
+    """hmoe_moe_experts (ops.moe_experts) against routed_gate_up + down_scatter on the same routing: y on the routed
+    rows, inv_pos and n_invalid bit-identical, for bf16, fp16 and int8 experts, the row-group tiles (h = 4096), ids
+    outside [0, E) and an empty input."""
+    from trenowanie_generatora_obrazkow_amd import ops
+    from trenowanie_generatora_obrazkow_amd.hf_compat import _quant_int8
+    print(f"moe_experts T={T} d={d} E={E} k={k} h={h} {wdt} bad={bad}", flush=True)
+    dev = torch.device("cuda")
+    g = torch.Generator().manual_seed(T + E + h)
+    act_dt = torch.float16 if wdt == "fp16" else torch.bfloat16
+    x = torch.randn(T, d, generator=g).to(act_dt).to(dev)
+    ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).int() if T else torch.zeros(0, k).int()
+    if bad and T:
+        ids.view(-1)[0] = E + 3
+    ids = ids.to(dev)
+    tw = torch.rand(T, k, generator=g).to(dev)
+    wgu = torch.randn(E, d, 2 * h, generator=g) * 0.02
+    wd = torch.randn(E, h, d, generator=g) * 0.02
+    wgu_s = wd_s = None
+    if wdt == "int8":
+        (wgu, wgu_s), (wd, wd_s) = _quant_int8(wgu), _quant_int8(wd)
+        wgu_s, wd_s = wgu_s.to(dev), wd_s.to(dev)
+    else:
+        wgu, wd = wgu.to(act_dt), wd.to(act_dt)
+    wgu, wd = wgu.to(dev), wd.to(dev)
+    disp, act, _ = ops.routed_gate_up(x, ids, E, wgu, topk_w=tw, wgu_s=wgu_s, want_inv=True)
+    y_ref, _ = ops.down_scatter(act, wd, disp.counts, T * k, disp.w_sorted, disp.order, wd_s=wd_s)
+    y, inv, n_inv = ops.moe_experts(x, ids, tw, wgu, wd, wgu_s=wgu_s, wd_s=wd_s)
+    torch.cuda.synchronize()
+    _same(inv, disp.inv_pos, "inv_pos")
+    _same(n_inv, disp.n_invalid, "n_invalid")
+    routed = inv.long() >= 0  # slots routed nowhere leave their y rows unwritten
+    _same(y[routed], y_ref[routed], "y")
+    out = ops.combine(y, T, k, inv_pos=inv)
+    _same(out, ops.combine(y_ref, T, k, inv_pos=disp.inv_pos), "combined")

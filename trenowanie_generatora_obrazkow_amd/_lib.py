@@ -47,6 +47,9 @@ SIGNATURES = {
     "hmoe_down_scatter_i8": (_I32, [_P, _P, _P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P, _I32, _P]),
     "hmoe_combine": (_I32, [_P, _P, _I64, _I32, _I64, _P, _I32, _P]),
     "hmoe_moe_forward_workspace_size": (_SZ, [_I64, _I64, _I32, _I32, _I64]),
+    "hmoe_moe_experts_workspace_size": (_SZ, [_I64, _I64, _I32, _I32, _I64, _I32, _I32]),
+    "hmoe_moe_experts": (_I32, [_P, _I64, _P, _I32, _P, _I32, _P, _P, _I32, _P, _P, _I32, _I32, _I64, _I64, _I32,
+                                _I32, _I64, _P, _P, _P, _P, _SZ, _I32, _P]),
     "hmoe_moe_forward": (_I32, [_P, _I64, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I64, _I32, _F32, _P, _P, _P, _P,
                                 _P, _SZ, _P]),
     "hmoe_combine_add": (_I32, [_P, _P, _I64, _I32, _I64, _P, _P, _I32, _P]),

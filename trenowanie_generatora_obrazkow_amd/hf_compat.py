@@ -31,9 +31,9 @@ def _fused_moe_infer(self, x, topk_ids, topk_weight):
     x = x.contiguous() if dp == d else torch.nn.functional.pad(x, (0, dp - d))  # stacks padded by fuse_moe
     M = n * k
     if _is_silu(self._act):
-        disp, act, _ = ops.routed_gate_up(x, topk_ids.contiguous(), E, self._wgu, topk_w=topk_weight.contiguous(),
-                                          wgu_s=self._wgu_s, want_inv=True)
-        y, _ = ops.down_scatter(act, self._wd, disp.counts, M, disp.w_sorted, disp.order, wd_s=self._wd_s)
+        # dispatch, both fused projections, routing weight and scatter in one C call
+        y, inv_pos, self._n_invalid = ops.moe_experts(x, topk_ids.contiguous(), topk_weight.contiguous(), self._wgu,
+                                                      self._wd, wgu_s=self._wgu_s, wd_s=self._wd_s)
     else:
         # any other activation: the module's own act_fn between the two grouped GEMMs, as the reference's fused
         # branch applies it (aurora/hf_compat.py:79-81); gathered rows in, routing weight and scatter in the down GEMM
@@ -41,8 +41,8 @@ def _fused_moe_infer(self, x, topk_ids, topk_weight):
         g, u = ops.grouped_mm(x, self._wgu, disp.counts, M, a_idx=disp.a_idx, w_scale=self._wgu_s).chunk(2, dim=-1)
         y = ops.grouped_mm((self._act(g) * u).contiguous(), self._wd, disp.counts, M, y_idx=disp.order,
                            scale=disp.w_sorted, w_scale=self._wd_s)
-    self._n_invalid = disp.n_invalid
-    out = ops.combine(y, n, k, inv_pos=disp.inv_pos)
+        self._n_invalid, inv_pos = disp.n_invalid, disp.inv_pos
+    out = ops.combine(y, n, k, inv_pos=inv_pos)
     return out if dp == d else out[:, :d].contiguous()
 
 

@@ -169,6 +169,51 @@ def moe_forward(x, wr, wgu, wd, k, bias=None, renorm=True, scaling=1.0, want_log
 _FWD_OPS = ("route_topk", "dispatch", "gate_up_swiglu", "down_scatter", "combine")
 
 
+def moe_experts(x, ids, tw, wgu, wd, wgu_s=None, wd_s=None):
+    """The expert part of a forward whose routing the caller's gate decided, in one C call (hmoe_moe_experts):
+    routed_gate_up (with inv_pos) and down_scatter with the same outputs.  x (T, d) bf16 or fp16 with contiguous rows;
+    ids (T, k) int32 / int64; tw (T, k); wgu (E, d, 2h) and wd (E, h, d) of x's type, or int8 with scales wgu_s
+    (E, 2h) and wd_s (E, d) -> (y (T*k, d) in (token, slot) order, inv_pos (T*k,) int32, n_invalid (1,) int32); the
+    combine (with inv_pos) sums y over the slots."""
+    T, k = ids.shape
+    if probe is not None and any(n in probe for n in _FWD_OPS):
+        # event timing of single ops (bench.py's probe): the same entry points one by one
+        disp, act, _ = routed_gate_up(x, ids, wgu.shape[0], wgu, topk_w=tw, wgu_s=wgu_s, want_inv=True)
+        y, _ = down_scatter(act, wd, disp.counts, T * k, disp.w_sorted, disp.order, wd_s=wd_s)
+        return y, disp.inv_pos, disp.n_invalid
+    if x.dim() != 2 or x.shape[0] != T or x.stride(1) != 1:
+        raise ValueError(f"x must be a ({T}, d) matrix with contiguous rows (got {tuple(x.shape)})")
+    dt = _act_dtype(x, "x")
+    d = x.shape[1]
+    if wgu.dim() != 3 or wd.dim() != 3 or wgu.dtype not in (x.dtype, torch.int8) or wd.dtype != wgu.dtype:
+        raise TypeError(f"wgu (E, d, 2h) and wd (E, h, d) of x's type or int8 expected (got {wgu.dtype}, {wd.dtype})")
+    E, h = wgu.shape[0], wd.shape[1]
+    L.require_gpu(x, "x")
+    _need(ids, "topk_ids", (T, k), (torch.int32, torch.int64))
+    if tuple(tw.shape) != (T, k):
+        raise ValueError(f"topk_weight: shape {tuple(tw.shape)}, expected {(T, k)}")
+    tw = _contig(tw if tw.dtype in (torch.float32, torch.bfloat16, torch.float16) else tw.float(), "topk_weight")
+    _need(wgu, "wgu", (E, d, 2 * h), (wgu.dtype,))
+    _need(wd, "wd", (E, h, d), (wd.dtype,))
+    wgu_s = _w_scale(wgu, wgu_s, 2 * h)
+    wd_s = _w_scale(wd, wd_s, d)
+    w_dt = L.dt(wgu)
+    lib = L.lib()
+    ws_bytes = lib.hmoe_moe_experts_workspace_size(T, d, E, k, h, w_dt, dt)
+    if ws_bytes == 0:
+        raise ValueError(f"moe_experts: unsupported sizes T={T} d={d} E={E} k={k} h={h}")
+    dev = x.device
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+    y = torch.empty(T * k, d, device=dev, dtype=x.dtype)
+    inv = torch.empty(T * k, device=dev, dtype=torch.int32)
+    n_invalid = torch.empty(1, device=dev, dtype=torch.int32)
+    L.call("hmoe_moe_experts", L.ptr(x), x.stride(0), L.ptr(ids), L.dt(ids), L.ptr(tw), L.dt(tw), L.ptr(wgu),
+           L.ptr(wgu_s), L.dt(wgu_s) if wgu_s is not None else 0, L.ptr(wd), L.ptr(wd_s),
+           L.dt(wd_s) if wd_s is not None else 0, w_dt, T, d, E, k, h, L.ptr(y), L.ptr(inv), L.ptr(n_invalid),
+           L.ptr(ws), ws_bytes, dt, _dev_stream(x))
+    return y, inv, n_invalid
+
+
 def route_sigmoid_group(x: torch.Tensor, wr: torch.Tensor, k: int, n_group: int, topk_group: int, expert_bias=None,
                         scaling=1.0, want_scores=False):
     """BailingMoeV2 sigmoid, group-limited router -> (scores (T, E) fp32 or None, topk_ids (T, k) int32,

@@ -148,9 +148,8 @@ class PoziomkaMoE(nn.Module):
             x2.record_stream(side)
         _, ids, w = ops.route_sigmoid_group(x2, gw, k, self.n_group, self.topk_group, expert_bias=gb,
                                             scaling=self.scaling)
-        disp, act, _ = ops.routed_gate_up(x2, ids, E, self._wgu, topk_w=w, wgu_s=self._wgu_s, want_inv=False)
-        M = T * k
-        y, _ = ops.down_scatter(act, self._wd, disp.counts, M, disp.w_sorted, disp.order, wd_s=self._wd_s)
+        # dispatch, both int8 projections, routing weight and scatter in one C call
+        y, _, _ = ops.moe_experts(x2, ids, w, self._wgu, self._wd, wgu_s=self._wgu_s, wd_s=self._wd_s)
         if side is not None:  # join before the combine reads the shared output
             main.wait_stream(side)
             shared.record_stream(main)
