@@ -140,6 +140,19 @@ def test_argument_validation_codes(lib):
     assert fwd(P, 4, 64, 8, 2, 60, P, L.hmoe_moe_forward_workspace_size(4, 64, 8, 2, 60)) == -2
     assert fwd(P, 4, 64, 8, 9, 64, P, ws) == -1
     assert fwd(P, 0, 64, 8, 2, 64, None, 0) == 0
+    # one-call experts: workspace, int8 weights without scales, a 16-bit weight type other than the activations',
+    # widths off the int8 granule, misaligned workspace
+    BF, F16, I8, I32_, F32 = 0, 1, 5, 3, 2
+    wse = L.hmoe_moe_experts_workspace_size(4, 64, 8, 2, 64, BF, BF)
+    exp = lambda wdt, h, wgu_s, wd_s, ws_ptr, ws_b, dt=BF: L.hmoe_moe_experts(
+        P, 64, P, I32_, P, F32, P, wgu_s, BF, P, wd_s, BF, wdt, 4, 64, 8, 2, h, P, P, P, ws_ptr, ws_b, dt, None)
+    assert exp(BF, 64, None, None, P, wse - 1) == -5
+    assert exp(I8, 64, None, None, P, L.hmoe_moe_experts_workspace_size(4, 64, 8, 2, 64, I8, BF)) == -1
+    assert exp(F16, 64, None, None, P, wse) == -3
+    assert exp(I8, 40, P, P, P, L.hmoe_moe_experts_workspace_size(4, 64, 8, 2, 40, I8, BF)) == -2
+    assert exp(BF, 64, None, None, P + 64, wse) == -1
+    assert exp(BF, 64, None, None, P, wse, dt=F32) == -3
+    assert L.hmoe_moe_experts_workspace_size(-1, 64, 8, 2, 64, BF, BF) == 0
 
 
 def test_workspace_queries(lib):
