@@ -25,6 +25,18 @@ def side_stream(device: torch.device):
     return _SIDE_STREAMS[key]
 
 
+_SIDE_EVENTS = {}  # device index -> (fork, join) events, reused by every fork to and join from the side stream
+
+
+def side_events(device: torch.device):
+    """A (fork, join) pair of events per device for forking work onto the side stream and joining it back: recorded
+    and waited on in stream order, so one pair serves every fork (wait_stream would make a new event each time)."""
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    if key not in _SIDE_EVENTS:
+        _SIDE_EVENTS[key] = (torch.cuda.Event(), torch.cuda.Event())
+    return _SIDE_EVENTS[key]
+
+
 # Optional event probe: when `probe` is set to {op name: list}, each listed op records a (start, end) pair of
 # torch.cuda.Events on the stream its kernels are launched on (the current stream) around its C call.
 probe = None

@@ -61,11 +61,32 @@ class _StackedMLP:
         return self.wgu, self.wd
 
 
+_ROW_COUNTS = {}  # device index -> int32 arange, entry T = T
+_OLD_ROW_COUNTS = []  # outgrown aranges, never freed: kernels on any stream may still read them
+
+
+def _one_count(T: int, device: torch.device) -> torch.Tensor:
+    """(1,) int32 on `device` holding T, the row count of a one-expert grouped GEMM: a view of a cached arange (no
+    launch per call), grown by doubling; while a graph is being captured and the arange is too short, a fill kernel
+    instead (allocations made under capture belong to the graph)."""
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    ar = _ROW_COUNTS.get(key)
+    if ar is None or ar.numel() <= T:
+        if torch.cuda.is_current_stream_capturing():
+            return torch.full((1,), T, dtype=torch.int32, device=device)
+        if ar is not None:
+            _OLD_ROW_COUNTS.append(ar)
+        ar = torch.arange(max(1024, 1 << T.bit_length()), dtype=torch.int32, device=device)
+        torch.cuda.current_stream(device).synchronize()  # complete before any stream reads it
+        _ROW_COUNTS[key] = ar
+    return ar[T:T + 1]
+
+
 def _dense_swiglu(x2: torch.Tensor, wgu: torch.Tensor, wd: torch.Tensor) -> torch.Tensor:
     """bf16(bf16(silu(bf16(x Wg))) * bf16(x Wu)) Wd rounded to bf16 -- F.linear / F.silu in bf16 (aurora/
     hf_pipeline.py:322) -- for x2 (T, d) bf16."""
     T = x2.shape[0]
-    one = torch.full((1,), T, dtype=torch.int32, device=x2.device)  # a fill kernel: no host-device copy
+    one = _one_count(T, x2.device)
     act, _ = ops.gate_up_swiglu(x2, wgu, one, T)
     y, _ = ops.down_scatter(act, wd, one, T, None, None)
     return y
@@ -142,7 +163,9 @@ class PoziomkaMoE(nn.Module):
         side = ops.side_stream(x2.device) if self.overlap_shared and T > 0 else None
         if side is not None:  # fork: the shared expert needs only x
             main = torch.cuda.current_stream(x2.device)
-            side.wait_stream(main)
+            fork_ev, join_ev = ops.side_events(x2.device)
+            fork_ev.record(main)
+            side.wait_event(fork_ev)
             with torch.cuda.stream(side):
                 shared = _dense_swiglu(x2, wgu_sh, wd_sh)
             x2.record_stream(side)
@@ -151,7 +174,8 @@ class PoziomkaMoE(nn.Module):
         # dispatch, both int8 projections, routing weight and scatter in one C call
         y, _, _ = ops.moe_experts(x2, ids, w, self._wgu, self._wd, wgu_s=self._wgu_s, wd_s=self._wd_s)
         if side is not None:  # join before the combine reads the shared output
-            main.wait_stream(side)
+            join_ev.record(side)
+            main.wait_event(join_ev)
             shared.record_stream(main)
         else:
             shared = _dense_swiglu(x2, wgu_sh, wd_sh)
