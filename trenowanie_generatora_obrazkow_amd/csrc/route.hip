@@ -1292,13 +1292,25 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
       }
     };
     const uint4 a = add ? reinterpret_cast<const uint4*>(add + t * d)[c] : make_uint4(0, 0, 0, 0);
+    // the row is loaded whether or not its slot was routed (every slot's row lies inside y), and a slot routed
+    // nowhere is zeroed afterwards: the row loads do not wait for inv_pos
     auto row = [&](int j) {
-      return (inv_pos && inv_pos[t * k + j] < 0) ? make_uint4(0, 0, 0, 0) : src[j * nvec];
+      const uint4 v = src[j * nvec];
+      return (inv_pos && inv_pos[t * k + j] < 0) ? make_uint4(0, 0, 0, 0) : v;
     };
     if constexpr (KT > 0) {
+      // every row load is issued before any inv_pos value is waited for
       uint4 v[KT];
 #pragma unroll
-      for (int j = 0; j < KT; ++j) v[j] = row(j);
+      for (int j = 0; j < KT; ++j) v[j] = src[j * nvec];
+      if (inv_pos) {
+        int iv[KT];
+#pragma unroll
+        for (int j = 0; j < KT; ++j) iv[j] = inv_pos[t * k + j];
+#pragma unroll
+        for (int j = 0; j < KT; ++j)
+          if (iv[j] < 0) v[j] = make_uint4(0, 0, 0, 0);
+      }
       first(v[0]);
 #pragma unroll
       for (int j = 1; j < KT; ++j) accum(v[j]);
