@@ -1017,13 +1017,13 @@ __global__ __launch_bounds__(256) void dispatch_index_kernel(const void* __restr
 }
 
 // Small inputs without row copies (M <= kSmallM flat rows, E <= kSmallE): the three passes in one workgroup of 16
-// waves.  Wave w takes the flat rows [w C, (w + 1) C) (C = 64 * ceil(M / 1024)), 64 at a time in flat order: a row's rank
-// among the wave's earlier rows of its expert comes from the wave ballots of the histogram pass (peers agree on every
-// id bit) plus the wave's running count, kept in LDS per (wave, expert).  The waves' counts are then scanned per
-// expert (wave order = flat order) and the totals over the experts, and each row's position is its expert's start
-// plus the earlier waves' count plus its rank: the same stable counting sort, so the same outputs as the three
+// waves.  Wave w takes the flat rows [w C, (w + 1) C) (C = 64 ceil(M / 1024)), 64 at a time in flat order: a row's
+// rank among the wave's earlier rows of its expert comes from the wave ballots of the histogram pass (peers agree on
+// every id bit) plus the wave's running count, kept in LDS per (wave, expert).  The waves' counts are then scanned
+// per expert (wave order = flat order) and the totals over the experts, and each row's position is its expert's
+// start plus the earlier waves' count plus its rank: the same stable counting sort, so the same outputs as the three
 // passes, with one launch instead of three.
-constexpr int kSmallRows = 8;                   // flat rows per lane
+constexpr int kSmallRows = 8;                   // flat rows per lane at most
 constexpr int kSmallE = 256;                    // experts: four consecutive ones per lane in the scan
 constexpr int64_t kSmallM = 16 * 64 * kSmallRows;  // 8192 flat rows
 
