@@ -75,11 +75,11 @@ int hmoe_route_topk(const void* x, int64_t ldx, const void* wr, const float* bia
 /* Sigmoid, group-limited top-k router of BailingMoeV2: replaces the routing of aurora/hf_pipeline.py:352-359
  * (PoziomkaMoE.forward).  Logits in fp32, each the fixed-order sum of hmoe_route_topk (no bias in them);
  * score = 1 / (1 + exp(-logit)) (the exp of the softmax router, IEEE division); routing = score + expert_bias (fp32,
- * NULL = 0) for selection only; the experts form n_group groups of E / n_group, a group's value is the sum of its two largest
- * routing values, the topk_group best groups are kept (ties to the lower group) and the k best experts among them
- * selected (descending, ties to the lower expert); topk_w = selected scores / (their sum in slot order + 1e-20) *
- * scaling.  scores (T, E) fp32 receives the sigmoid scores (NULL to skip; for T * E <= 2^18 the logits pass through
- * it as in hmoe_route_topk, so passing it is faster for small inputs).  E % n_group == 0; unless
+ * NULL = 0) for selection only; the experts form n_group groups of E / n_group, a group's value is the sum of its two
+ * largest routing values, the topk_group best groups are kept (ties to the lower group) and the k best experts among
+ * them selected (descending, ties to the lower expert); topk_w = selected scores / (their sum in slot order + 1e-20)
+ * * scaling.  scores (T, E) fp32 receives the sigmoid scores (NULL to skip; for T * E <= 2^18 the logits pass
+ * through it as in hmoe_route_topk, so passing it is faster for small inputs).  E % n_group == 0; unless
  * topk_group >= n_group (every group kept), E / n_group is a power of two in [2, 64] and k <= topk_group *
  * E / n_group.  Other limits as hmoe_route_topk. */
 int hmoe_route_sigmoid_group(const void* x, int64_t ldx, const void* wr, const float* expert_bias, int64_t T,
