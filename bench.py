@@ -76,7 +76,7 @@ def zipf_bias(E, seed=0, s=1.2, n_empty=2):
     return b
 
 
-PROBE_STRIDE = 4
+PROBE_STRIDE = 8
 
 
 def time_steps(step, steps, warmup, graph, probe_kernel, probe_every=1, probe_first=0):
