@@ -1068,7 +1068,14 @@ static int launch_fwd(const GemmParams& p, int64_t ncols, bool f16, hipStream_t 
 template <int EPI, bool F16 = false>
 static int launch_mgroup_i8_t(const GemmParams& p, int64_t ncols, hipStream_t s) {
   const int64_t tl = mgroup_tiles<CfgL8, EPI>(p.M, p.E, ncols);
-  if (pick_large_mgroup<EPI>(tl, ncols, p.K, true)) return launch<CfgL8, MGROUP, false, true, EPI, false, F16>(p, tl, s);
+  bool large = pick_large_mgroup<EPI>(tl, ncols, p.K, true);
+  // gate/up with many experts (E >= 128): the tile bound counts a partial tile per expert, and below 3.25 large
+  // tiles per CU by it the small tiles ran faster (E = 128, h = 320, top-8, 4096 tokens, bound 3.0: gate/up 186 ->
+  // 166 us, the BailingMoeV2 block 407 -> 379 us).  At 5120 tokens (3.375) the gate/up alone still ran 5% faster
+  // on small tiles but the block, where it shares the CUs with the shared expert, 5% slower; at 3.75 the large
+  // tiles ran 5% faster alone.  With 16 or 64 experts the large tiles stay ahead over that range.
+  if (large && EPI == EPI_SWIGLU && !env_force() && p.E >= 128 && tl * 4 < cu_count() * 13) large = false;
+  if (large) return launch<CfgL8, MGROUP, false, true, EPI, false, F16>(p, tl, s);
   return launch<CfgS8, MGROUP, false, true, EPI, false, F16>(p, mgroup_tiles<CfgS8, EPI>(p.M, p.E, ncols), s);
 }
 template <int EPI>
